@@ -1,0 +1,155 @@
+/*
+ * mi_adamw.h -- C ABI of the MI355X (gfx950) fused clip + AdamW optimizer step.
+ *
+ * One shared library, libmi_adamw.so, exports these symbols.  They take plain
+ * device pointers, sizes, host structs and a hipStream_t (passed as void*), and
+ * never throw: every entry point returns MI_ADAMW_OK (0), a negative
+ * MI_ADAMW_E_* code for a rejected argument, or a positive hipError_t value.
+ * All work is enqueued on the given stream; nothing synchronises the host.
+ *
+ * What the entry points replace.  mini-megatron steps `torch.optim.AdamW(...,
+ * fused=False)` once per iteration (main.py:177 builds it, main.py:209 and
+ * parallel/pipeline_parallel.py:260 call step()).  That runs torch's
+ * `_single_tensor_adam` (torch/optim/adam.py:396-547): 8 elementwise kernels
+ * per parameter tensor.  The gradient clip that config.py:16 names
+ * (MAX_GRAD_NORM) is torch's clip_grad_norm_ (torch/nn/utils/clip_grad.py:186).
+ * The Python class mi_adamw.FusedAdamW (a torch.optim.Optimizer) is the only
+ * caller; it is the drop-in for the reference's optimizer object.
+ *
+ * Layout.  A launch covers many tensors through two device-resident tables:
+ *   - a tensor table (mi_adamw_tensor[]): the pointers and size of each tensor;
+ *   - a chunk table (mi_adamw_chunk[]): (tensor, chunk index) pairs, one per
+ *     `chunk_elems`-element slice of a tensor.  Chunk i of tensor t covers
+ *     elements [i*chunk_elems, min((i+1)*chunk_elems, numel)).
+ * The "flat" entry points take one contiguous range instead of the tables
+ * (the flat-buffer layout: every tensor packed at a 128-byte-aligned offset).
+ *
+ * Numerics.  Each element follows the fp32 op chain of adam.py:419-547, with
+ * one fp32 rounding per ATen op, in the contraction pattern torch-ROCm's kernels
+ * use (lerp, addcmul and addcdiv as fused multiply-adds; division by the host
+ * scalar bc2_sqrt as a multiply by its fp32 reciprocal).  The caller computes
+ * the per-step scalars on the host in float64 (adam.py:529-536) and passes them
+ * rounded to fp32 in mi_adamw_hyper.
+ */
+#ifndef MI_ADAMW_H
+#define MI_ADAMW_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MI_ADAMW_ABI_VERSION 1
+#define MI_ADAMW_MAX_HYPER 16      /* hyperparameter sets per launch */
+#define MI_ADAMW_MAX_NORM_BLOCKS 4096 /* partial sums per grad-norm launch */
+
+/* Return codes (positive values are hipError_t). */
+#define MI_ADAMW_OK 0
+#define MI_ADAMW_E_INVALID (-1)    /* a size, count or pointer argument is out of range */
+#define MI_ADAMW_E_ALIGN (-2)      /* a tensor flagged aligned has a misaligned pointer */
+
+/* Storage dtype of exp_avg / exp_avg_sq. */
+#define MI_ADAMW_STATE_F32 0
+#define MI_ADAMW_STATE_BF16 1
+
+/* mi_adamw_step* flags. */
+#define MI_ADAMW_F_CLIP (1 << 0)       /* multiply every gradient by *grad_scale first */
+#define MI_ADAMW_F_BF16_COPY (1 << 1)  /* write the updated parameter to param_copy as bf16 */
+#define MI_ADAMW_F_WRITE_GRAD (1 << 2) /* store the scaled gradient back into grad */
+
+/* mi_adamw_tensor.flags */
+#define MI_ADAMW_T_VEC (1 << 0) /* fp32 pointers 16-byte aligned and bf16 pointers 8-byte
+                                   aligned: the dwordx4 path may be used */
+
+typedef struct mi_adamw_tensor {
+    float *param;          /* fp32 master parameter, updated in place                */
+    float *grad;           /* fp32 gradient (written only with MI_ADAMW_F_WRITE_GRAD) */
+    void *exp_avg;         /* first moment, fp32 or bf16 (state dtype of the launch)  */
+    void *exp_avg_sq;      /* second moment, fp32 or bf16                             */
+    uint16_t *param_copy;  /* bf16 model copy, or NULL without MI_ADAMW_F_BF16_COPY   */
+    int64_t numel;         /* elements (a complex64 tensor counts 2 per value)        */
+    int32_t hyper;         /* index of this tensor's mi_adamw_hyper in the launch     */
+    int32_t flags;         /* MI_ADAMW_T_*                                            */
+} mi_adamw_tensor;
+
+typedef struct mi_adamw_chunk {
+    int32_t tensor;        /* row of the tensor table            */
+    int32_t index;         /* chunk number within that tensor    */
+} mi_adamw_chunk;
+
+/* Per-step scalars of one parameter group at one step count, as the ATen
+ * kernels of adam.py see them (each a float64 host value cast to fp32). */
+typedef struct mi_adamw_hyper {
+    float wd_factor;       /* 1 - lr*weight_decay; 1 when weight_decay == 0  (adam.py:419) */
+    float lerp_w;          /* 1 - beta1                                      (adam.py:457) */
+    float beta2;           /* beta2                                          (adam.py:476) */
+    float one_minus_beta2; /* 1 - beta2                                      (adam.py:476) */
+    float inv_bc2_sqrt;    /* 1.0f / (float)((1 - beta2**step) ** 0.5), an fp32 division
+                              (adam.py:536,545: tensor / host scalar)                        */
+    float eps;             /* eps                                            (adam.py:545) */
+    float neg_step_size;   /* -(lr / (1 - beta1**step))                      (adam.py:534,547) */
+    float grad_sign;       /* -1 with maximize=True, else 1                  (adam.py:397) */
+} mi_adamw_hyper;
+
+/* Library identification: "mi_adamw <abi> gfx950 ...". */
+const char *mi_adamw_version(void);
+
+/* Text for a return code (MI_ADAMW_E_* or hipError_t). */
+const char *mi_adamw_strerror(int code);
+
+/* Host-side helper: fill `out` (capacity `cap` entries, host memory) with the
+ * chunk table of `n_tensors` tensors of the given sizes.  Returns the number of
+ * chunks written, or MI_ADAMW_E_INVALID if it would exceed `cap` or if
+ * chunk_elems is not a positive multiple of 1024.  With out == NULL only counts. */
+int64_t mi_adamw_build_chunks(const int64_t *numels, int32_t n_tensors, int64_t chunk_elems,
+                              mi_adamw_chunk *out, int64_t cap);
+
+/* Global gradient L2 norm and clip coefficient (one launch).
+ * Replaces clip_grad.py:50-117 (_get_total_norm, norm_type 2) and :165-169.
+ *   d_norm  <- fp32(sqrt(sum of g*g over every grad)), summed in float64;
+ *   d_coef  <- min(max_norm * (1 / (norm + 1e-6)), 1) in fp32 (NaN propagates).
+ * `d_partials` holds MI_ADAMW_MAX_NORM_BLOCKS doubles; `d_counter` one uint32
+ * that must be zero before the first call (each call leaves it zero).  The
+ * partial-sum assignment is fixed, so the result is bitwise reproducible. */
+int mi_adamw_grad_norm(const mi_adamw_tensor *d_tensors, const mi_adamw_chunk *d_chunks,
+                       int64_t n_chunks, int64_t chunk_elems, float max_norm,
+                       double *d_partials, uint32_t *d_counter, float *d_norm, float *d_coef,
+                       void *stream);
+
+/* Same over one contiguous fp32 gradient range of n elements. */
+int mi_adamw_grad_norm_flat(const float *d_grad, int64_t n, int64_t chunk_elems, float max_norm,
+                            double *d_partials, uint32_t *d_counter, float *d_norm,
+                            float *d_coef, void *stream);
+
+/* Multiply every gradient of the tables by *d_coef in place.
+ * Replaces clip_grad.py:170-183 (_clip_grads_with_norm_'s foreach mul). */
+int mi_adamw_scale_grads(const mi_adamw_tensor *d_tensors, const mi_adamw_chunk *d_chunks,
+                         int64_t n_chunks, int64_t chunk_elems, const float *d_coef,
+                         void *stream);
+
+/* The fused AdamW update over every chunk of the tables (one launch).
+ * Replaces the per-tensor loop body of adam.py:396-547.
+ * hypers: host array of n_hyper (<= MI_ADAMW_MAX_HYPER) sets, indexed by
+ * mi_adamw_tensor.hyper.  d_grad_scale: device fp32 scalar, read with
+ * MI_ADAMW_F_CLIP (normally d_coef of mi_adamw_grad_norm on the same stream).
+ * state_dtype: MI_ADAMW_STATE_*.  flags: MI_ADAMW_F_*.
+ * max_blocks: upper bound on workgroups (0 = one per chunk). */
+int mi_adamw_step(const mi_adamw_tensor *d_tensors, const mi_adamw_chunk *d_chunks,
+                  int64_t n_chunks, int64_t chunk_elems, const mi_adamw_hyper *hypers,
+                  int32_t n_hyper, const float *d_grad_scale, int32_t state_dtype,
+                  int32_t flags, int32_t max_blocks, void *stream);
+
+/* The fused AdamW update over one contiguous range of n elements (the
+ * flat-buffer layout; replaces the owned-parameter step of
+ * parallel/distributed_optimizer.py:36-37).  `t` is a host struct whose
+ * pointers are device pointers; t->hyper is ignored (hyper is the one set). */
+int mi_adamw_step_flat(const mi_adamw_tensor *t, const mi_adamw_hyper *hyper,
+                       const float *d_grad_scale, int64_t chunk_elems, int32_t state_dtype,
+                       int32_t flags, int32_t max_blocks, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MI_ADAMW_H */

@@ -1,0 +1,147 @@
+"""ctypes binding of libmi_adamw.so (the C ABI declared in include/mi_adamw.h).
+
+The library is loaded after torch has initialised HIP, so that its
+libamdhip64 dependency resolves to the HIP runtime torch already mapped and
+the device pointers and stream handles torch hands out are valid in it.
+There is no CPU fallback: if the library is missing or was built for another
+ABI, loading raises.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+import torch
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libmi_adamw.so")
+
+ABI_VERSION = 1
+MAX_HYPER = 16
+MAX_NORM_BLOCKS = 4096
+
+OK = 0
+E_INVALID = -1
+E_ALIGN = -2
+
+STATE_F32 = 0
+STATE_BF16 = 1
+
+F_CLIP = 1 << 0
+F_BF16_COPY = 1 << 1
+F_WRITE_GRAD = 1 << 2
+
+T_VEC = 1 << 0
+
+# Every symbol include/mi_adamw.h declares.
+EXPORTS = (
+    "mi_adamw_version",
+    "mi_adamw_strerror",
+    "mi_adamw_build_chunks",
+    "mi_adamw_grad_norm",
+    "mi_adamw_grad_norm_flat",
+    "mi_adamw_scale_grads",
+    "mi_adamw_step",
+    "mi_adamw_step_flat",
+)
+
+
+class TensorRow(ctypes.Structure):
+    """mi_adamw_tensor: one row of the device-resident tensor table."""
+
+    _fields_ = [
+        ("param", ctypes.c_void_p),
+        ("grad", ctypes.c_void_p),
+        ("exp_avg", ctypes.c_void_p),
+        ("exp_avg_sq", ctypes.c_void_p),
+        ("param_copy", ctypes.c_void_p),
+        ("numel", ctypes.c_int64),
+        ("hyper", ctypes.c_int32),
+        ("flags", ctypes.c_int32),
+    ]
+
+
+class ChunkRow(ctypes.Structure):
+    """mi_adamw_chunk: (tensor row, chunk number within the tensor)."""
+
+    _fields_ = [("tensor", ctypes.c_int32), ("index", ctypes.c_int32)]
+
+
+class Hyper(ctypes.Structure):
+    """mi_adamw_hyper: the fp32 scalars of one (param group, step count)."""
+
+    _fields_ = [
+        ("wd_factor", ctypes.c_float),
+        ("lerp_w", ctypes.c_float),
+        ("beta2", ctypes.c_float),
+        ("one_minus_beta2", ctypes.c_float),
+        ("inv_bc2_sqrt", ctypes.c_float),
+        ("eps", ctypes.c_float),
+        ("neg_step_size", ctypes.c_float),
+        ("grad_sign", ctypes.c_float),
+    ]
+
+
+assert ctypes.sizeof(TensorRow) == 56
+assert ctypes.sizeof(ChunkRow) == 8
+assert ctypes.sizeof(Hyper) == 32
+
+_vp = ctypes.c_void_p
+_i64 = ctypes.c_int64
+_i32 = ctypes.c_int32
+_f32 = ctypes.c_float
+
+_SIGNATURES = {
+    "mi_adamw_version": ([], ctypes.c_char_p),
+    "mi_adamw_strerror": ([ctypes.c_int], ctypes.c_char_p),
+    "mi_adamw_build_chunks": ([_vp, _i32, _i64, _vp, _i64], _i64),
+    "mi_adamw_grad_norm": ([_vp, _vp, _i64, _i64, _f32, _vp, _vp, _vp, _vp, _vp], ctypes.c_int),
+    "mi_adamw_grad_norm_flat": ([_vp, _i64, _i64, _f32, _vp, _vp, _vp, _vp, _vp], ctypes.c_int),
+    "mi_adamw_scale_grads": ([_vp, _vp, _i64, _i64, _vp, _vp], ctypes.c_int),
+    "mi_adamw_step": ([_vp, _vp, _i64, _i64, _vp, _i32, _vp, _i32, _i32, _i32, _vp], ctypes.c_int),
+    "mi_adamw_step_flat": ([_vp, _vp, _vp, _i64, _i32, _i32, _i32, _vp], ctypes.c_int),
+}
+
+_lib = None
+
+
+class MiAdamwError(RuntimeError):
+    """A non-zero return code from libmi_adamw."""
+
+
+def load(path: str = LIB_PATH) -> ctypes.CDLL:
+    """Load (once) and bind libmi_adamw.so.  Raises if it is missing."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(path):
+        raise MiAdamwError(
+            f"libmi_adamw.so not found at {path}; build it with "
+            "`python -m mi_adamw.build` (hipcc, gfx950) before using mi_adamw")
+    # Bring up torch's HIP runtime first when a GPU is present, so the
+    # library's libamdhip64 dependency binds to the same runtime instance.
+    if torch.cuda.is_available():
+        torch.cuda.init()
+    lib = ctypes.CDLL(path)
+    for name, (args, res) in _SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.argtypes = args
+        fn.restype = res
+    version = lib.mi_adamw_version().decode()
+    if not version.startswith(f"mi_adamw {ABI_VERSION} "):
+        raise MiAdamwError(f"libmi_adamw ABI mismatch: library reports {version!r}")
+    _lib = lib
+    return lib
+
+
+def strerror(code: int) -> str:
+    return load().mi_adamw_strerror(code).decode()
+
+
+def check(code: int, what: str) -> None:
+    if code != OK:
+        raise MiAdamwError(f"{what} failed: {strerror(code)} (code {code})")
+
+
+def version() -> str:
+    return load().mi_adamw_version().decode()

@@ -1,0 +1,603 @@
+// mi_adamw.hip -- fused clip + AdamW optimizer step for MI355X (gfx950).
+//
+// Kernels (all HBM-streaming, no MFMA: the step is ~15 fp32 ops per 22-34 bytes):
+//   mi_adamw_sumsq_kernel  pass 1 of the clip: float64 sum of g*g over every
+//                          gradient, reduced wave (DPP/shuffle) -> LDS -> one
+//                          partial per workgroup; the last workgroup to finish
+//                          reduces the partials in a fixed order and writes the
+//                          norm and the clip coefficient (no host sync).
+//   mi_adamw_update_kernel pass 2: p, g, m, v streamed with dwordx4 loads and
+//                          stores, the AdamW op chain in fp32 registers, optional
+//                          bf16 moments, bf16 model copy and gradient write-back.
+//   mi_adamw_scale_kernel  g *= coef in place (clip_grad_norm_'s write-back).
+//
+// Every launch walks a chunk table (one entry per `chunk_elems` slice of a
+// tensor) so that all parameter tensors go through one launch, or one
+// contiguous range in the flat-buffer layout.
+//
+// The element math follows torch's per-op chain (torch/optim/adam.py:419-547)
+// with one fp32 rounding per ATen op.  The file is compiled with
+// -ffp-contract=off; each fused multiply-add below is explicit and sits where
+// torch-ROCm's own kernels fuse (lerp, addcmul, addcdiv).
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <stddef.h>
+#include <string.h>
+
+#include "mi_adamw.h"
+
+namespace {
+
+constexpr int kThreads = 256;            // 4 wave64 per workgroup
+constexpr int kVec = 4;                  // fp32 elements per lane per access
+constexpr int kTile = kThreads * kVec;   // elements one workgroup covers per access
+constexpr int kUnroll = 2;               // tiles in flight per lane
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+struct HyperPack {
+    mi_adamw_hyper h[MI_ADAMW_MAX_HYPER];
+};
+
+static_assert(sizeof(mi_adamw_tensor) == 56, "mi_adamw_tensor is read as 7 words");
+static_assert(offsetof(mi_adamw_tensor, hyper) == 48 && offsetof(mi_adamw_tensor, flags) == 52,
+              "hyper and flags share the last word");
+static_assert(sizeof(mi_adamw_chunk) == 8, "mi_adamw_chunk is two int32");
+
+// ---------------------------------------------------------------------------
+// Element math
+
+// fp32 -> bf16, round to nearest even; every NaN becomes 0x7FC0 (the value
+// torch's Tensor.to(torch.bfloat16) produces).
+__device__ __forceinline__ uint32_t bf16_bits(float x) {
+    uint32_t u = __float_as_uint(x);
+    if ((u & 0x7f800000u) == 0x7f800000u && (u & 0x007fffffu)) return 0x7fc0u;
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return u >> 16;
+}
+__device__ __forceinline__ float bf16_to_f32(uint32_t h16) { return __uint_as_float(h16 << 16); }
+
+// Lerp.h:21-35, fp32 opmath, fused the way torch-ROCm compiles it.
+__device__ __forceinline__ float lerp_fused(float self, float end, float w) {
+    float diff = end - self;
+    if (__builtin_fabsf(w) < 0.5f) return __builtin_fmaf(w, diff, self);
+    return __builtin_fmaf(-diff, 1.0f - w, end);
+}
+
+// One element of adam.py:419-547.  g already carries the clip scale and sign.
+__device__ __forceinline__ void adamw_elem(float& p, float g, float& m, float& v,
+                                           const mi_adamw_hyper& h) {
+    p = p * h.wd_factor;                                   // adam.py:419 mul_
+    m = lerp_fused(m, g, h.lerp_w);                        // adam.py:457 lerp_
+    v = v * h.beta2;                                       // adam.py:476 mul_
+    v = __builtin_fmaf(h.one_minus_beta2, g * g, v);       // adam.py:476 addcmul_
+    float d = __builtin_sqrtf(v);                          // adam.py:545 sqrt
+    d = d * h.inv_bc2_sqrt;                                //   / bc2_sqrt (reciprocal mul)
+    d = d + h.eps;                                         //   add_(eps)
+    p = __builtin_fmaf(h.neg_step_size, m / d, p);         // adam.py:547 addcdiv_
+}
+
+// ---------------------------------------------------------------------------
+// Streaming loads and stores.  Every value is touched exactly once per step,
+// so loads and stores carry the nontemporal hint.  Tensor pointers come out of
+// the tensor table, so the compiler cannot tell they are global memory; the
+// casts to address space 1 make it emit global_load/global_store (vmcnt only)
+// instead of flat accesses.
+
+#define GLOBAL __attribute__((address_space(1)))
+
+__device__ __forceinline__ f32x4 ld4(const float* p) {
+    return __builtin_nontemporal_load((const GLOBAL f32x4*)(p));
+}
+__device__ __forceinline__ void st4(float* p, f32x4 v) {
+    __builtin_nontemporal_store(v, (GLOBAL f32x4*)(p));
+}
+__device__ __forceinline__ float ld1(const float* p) { return *(const GLOBAL float*)(p); }
+__device__ __forceinline__ void st1(float* p, float v) { *(GLOBAL float*)(p) = v; }
+__device__ __forceinline__ uint32_t ld1_u16(const uint16_t* p) {
+    return *(const GLOBAL uint16_t*)(p);
+}
+__device__ __forceinline__ void st1_u16(uint16_t* p, uint32_t v) {
+    *(GLOBAL uint16_t*)(p) = static_cast<uint16_t>(v);
+}
+__device__ __forceinline__ f32x4 ld4_bf16(const uint16_t* p) {
+    u32x2 w = __builtin_nontemporal_load((const GLOBAL u32x2*)(p));
+    f32x4 r;
+    r.x = __uint_as_float(w.x << 16);
+    r.y = __uint_as_float(w.x & 0xffff0000u);
+    r.z = __uint_as_float(w.y << 16);
+    r.w = __uint_as_float(w.y & 0xffff0000u);
+    return r;
+}
+__device__ __forceinline__ void st4_bf16(uint16_t* p, f32x4 v) {
+    u32x2 w;
+    w.x = bf16_bits(v.x) | (bf16_bits(v.y) << 16);
+    w.y = bf16_bits(v.z) | (bf16_bits(v.w) << 16);
+    __builtin_nontemporal_store(w, (GLOBAL u32x2*)(p));
+}
+
+// adamw_elem on the four lanes of a dwordx4 group.
+__device__ __forceinline__ void adamw_vec(f32x4& p, f32x4 g, f32x4& m, f32x4& v,
+                                          const mi_adamw_hyper& h) {
+    float p0 = p.x, p1 = p.y, p2 = p.z, p3 = p.w;
+    float m0 = m.x, m1 = m.y, m2 = m.z, m3 = m.w;
+    float v0 = v.x, v1 = v.y, v2 = v.z, v3 = v.w;
+    adamw_elem(p0, g.x, m0, v0, h);
+    adamw_elem(p1, g.y, m1, v1, h);
+    adamw_elem(p2, g.z, m2, v2, h);
+    adamw_elem(p3, g.w, m3, v3, h);
+    p = f32x4{p0, p1, p2, p3};
+    m = f32x4{m0, m1, m2, m3};
+    v = f32x4{v0, v1, v2, v3};
+}
+
+template <typename S> struct StateIO;
+template <> struct StateIO<float> {
+    static __device__ __forceinline__ f32x4 ld(const void* b, int64_t i) {
+        return ld4(static_cast<const float*>(b) + i);
+    }
+    static __device__ __forceinline__ void st(void* b, int64_t i, f32x4 v) {
+        st4(static_cast<float*>(b) + i, v);
+    }
+    static __device__ __forceinline__ float ld1(const void* b, int64_t i) {
+        return ::ld1(static_cast<const float*>(b) + i);
+    }
+    static __device__ __forceinline__ void st1(void* b, int64_t i, float v) {
+        ::st1(static_cast<float*>(b) + i, v);
+    }
+};
+template <> struct StateIO<uint16_t> {
+    static __device__ __forceinline__ f32x4 ld(const void* b, int64_t i) {
+        return ld4_bf16(static_cast<const uint16_t*>(b) + i);
+    }
+    static __device__ __forceinline__ void st(void* b, int64_t i, f32x4 v) {
+        st4_bf16(static_cast<uint16_t*>(b) + i, v);
+    }
+    static __device__ __forceinline__ float ld1(const void* b, int64_t i) {
+        return bf16_to_f32(ld1_u16(static_cast<const uint16_t*>(b) + i));
+    }
+    static __device__ __forceinline__ void st1(void* b, int64_t i, float v) {
+        st1_u16(static_cast<uint16_t*>(b) + i, bf16_bits(v));
+    }
+};
+
+// ---------------------------------------------------------------------------
+// Work sources: where chunk c of a launch lives.
+
+#define CONSTANT __attribute__((address_space(4)))
+
+// The tables do not change while a launch runs, so they are read through the
+// constant address space: the compiler then fetches a chunk entry and its
+// tensor row with scalar loads (s_load), keeps the tensor's base pointers in
+// SGPRs and addresses the streams as SGPR base + VGPR offset.
+struct TableSource {
+    const mi_adamw_tensor* tensors;
+    const mi_adamw_chunk* chunks;
+    __device__ __forceinline__ void get(int64_t c, int64_t chunk_elems, mi_adamw_tensor& t,
+                                        int64_t& begin, int64_t& end) const {
+        const CONSTANT int32_t* ck = (const CONSTANT int32_t*)(chunks + c);
+        const int32_t row = ck[0];
+        const int32_t index = ck[1];
+        // mi_adamw_tensor is 7 eight-byte words: 5 pointers, numel, (hyper, flags).
+        const CONSTANT uint64_t* w = (const CONSTANT uint64_t*)(tensors + row);
+        t.param = reinterpret_cast<float*>(w[0]);
+        t.grad = reinterpret_cast<float*>(w[1]);
+        t.exp_avg = reinterpret_cast<void*>(w[2]);
+        t.exp_avg_sq = reinterpret_cast<void*>(w[3]);
+        t.param_copy = reinterpret_cast<uint16_t*>(w[4]);
+        t.numel = static_cast<int64_t>(w[5]);
+        t.hyper = static_cast<int32_t>(w[6] & 0xffffffffu);
+        t.flags = static_cast<int32_t>(w[6] >> 32);
+        begin = static_cast<int64_t>(index) * chunk_elems;
+        end = begin + chunk_elems < t.numel ? begin + chunk_elems : t.numel;
+    }
+};
+
+struct FlatSource {
+    mi_adamw_tensor t;
+    __device__ __forceinline__ void get(int64_t c, int64_t chunk_elems, mi_adamw_tensor& out,
+                                        int64_t& begin, int64_t& end) const {
+        out = t;
+        begin = c * chunk_elems;
+        end = begin + chunk_elems < t.numel ? begin + chunk_elems : t.numel;
+    }
+};
+
+// ---------------------------------------------------------------------------
+// Reductions
+
+__device__ __forceinline__ double wave_sum(double x) {
+    // wave64 butterfly; __shfl_xor moves the two 32-bit halves.
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) x += __shfl_xor(x, off, 64);
+    return x;
+}
+
+// Sum over the workgroup; the result is valid in every lane of wave 0.
+__device__ __forceinline__ double block_sum(double x) {
+    __shared__ double lds[kThreads / 64];
+    x = wave_sum(x);
+    const int wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63;
+    if (lane == 0) lds[wave] = x;
+    __syncthreads();
+    double r = 0.0;
+    if (wave == 0) {
+        r = lane < kThreads / 64 ? lds[lane] : 0.0;
+        r = wave_sum(r);
+    }
+    __syncthreads();
+    return r;
+}
+
+// ---------------------------------------------------------------------------
+// Pass 1: float64 sum of squares and the clip coefficient.
+
+template <class Src>
+__global__ __launch_bounds__(kThreads) void mi_adamw_sumsq_kernel(
+    Src src, int64_t n_chunks, int64_t chunk_elems, float max_norm, double* __restrict__ partials,
+    uint32_t* __restrict__ counter, float* __restrict__ norm_out, float* __restrict__ coef_out) {
+    double acc0 = 0.0, acc1 = 0.0;
+    for (int64_t c = blockIdx.x; c < n_chunks; c += gridDim.x) {
+        mi_adamw_tensor t;
+        int64_t begin, end;
+        src.get(c, chunk_elems, t, begin, end);
+        const float* __restrict__ g = t.grad;
+        if (t.flags & MI_ADAMW_T_VEC) {
+            const int64_t vend = begin + ((end - begin) & ~static_cast<int64_t>(kVec - 1));
+            int64_t i = begin + threadIdx.x * kVec;
+            for (; i + kTile < vend; i += 2 * kTile) {
+                f32x4 a = ld4(g + i), b = ld4(g + i + kTile);
+                acc0 += (double)a.x * a.x + (double)a.y * a.y;
+                acc1 += (double)a.z * a.z + (double)a.w * a.w;
+                acc0 += (double)b.x * b.x + (double)b.y * b.y;
+                acc1 += (double)b.z * b.z + (double)b.w * b.w;
+            }
+            for (; i < vend; i += kTile) {
+                f32x4 a = ld4(g + i);
+                acc0 += (double)a.x * a.x + (double)a.y * a.y;
+                acc1 += (double)a.z * a.z + (double)a.w * a.w;
+            }
+            for (int64_t j = vend + threadIdx.x; j < end; j += kThreads) {
+                double x = ld1(g + j);
+                acc0 += x * x;
+            }
+        } else {
+            for (int64_t j = begin + threadIdx.x; j < end; j += kThreads) {
+                double x = ld1(g + j);
+                acc0 += x * x;
+            }
+        }
+    }
+    double total = block_sum(acc0 + acc1);
+
+    __shared__ bool is_last;
+    if (threadIdx.x == 0) {
+        __hip_atomic_store(&partials[blockIdx.x], total, __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+        __threadfence();  // release this partial before the count
+        uint32_t prev = atomicAdd(counter, 1u);
+        is_last = (prev == gridDim.x - 1);
+    }
+    __syncthreads();
+    if (!is_last) return;
+
+    // Last workgroup: every partial is visible (acquire), reduce them in a
+    // fixed order so the result does not depend on which workgroup ran last.
+    __threadfence();
+    double s = 0.0;
+    for (uint32_t i = threadIdx.x; i < gridDim.x; i += kThreads)
+        s += __hip_atomic_load(&partials[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    s = block_sum(s);
+    if (threadIdx.x == 0) {
+        const float norm = static_cast<float>(__builtin_sqrt(s));
+        // clip_grad.py:165-169: t = norm + 1e-6; coef = max_norm * (1/t); clamp(max=1)
+        const float t = norm + 1e-6f;
+        const float r = 1.0f / t;
+        const float coef = r * max_norm;
+        *norm_out = norm;
+        *coef_out = coef > 1.0f ? 1.0f : coef;  // NaN stays NaN, as torch.clamp
+        __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Pass 2: the AdamW update.
+
+template <class Src, typename StateT, bool kClip, bool kCopy, bool kWriteGrad>
+__global__ __launch_bounds__(kThreads) void mi_adamw_update_kernel(
+    Src src, int64_t n_chunks, int64_t chunk_elems, HyperPack hp,
+    const float* __restrict__ grad_scale) {
+    using IO = StateIO<StateT>;
+    const float scale = kClip ? *grad_scale : 1.0f;
+    for (int64_t c = blockIdx.x; c < n_chunks; c += gridDim.x) {
+        mi_adamw_tensor t;
+        int64_t begin, end;
+        src.get(c, chunk_elems, t, begin, end);
+        const mi_adamw_hyper h = hp.h[t.hyper];
+        const float gmul = h.grad_sign;
+        float* __restrict__ P = t.param;
+        float* __restrict__ G = t.grad;
+        void* __restrict__ M = t.exp_avg;
+        void* __restrict__ V = t.exp_avg_sq;
+        uint16_t* __restrict__ C = t.param_copy;
+
+        int64_t vend = begin;
+        if (t.flags & MI_ADAMW_T_VEC) {
+            vend = begin + ((end - begin) & ~static_cast<int64_t>(kVec - 1));
+            int64_t i = begin + threadIdx.x * kVec;
+            for (; i + (kUnroll - 1) * kTile < vend; i += kUnroll * kTile) {
+                f32x4 p[kUnroll], g[kUnroll], m[kUnroll], v[kUnroll];
+#pragma unroll
+                for (int u = 0; u < kUnroll; ++u) {
+                    const int64_t k = i + u * kTile;
+                    g[u] = ld4(G + k);
+                    p[u] = ld4(P + k);
+                    m[u] = IO::ld(M, k);
+                    v[u] = IO::ld(V, k);
+                }
+#pragma unroll
+                for (int u = 0; u < kUnroll; ++u) {
+                    const int64_t k = i + u * kTile;
+                    f32x4 gs = g[u];
+                    if (kClip) gs = f32x4{gs.x * scale, gs.y * scale, gs.z * scale, gs.w * scale};
+                    if (kWriteGrad) st4(G + k, gs);
+                    gs = f32x4{gs.x * gmul, gs.y * gmul, gs.z * gmul, gs.w * gmul};
+                    adamw_vec(p[u], gs, m[u], v[u], h);
+                    st4(P + k, p[u]);
+                    IO::st(M, k, m[u]);
+                    IO::st(V, k, v[u]);
+                    if (kCopy) st4_bf16(C + k, p[u]);
+                }
+            }
+            for (; i < vend; i += kTile) {
+                f32x4 g1 = ld4(G + i), p1 = ld4(P + i);
+                f32x4 m1 = IO::ld(M, i), v1 = IO::ld(V, i);
+                if (kClip) g1 = f32x4{g1.x * scale, g1.y * scale, g1.z * scale, g1.w * scale};
+                if (kWriteGrad) st4(G + i, g1);
+                g1 = f32x4{g1.x * gmul, g1.y * gmul, g1.z * gmul, g1.w * gmul};
+                adamw_vec(p1, g1, m1, v1, h);
+                st4(P + i, p1);
+                IO::st(M, i, m1);
+                IO::st(V, i, v1);
+                if (kCopy) st4_bf16(C + i, p1);
+            }
+        }
+        // Scalar path: the ragged tail of a vector tensor, or a whole tensor
+        // whose pointers are not aligned for dwordx4.
+        for (int64_t j = vend + threadIdx.x; j < end; j += kThreads) {
+            float g1 = ld1(G + j);
+            if (kClip) g1 = g1 * scale;
+            if (kWriteGrad) st1(G + j, g1);
+            g1 = g1 * gmul;
+            float p1 = ld1(P + j), m1 = IO::ld1(M, j), v1 = IO::ld1(V, j);
+            adamw_elem(p1, g1, m1, v1, h);
+            st1(P + j, p1);
+            IO::st1(M, j, m1);
+            IO::st1(V, j, v1);
+            if (kCopy) st1_u16(C + j, bf16_bits(p1));
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// g *= coef (clip write-back on its own).
+
+__global__ __launch_bounds__(kThreads) void mi_adamw_scale_kernel(
+    TableSource src, int64_t n_chunks, int64_t chunk_elems, const float* __restrict__ coef) {
+    const float s = *coef;
+    for (int64_t c = blockIdx.x; c < n_chunks; c += gridDim.x) {
+        mi_adamw_tensor t;
+        int64_t begin, end;
+        src.get(c, chunk_elems, t, begin, end);
+        float* __restrict__ G = t.grad;
+        int64_t vend = begin;
+        if (t.flags & MI_ADAMW_T_VEC) {
+            vend = begin + ((end - begin) & ~static_cast<int64_t>(kVec - 1));
+            for (int64_t i = begin + threadIdx.x * kVec; i < vend; i += kTile) {
+                f32x4 g = ld4(G + i);
+                st4(G + i, f32x4{g.x * s, g.y * s, g.z * s, g.w * s});
+            }
+        }
+        for (int64_t j = vend + threadIdx.x; j < end; j += kThreads) st1(G + j, ld1(G + j) * s);
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Host side
+
+constexpr int kNormBlocks = 2048;   // partial sums of the norm pass (<= MAX_NORM_BLOCKS)
+
+bool chunk_elems_ok(int64_t chunk_elems) {
+    return chunk_elems > 0 && (chunk_elems % kTile) == 0 && chunk_elems <= (int64_t(1) << 30);
+}
+
+int launch_status() {
+    hipError_t e = hipGetLastError();
+    return e == hipSuccess ? MI_ADAMW_OK : static_cast<int>(e);
+}
+
+unsigned grid_for(int64_t n_chunks, int32_t max_blocks) {
+    int64_t g = n_chunks;
+    if (max_blocks > 0 && g > max_blocks) g = max_blocks;
+    if (g > 0x7fffffff / kThreads) g = 0x7fffffff / kThreads;
+    return static_cast<unsigned>(g);
+}
+
+bool aligned(const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0; }
+
+template <class Src>
+int launch_norm(const Src& src, int64_t n_chunks, int64_t chunk_elems, float max_norm,
+                double* partials, uint32_t* counter, float* norm, float* coef, hipStream_t s) {
+    if (n_chunks <= 0 || !chunk_elems_ok(chunk_elems) || !partials || !counter || !norm || !coef)
+        return MI_ADAMW_E_INVALID;
+    unsigned grid = grid_for(n_chunks, kNormBlocks);
+    hipLaunchKernelGGL(mi_adamw_sumsq_kernel<Src>, dim3(grid), dim3(kThreads), 0, s, src,
+                       n_chunks, chunk_elems, max_norm, partials, counter, norm, coef);
+    return launch_status();
+}
+
+template <class Src, typename StateT, bool kClip>
+int launch_update_cw(const Src& src, int64_t n_chunks, int64_t chunk_elems, const HyperPack& hp,
+                     const float* scale, int32_t flags, unsigned grid, hipStream_t s) {
+    const bool copy = flags & MI_ADAMW_F_BF16_COPY;
+    const bool wg = flags & MI_ADAMW_F_WRITE_GRAD;
+    if (copy && wg)
+        hipLaunchKernelGGL((mi_adamw_update_kernel<Src, StateT, kClip, true, true>), dim3(grid),
+                           dim3(kThreads), 0, s, src, n_chunks, chunk_elems, hp, scale);
+    else if (copy)
+        hipLaunchKernelGGL((mi_adamw_update_kernel<Src, StateT, kClip, true, false>), dim3(grid),
+                           dim3(kThreads), 0, s, src, n_chunks, chunk_elems, hp, scale);
+    else if (wg)
+        hipLaunchKernelGGL((mi_adamw_update_kernel<Src, StateT, kClip, false, true>), dim3(grid),
+                           dim3(kThreads), 0, s, src, n_chunks, chunk_elems, hp, scale);
+    else
+        hipLaunchKernelGGL((mi_adamw_update_kernel<Src, StateT, kClip, false, false>), dim3(grid),
+                           dim3(kThreads), 0, s, src, n_chunks, chunk_elems, hp, scale);
+    return launch_status();
+}
+
+template <class Src>
+int launch_update(const Src& src, int64_t n_chunks, int64_t chunk_elems, const HyperPack& hp,
+                  const float* scale, int32_t state_dtype, int32_t flags, int32_t max_blocks,
+                  hipStream_t s) {
+    if (n_chunks <= 0 || !chunk_elems_ok(chunk_elems)) return MI_ADAMW_E_INVALID;
+    if (state_dtype != MI_ADAMW_STATE_F32 && state_dtype != MI_ADAMW_STATE_BF16)
+        return MI_ADAMW_E_INVALID;
+    if (flags & ~(MI_ADAMW_F_CLIP | MI_ADAMW_F_BF16_COPY | MI_ADAMW_F_WRITE_GRAD))
+        return MI_ADAMW_E_INVALID;
+    const bool clip = flags & MI_ADAMW_F_CLIP;
+    if (clip && !scale) return MI_ADAMW_E_INVALID;
+    const unsigned grid = grid_for(n_chunks, max_blocks);
+    if (state_dtype == MI_ADAMW_STATE_F32)
+        return clip ? launch_update_cw<Src, float, true>(src, n_chunks, chunk_elems, hp, scale,
+                                                          flags, grid, s)
+                    : launch_update_cw<Src, float, false>(src, n_chunks, chunk_elems, hp, scale,
+                                                           flags, grid, s);
+    return clip ? launch_update_cw<Src, uint16_t, true>(src, n_chunks, chunk_elems, hp, scale,
+                                                         flags, grid, s)
+                : launch_update_cw<Src, uint16_t, false>(src, n_chunks, chunk_elems, hp, scale,
+                                                          flags, grid, s);
+}
+
+// Validate one host-visible tensor descriptor for the flat entry points.
+int check_flat(const mi_adamw_tensor* t, int32_t state_dtype, int32_t flags) {
+    if (!t || t->numel <= 0 || !t->param || !t->grad || !t->exp_avg || !t->exp_avg_sq)
+        return MI_ADAMW_E_INVALID;
+    if ((flags & MI_ADAMW_F_BF16_COPY) && !t->param_copy) return MI_ADAMW_E_INVALID;
+    if (t->flags & MI_ADAMW_T_VEC) {
+        const uintptr_t sa = state_dtype == MI_ADAMW_STATE_BF16 ? 8 : 16;
+        if (!aligned(t->param, 16) || !aligned(t->grad, 16) || !aligned(t->exp_avg, sa) ||
+            !aligned(t->exp_avg_sq, sa) ||
+            ((flags & MI_ADAMW_F_BF16_COPY) && !aligned(t->param_copy, 8)))
+            return MI_ADAMW_E_ALIGN;
+    }
+    return MI_ADAMW_OK;
+}
+
+}  // namespace
+
+// ---------------------------------------------------------------------------
+// C ABI
+
+extern "C" {
+
+const char* mi_adamw_version(void) {
+    return "mi_adamw 1 gfx950 fused clip+adamw (fp32/bf16 state, bf16 copy, flat)";
+}
+
+const char* mi_adamw_strerror(int code) {
+    if (code == MI_ADAMW_OK) return "success";
+    if (code == MI_ADAMW_E_INVALID) return "mi_adamw: invalid argument (size, count or pointer)";
+    if (code == MI_ADAMW_E_ALIGN) return "mi_adamw: pointer not aligned for the vector path";
+    if (code > 0) return hipGetErrorString(static_cast<hipError_t>(code));
+    return "mi_adamw: unknown error";
+}
+
+int64_t mi_adamw_build_chunks(const int64_t* numels, int32_t n_tensors, int64_t chunk_elems,
+                              mi_adamw_chunk* out, int64_t cap) {
+    if (!numels || n_tensors < 0 || !chunk_elems_ok(chunk_elems)) return MI_ADAMW_E_INVALID;
+    int64_t n = 0;
+    for (int32_t t = 0; t < n_tensors; ++t) {
+        if (numels[t] < 0) return MI_ADAMW_E_INVALID;
+        const int64_t k = (numels[t] + chunk_elems - 1) / chunk_elems;
+        if (k > 0x7fffffff) return MI_ADAMW_E_INVALID;
+        for (int64_t i = 0; i < k; ++i, ++n) {
+            if (out) {
+                if (n >= cap) return MI_ADAMW_E_INVALID;
+                out[n].tensor = t;
+                out[n].index = static_cast<int32_t>(i);
+            }
+        }
+    }
+    return n;
+}
+
+int mi_adamw_grad_norm(const mi_adamw_tensor* d_tensors, const mi_adamw_chunk* d_chunks,
+                       int64_t n_chunks, int64_t chunk_elems, float max_norm, double* d_partials,
+                       uint32_t* d_counter, float* d_norm, float* d_coef, void* stream) {
+    if (!d_tensors || !d_chunks) return MI_ADAMW_E_INVALID;
+    TableSource src{d_tensors, d_chunks};
+    return launch_norm(src, n_chunks, chunk_elems, max_norm, d_partials, d_counter, d_norm,
+                       d_coef, static_cast<hipStream_t>(stream));
+}
+
+int mi_adamw_grad_norm_flat(const float* d_grad, int64_t n, int64_t chunk_elems, float max_norm,
+                            double* d_partials, uint32_t* d_counter, float* d_norm, float* d_coef,
+                            void* stream) {
+    if (!d_grad || n <= 0 || !chunk_elems_ok(chunk_elems)) return MI_ADAMW_E_INVALID;
+    FlatSource src;
+    memset(&src.t, 0, sizeof(src.t));
+    src.t.grad = const_cast<float*>(d_grad);
+    src.t.numel = n;
+    src.t.flags = aligned(d_grad, 16) ? MI_ADAMW_T_VEC : 0;
+    const int64_t n_chunks = (n + chunk_elems - 1) / chunk_elems;
+    return launch_norm(src, n_chunks, chunk_elems, max_norm, d_partials, d_counter, d_norm, d_coef,
+                       static_cast<hipStream_t>(stream));
+}
+
+int mi_adamw_scale_grads(const mi_adamw_tensor* d_tensors, const mi_adamw_chunk* d_chunks,
+                         int64_t n_chunks, int64_t chunk_elems, const float* d_coef,
+                         void* stream) {
+    if (!d_tensors || !d_chunks || !d_coef || n_chunks <= 0 || !chunk_elems_ok(chunk_elems))
+        return MI_ADAMW_E_INVALID;
+    TableSource src{d_tensors, d_chunks};
+    hipLaunchKernelGGL(mi_adamw_scale_kernel, dim3(grid_for(n_chunks, 0)), dim3(kThreads), 0,
+                       static_cast<hipStream_t>(stream), src, n_chunks, chunk_elems, d_coef);
+    return launch_status();
+}
+
+int mi_adamw_step(const mi_adamw_tensor* d_tensors, const mi_adamw_chunk* d_chunks,
+                  int64_t n_chunks, int64_t chunk_elems, const mi_adamw_hyper* hypers,
+                  int32_t n_hyper, const float* d_grad_scale, int32_t state_dtype, int32_t flags,
+                  int32_t max_blocks, void* stream) {
+    if (!d_tensors || !d_chunks || !hypers || n_hyper <= 0 || n_hyper > MI_ADAMW_MAX_HYPER)
+        return MI_ADAMW_E_INVALID;
+    HyperPack hp;
+    memset(&hp, 0, sizeof(hp));
+    memcpy(hp.h, hypers, sizeof(mi_adamw_hyper) * n_hyper);
+    TableSource src{d_tensors, d_chunks};
+    return launch_update(src, n_chunks, chunk_elems, hp, d_grad_scale, state_dtype, flags,
+                         max_blocks, static_cast<hipStream_t>(stream));
+}
+
+int mi_adamw_step_flat(const mi_adamw_tensor* t, const mi_adamw_hyper* hyper,
+                       const float* d_grad_scale, int64_t chunk_elems, int32_t state_dtype,
+                       int32_t flags, int32_t max_blocks, void* stream) {
+    if (!hyper || !chunk_elems_ok(chunk_elems)) return MI_ADAMW_E_INVALID;
+    int rc = check_flat(t, state_dtype, flags);
+    if (rc != MI_ADAMW_OK) return rc;
+    HyperPack hp;
+    memset(&hp, 0, sizeof(hp));
+    hp.h[0] = *hyper;
+    FlatSource src;
+    src.t = *t;
+    src.t.hyper = 0;
+    const int64_t n_chunks = (t->numel + chunk_elems - 1) / chunk_elems;
+    return launch_update(src, n_chunks, chunk_elems, hp, d_grad_scale, state_dtype, flags,
+                         max_blocks, static_cast<hipStream_t>(stream));
+}
+
+}  // extern "C"

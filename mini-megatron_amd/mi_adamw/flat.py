@@ -1,0 +1,115 @@
+"""Flat-buffer layout: every parameter, gradient and moment packed contiguously.
+
+mini-megatron's ZeRO-1 optimizer (parallel/distributed_optimizer.py:7-48)
+assigns whole tensors to data-parallel ranks round-robin and steps a per-rank
+torch AdamW over them.  The flat layout here is the single-GPU building block
+of a range-sharded ZeRO-1: each param group occupies one contiguous range of
+four flat buffers (params, grads, exp_avg, exp_avg_sq, plus an optional bf16
+model copy), every tensor starts at a 128-byte-aligned offset (32 fp32
+elements), and the step of a group is one contiguous range for the kernel.
+
+Parameters become views of the flat parameter buffer (``p.data`` is replaced)
+and gradients stay allocated as views of the flat gradient buffer, so
+backward accumulates straight into it.  Consequence: every parameter whose
+``p.grad`` is a view is stepped every step, exactly as torch.optim.AdamW does
+after ``zero_grad(set_to_none=False)``.  A parameter whose grad was set to
+None is skipped (torch semantics); a gradient tensor that autograd allocated
+elsewhere is copied into the buffer at the next step.
+"""
+from __future__ import annotations
+
+import torch
+
+ALIGN_ELEMS = 32  # 128 bytes of fp32
+
+
+def _align(n: int) -> int:
+    return (n + ALIGN_ELEMS - 1) // ALIGN_ELEMS * ALIGN_ELEMS
+
+
+class FlatLayout:
+    def __init__(self, param_groups, state_dtype: torch.dtype, bf16_copy: bool):
+        params = [p for g in param_groups for p in g["params"]]
+        if not params:
+            raise ValueError("flat_buffer=True needs at least one parameter")
+        device = params[0].device
+        for p in params:
+            if p.dtype != torch.float32:
+                raise NotImplementedError("flat_buffer=True supports fp32 parameters only")
+            if p.device != device:
+                raise NotImplementedError("flat_buffer=True needs every parameter on one device")
+        if device.type != "cuda":
+            raise RuntimeError("flat_buffer=True needs parameters on a ROCm GPU")
+        self.device = device
+        self.offsets: dict[int, int] = {}
+        self.group_ranges: list[tuple[int, int]] = []
+        off = 0
+        for g in param_groups:
+            start = off
+            for p in g["params"]:
+                self.offsets[id(p)] = off
+                off = _align(off + p.numel())
+            self.group_ranges.append((start, off))
+        self.total = off
+        self.param = torch.zeros(off, dtype=torch.float32, device=device)
+        self.grad = torch.zeros(off, dtype=torch.float32, device=device)
+        self.exp_avg = torch.zeros(off, dtype=state_dtype, device=device)
+        self.exp_avg_sq = torch.zeros(off, dtype=state_dtype, device=device)
+        self.copy = torch.zeros(off, dtype=torch.bfloat16, device=device) if bf16_copy else None
+        with torch.no_grad():
+            for p in params:
+                view = self._view(self.param, p)
+                view.copy_(p.detach())
+                p.data = view
+                gview = self._view(self.grad, p)
+                if p.grad is not None:
+                    gview.copy_(p.grad)
+                p.grad = gview
+            if self.copy is not None:
+                self.copy.copy_(self.param)
+
+    def _view(self, buf: torch.Tensor, p: torch.Tensor) -> torch.Tensor:
+        off = self.offsets[id(p)]
+        return buf[off:off + p.numel()].view(p.shape)
+
+    def grad_view(self, p: torch.Tensor) -> torch.Tensor:
+        return self._view(self.grad, p)
+
+    def is_grad_view(self, p: torch.Tensor, g: torch.Tensor) -> bool:
+        off = self.offsets[id(p)]
+        return g.data_ptr() == self.grad.data_ptr() + 4 * off and g.is_contiguous()
+
+    def absorb_grad(self, p: torch.Tensor) -> torch.Tensor:
+        """Copy a gradient allocated outside the buffer into it; p.grad becomes the view."""
+        view = self.grad_view(p)
+        view.copy_(p.grad)
+        p.grad = view
+        return view
+
+    def state_views(self, p: torch.Tensor):
+        return self._view(self.exp_avg, p), self._view(self.exp_avg_sq, p)
+
+    def adopt_state(self, p: torch.Tensor, key: str, t: torch.Tensor) -> torch.Tensor:
+        view = self._view(self.exp_avg if key == "exp_avg" else self.exp_avg_sq, p)
+        view.copy_(t)
+        return view
+
+    def copy_view(self, p: torch.Tensor) -> torch.Tensor:
+        return self._view(self.copy, p)
+
+    def zero_grads(self, param_groups) -> None:
+        self.grad.zero_()
+        for g in param_groups:
+            for p in g["params"]:
+                if p.grad is None or not self.is_grad_view(p, p.grad):
+                    p.grad = self.grad_view(p)
+
+    def group_row(self, gi: int):
+        """(param, grad, exp_avg, exp_avg_sq, copy) pointers and length of group gi's range."""
+        start, end = self.group_ranges[gi]
+        s_item = self.exp_avg.element_size()
+        return (self.param.data_ptr() + 4 * start, self.grad.data_ptr() + 4 * start,
+                self.exp_avg.data_ptr() + s_item * start,
+                self.exp_avg_sq.data_ptr() + s_item * start,
+                0 if self.copy is None else self.copy.data_ptr() + 2 * start,
+                end - start)

@@ -1,0 +1,567 @@
+"""FusedAdamW: a drop-in torch.optim.AdamW whose step is one HIP launch (two with clip).
+
+Reference interface.  mini-megatron builds ``torch.optim.AdamW(params,
+lr=LEARNING_RATE, weight_decay=WEIGHT_DECAY, fused=args.fused)`` (main.py:144,
+main.py:177), drives ``group["lr"]`` through LambdaLR (main.py:178-180), calls
+``zero_grad()`` and ``step()`` once per iteration (main.py:204,209;
+parallel/pipeline_parallel.py:219-220,260), reads ``param_groups[0]["params"]``
+(parallel/pipeline_parallel.py:219) and checkpoints ``state_dict()``
+(checkpoint.py:9,19).  Without ``--fused`` that AdamW runs torch's
+``_single_tensor_adam`` (torch/optim/adam.py:347-551): 8 ATen kernels per
+parameter tensor.  FusedAdamW keeps the constructor, ``param_groups``,
+``state`` layout, ``state_dict`` format and ``step()`` semantics of
+``torch.optim.AdamW`` (torch/optim/adamw.py:21-49, adam.py:35-272) and
+replaces the per-tensor loop with the kernels of libmi_adamw:
+
+* ``mi_adamw_grad_norm`` -- optional global gradient-norm clip (config.py:16
+  names MAX_GRAD_NORM; torch/nn/utils/clip_grad.py:186-233), computed and
+  applied on the device with no host synchronisation;
+* ``mi_adamw_step`` / ``mi_adamw_step_flat`` -- the AdamW update of every
+  tensor, with fp32 or bf16 moments and an optional bf16 model copy.
+
+Per-element results match ``torch.optim.AdamW(foreach=False)`` on the same GPU
+tensors: the kernels follow the fp32 op chain and the fused multiply-adds of
+torch-ROCm's ATen kernels, and the per-step scalars below are computed on the
+host in float64 exactly as adam.py:414-536 computes them.
+"""
+from __future__ import annotations
+
+from typing import Any, Iterable
+
+import numpy as np
+import torch
+from torch.optim import Optimizer
+
+from . import _lib
+from .flat import FlatLayout
+
+DEFAULT_CHUNK_ELEMS = 65536
+
+_ROW_DTYPE = np.dtype([
+    ("param", "<u8"), ("grad", "<u8"), ("exp_avg", "<u8"), ("exp_avg_sq", "<u8"),
+    ("param_copy", "<u8"), ("numel", "<i8"), ("hyper", "<i4"), ("flags", "<i4"),
+])
+assert _ROW_DTYPE.itemsize == 56
+
+
+def _to_scalar(x):
+    """torch/optim/optimizer.py _to_scalar: a 1-element tensor becomes its Python value."""
+    if isinstance(x, torch.Tensor):
+        return x.item()
+    return x
+
+
+def _hyper(group: dict, step: float) -> _lib.Hyper:
+    """The fp32 scalars one (group, step) hands the kernel.
+
+    adam.py:414-536 in the non-capturable branch: lr, betas and the step count
+    are Python floats; bias corrections, step size and ``bc2 ** 0.5`` are
+    float64; each scalar reaches its ATen kernel cast to fp32, and the division
+    of ``sqrt(v)`` by the host scalar ``bc2_sqrt`` runs on the GPU as a multiply
+    by the reciprocal taken in float64.
+    """
+    lr = float(_to_scalar(group["lr"]))
+    beta1, beta2 = (float(_to_scalar(b)) for b in group["betas"])
+    wd = group["weight_decay"]
+    bias_correction1 = 1 - beta1 ** step
+    bias_correction2 = 1 - beta2 ** step
+    step_size = lr / bias_correction1
+    bias_correction2_sqrt = bias_correction2 ** 0.5
+    f32 = np.float32
+    return _lib.Hyper(
+        wd_factor=float(f32(1 - lr * wd)) if wd != 0 else 1.0,
+        lerp_w=float(f32(1 - beta1)),
+        beta2=float(f32(beta2)),
+        one_minus_beta2=float(f32(1 - beta2)),
+        inv_bc2_sqrt=float(f32(1.0 / bias_correction2_sqrt)),
+        eps=float(f32(group["eps"])),
+        neg_step_size=float(f32(-step_size)),
+        grad_sign=-1.0 if group["maximize"] else 1.0,
+    )
+
+
+def _ptr(t: torch.Tensor | None) -> int:
+    return 0 if t is None else t.data_ptr()
+
+
+class _Launch:
+    """Device-resident tensor and chunk tables for one kernel launch."""
+
+    __slots__ = ("rows", "chunks", "n_chunks", "n_rows")
+
+    def __init__(self, rows: np.ndarray, chunk_elems: int, device: torch.device):
+        lib = _lib.load()
+        numels = np.ascontiguousarray(rows["numel"], dtype=np.int64)
+        n = lib.mi_adamw_build_chunks(numels.ctypes.data, len(numels), chunk_elems, None, 0)
+        _lib.check(int(n) if n < 0 else 0, "mi_adamw_build_chunks")
+        chunks = np.empty(max(int(n), 1) * 2, dtype=np.int32)
+        n2 = lib.mi_adamw_build_chunks(numels.ctypes.data, len(numels), chunk_elems,
+                                       chunks.ctypes.data, int(n))
+        if n2 != n:
+            raise _lib.MiAdamwError("mi_adamw_build_chunks: inconsistent chunk count")
+        self.n_chunks = int(n)
+        self.n_rows = len(rows)
+        self.rows = torch.from_numpy(rows.view(np.uint8).copy()).to(device)
+        self.chunks = torch.from_numpy(chunks.view(np.uint8)).to(device)
+
+
+class FusedAdamW(Optimizer):
+    """AdamW with the whole step fused into one MI355X kernel launch.
+
+    The constructor takes torch.optim.AdamW's arguments, with its defaults and
+    its ValueError checks, plus keyword-only options:
+
+    max_grad_norm:    if set, clip the global gradient L2 norm to this value
+                      before the update, as ``torch.nn.utils.clip_grad_norm_``
+                      would, fused into the step (the norm of the last step is
+                      kept in ``last_grad_norm``, a 0-d device tensor).
+    clip_write_grads: with max_grad_norm, also store the clipped gradients back
+                      into ``p.grad`` (clip_grad_norm_ does; costs 4 B/param).
+    state_dtype:      torch.float32 (default) or torch.bfloat16 for exp_avg and
+                      exp_avg_sq; the math stays fp32 and stores round to
+                      nearest even.
+    bf16_copy:        keep a bf16 copy of every parameter, written by the step
+                      (``bf16_params()`` lists them in param order).
+    flat_buffer:      pack every parameter, gradient and moment into flat
+                      buffers (each tensor at a 128-byte-aligned offset) and
+                      step each param group as one contiguous range.  Gradients
+                      stay allocated: zero_grad() zeroes them in place.
+    chunk_elems:      elements per work chunk (multiple of 1024).
+
+    Not supported (NotImplementedError at construction): amsgrad,
+    capturable, differentiable.
+    """
+
+    def __init__(
+        self,
+        params,
+        lr: float | torch.Tensor = 1e-3,
+        betas: tuple[float | torch.Tensor, float | torch.Tensor] = (0.9, 0.999),
+        eps: float = 1e-8,
+        weight_decay: float = 1e-2,
+        amsgrad: bool = False,
+        *,
+        maximize: bool = False,
+        foreach: bool | None = None,
+        capturable: bool = False,
+        differentiable: bool = False,
+        fused: bool | None = None,
+        max_grad_norm: float | None = None,
+        clip_write_grads: bool = False,
+        state_dtype: torch.dtype = torch.float32,
+        bf16_copy: bool = False,
+        flat_buffer: bool = False,
+        chunk_elems: int = DEFAULT_CHUNK_ELEMS,
+    ) -> None:
+        # adam.py:58-86, in the same order and with the same messages.
+        if isinstance(lr, torch.Tensor):
+            if foreach and not capturable:
+                raise ValueError(
+                    "lr as a Tensor is not supported for capturable=False and foreach=True")
+            if lr.numel() != 1:
+                raise ValueError("Tensor lr must be 1-element")
+        if not 0.0 <= lr:
+            raise ValueError(f"Invalid learning rate: {lr}")
+        if not 0.0 <= eps:
+            raise ValueError(f"Invalid epsilon value: {eps}")
+        if not 0.0 <= betas[0] < 1.0:
+            raise ValueError(f"Invalid beta parameter at index 0: {betas[0]}")
+        if not 0.0 <= betas[1] < 1.0:
+            raise ValueError(f"Invalid beta parameter at index 1: {betas[1]}")
+        if not 0.0 <= weight_decay:
+            raise ValueError(f"Invalid weight_decay value: {weight_decay}")
+        if not ((isinstance(betas[0], float) and isinstance(betas[1], float))
+                or (isinstance(betas[0], torch.Tensor) and isinstance(betas[1], torch.Tensor))):
+            raise ValueError("betas must be either both floats or both Tensors")
+        for i, b in enumerate(betas):
+            if isinstance(b, torch.Tensor):
+                if not capturable and foreach:
+                    raise ValueError(f"betas[{i}] as a Tensor is not supported for "
+                                     "capturable=False and foreach=True")
+                if b.numel() != 1:
+                    raise ValueError(f"Tensor betas[{i}] must be 1-element")
+        betas = tuple(map(_to_scalar, betas))
+        if fused and differentiable:
+            raise RuntimeError("`fused` does not support `differentiable`")
+        if fused and foreach:
+            raise RuntimeError("`fused` and `foreach` cannot be `True` together.")
+        if amsgrad:
+            raise NotImplementedError("FusedAdamW: amsgrad=True is not supported")
+        if capturable:
+            raise NotImplementedError("FusedAdamW: capturable=True is not supported")
+        if differentiable:
+            raise NotImplementedError("FusedAdamW: differentiable=True is not supported")
+        if max_grad_norm is not None and not max_grad_norm > 0:
+            raise ValueError(f"Invalid max_grad_norm: {max_grad_norm}")
+        if state_dtype not in (torch.float32, torch.bfloat16):
+            raise ValueError(f"state_dtype must be torch.float32 or torch.bfloat16, got {state_dtype}")
+        if chunk_elems <= 0 or chunk_elems % 1024:
+            raise ValueError("chunk_elems must be a positive multiple of 1024")
+
+        self.max_grad_norm = None if max_grad_norm is None else float(max_grad_norm)
+        self.clip_write_grads = bool(clip_write_grads)
+        self.state_dtype = state_dtype
+        self.bf16_copy = bool(bf16_copy)
+        self.flat_buffer = bool(flat_buffer)
+        self.chunk_elems = int(chunk_elems)
+        self.max_blocks = 0
+        self.last_grad_norm: torch.Tensor | None = None
+        self._slots: dict[int, int] = {}
+        self._steps = torch.zeros(0, dtype=torch.float32)
+        self._step_views: list[torch.Tensor | None] = []
+        self._copies: dict[int, torch.Tensor] = {}
+        self._launch_cache: tuple | None = None
+        self._workspace: dict[torch.device, tuple] = {}
+        self._flat: FlatLayout | None = None
+        self.timing_events = None
+
+        defaults = dict(
+            lr=lr, betas=betas, eps=eps, weight_decay=weight_decay, amsgrad=amsgrad,
+            maximize=maximize, foreach=foreach, capturable=capturable,
+            differentiable=differentiable, fused=fused, decoupled_weight_decay=True,
+        )
+        super().__init__(params, defaults)
+        self.register_load_state_dict_post_hook(FusedAdamW._after_load_state_dict)
+
+        if self.flat_buffer:
+            self._flat = FlatLayout(self.param_groups, self.state_dtype, self.bf16_copy)
+        elif self.bf16_copy:
+            for group in self.param_groups:
+                for p in group["params"]:
+                    self._copies[id(p)] = p.detach().to(torch.bfloat16)
+
+    # ------------------------------------------------------------------ torch API
+
+    def __setstate__(self, state: dict[str, Any]) -> None:
+        super().__setstate__(state)
+        for group in self.param_groups:
+            group.setdefault("amsgrad", False)
+            group.setdefault("maximize", False)
+            group.setdefault("foreach", None)
+            group.setdefault("capturable", False)
+            group.setdefault("differentiable", False)
+            group.setdefault("fused", None)
+            group["decoupled_weight_decay"] = True
+
+    def add_param_group(self, param_group: dict[str, Any]) -> None:
+        if getattr(self, "_flat", None) is not None:
+            raise NotImplementedError("FusedAdamW(flat_buffer=True): add_param_group after "
+                                      "construction is not supported")
+        super().add_param_group(param_group)
+        if not hasattr(self, "_slots"):
+            return
+        new = [p for p in self.param_groups[-1]["params"] if id(p) not in self._slots]
+        if not new:
+            return
+        old_n = len(self._step_views)
+        steps = torch.zeros(old_n + len(new), dtype=torch.float32)
+        steps[:old_n] = self._steps
+        self._steps = steps
+        for i, p in enumerate(new):
+            self._slots[id(p)] = old_n + i
+        self._step_views.extend([None] * len(new))
+        # Existing per-param step tensors are views of the old buffer: move them.
+        for p_id, slot in list(self._slots.items()):
+            if slot < old_n and self._step_views[slot] is not None:
+                self._step_views[slot] = self._steps[slot]
+        for p, st in self.state.items():
+            if isinstance(p, torch.Tensor) and id(p) in self._slots and "step" in st:
+                slot = self._slots[id(p)]
+                if self._step_views[slot] is not None:
+                    st["step"] = self._step_views[slot]
+        if getattr(self, "bf16_copy", False) and getattr(self, "_flat", None) is None:
+            for p in new:
+                self._copies[id(p)] = p.detach().to(torch.bfloat16)
+        self._launch_cache = None
+
+    def zero_grad(self, set_to_none: bool = True) -> None:
+        if self._flat is not None:
+            # Gradients are views of the flat gradient buffer: zero them in
+            # place so backward accumulates into the buffer again.
+            self._flat.zero_grads(self.param_groups)
+            return
+        super().zero_grad(set_to_none=set_to_none)
+
+    def bf16_params(self) -> list[torch.Tensor]:
+        """The bf16 model copies, in param_groups order (bf16_copy=True)."""
+        if not self.bf16_copy:
+            raise RuntimeError("FusedAdamW was built without bf16_copy=True")
+        if self._flat is not None:
+            return [self._flat.copy_view(p) for g in self.param_groups for p in g["params"]]
+        return [self._copies[id(p)] for g in self.param_groups for p in g["params"]]
+
+    def bf16_param(self, p: torch.Tensor) -> torch.Tensor:
+        if not self.bf16_copy:
+            raise RuntimeError("FusedAdamW was built without bf16_copy=True")
+        if self._flat is not None:
+            return self._flat.copy_view(p)
+        return self._copies[id(p)]
+
+    def state_dict(self) -> dict[str, Any]:
+        sd = super().state_dict()
+        # The packed step buffer is an implementation detail: hand out
+        # independent step tensors, as torch.optim.AdamW does.
+        for st in sd["state"].values():
+            if isinstance(st, dict) and isinstance(st.get("step"), torch.Tensor):
+                st["step"] = st["step"].clone()
+        return sd
+
+    @staticmethod
+    def _after_load_state_dict(self: "FusedAdamW") -> None:
+        """Re-home loaded state: steps into the packed CPU buffer, moments in state_dtype."""
+        for group in self.param_groups:
+            for p in group["params"]:
+                st = self.state.get(p)
+                if not st:
+                    continue
+                slot = self._slots[id(p)]
+                step = st.get("step")
+                if isinstance(step, torch.Tensor):
+                    self._steps[slot] = float(step.item())
+                elif step is not None:
+                    self._steps[slot] = float(step)
+                self._step_views[slot] = self._steps[slot]
+                st["step"] = self._step_views[slot]
+                for key in ("exp_avg", "exp_avg_sq"):
+                    if key in st:
+                        t = st[key]
+                        if self._flat is not None:
+                            st[key] = self._flat.adopt_state(p, key, t)
+                        elif t.dtype != self._state_dtype_for(p):
+                            st[key] = t.to(self._state_dtype_for(p)).contiguous()
+        self._launch_cache = None
+
+    # ------------------------------------------------------------------ step
+
+    def _state_dtype_for(self, p: torch.Tensor) -> torch.dtype:
+        return p.dtype if self.state_dtype == torch.float32 else self.state_dtype
+
+    def _init_state(self, p: torch.Tensor, st: dict) -> None:
+        """adam.py:160-184 lazy state, with the step kept in the packed CPU buffer."""
+        slot = self._slots[id(p)]
+        self._steps[slot] = 0.0
+        self._step_views[slot] = self._steps[slot]
+        st["step"] = self._step_views[slot]
+        if self._flat is not None:
+            st["exp_avg"], st["exp_avg_sq"] = self._flat.state_views(p)
+            st["exp_avg"].zero_()
+            st["exp_avg_sq"].zero_()
+        elif self.state_dtype == torch.float32:
+            st["exp_avg"] = torch.zeros_like(p, memory_format=torch.preserve_format)
+            st["exp_avg_sq"] = torch.zeros_like(p, memory_format=torch.preserve_format)
+        else:
+            st["exp_avg"] = torch.zeros_like(p, dtype=self.state_dtype,
+                                             memory_format=torch.contiguous_format)
+            st["exp_avg_sq"] = torch.zeros_like(p, dtype=self.state_dtype,
+                                                memory_format=torch.contiguous_format)
+
+    def _check_param(self, p: torch.Tensor, g: torch.Tensor) -> None:
+        if g.is_sparse:
+            raise RuntimeError(
+                "Adam does not support sparse gradients, please consider SparseAdam instead")
+        if p.device.type != "cuda":
+            raise RuntimeError(
+                f"FusedAdamW steps parameters on a ROCm GPU only; got a {p.device.type} parameter")
+        if p.dtype not in (torch.float32, torch.complex64):
+            raise NotImplementedError(f"FusedAdamW: parameter dtype {p.dtype} is not supported "
+                                      "(fp32 master parameters only)")
+        if torch.is_complex(p) and self.state_dtype != torch.float32:
+            raise NotImplementedError("FusedAdamW: complex parameters need fp32 state")
+        if g.dtype != p.dtype or g.shape != p.shape or g.device != p.device:
+            raise RuntimeError("FusedAdamW: gradient dtype/shape/device differs from its parameter")
+        if not (p.is_contiguous() and g.is_contiguous()):
+            raise NotImplementedError("FusedAdamW: parameters and gradients must be contiguous")
+
+    @torch.no_grad()
+    def step(self, closure=None):
+        """One optimizer step (adam.py:214-272), fused.  Returns closure's loss."""
+        self._cuda_graph_capture_health_check()
+        loss = None
+        if closure is not None:
+            with torch.enable_grad():
+                loss = closure()
+
+        # Gather params with grads (adam.py:148-153) and initialise their state.
+        entries = []   # (group index, param, grad)
+        slots = []
+        for gi, group in enumerate(self.param_groups):
+            for p in group["params"]:
+                g = p.grad
+                if g is None:
+                    continue
+                if self._flat is not None and not self._flat.is_grad_view(p, g):
+                    self._check_param(p, g)
+                    g = self._flat.absorb_grad(p)
+                self._check_param(p, g)
+                st = self.state[p]
+                if len(st) == 0:
+                    self._init_state(p, st)
+                else:
+                    slot = self._slots[id(p)]
+                    if st["step"] is not self._step_views[slot]:
+                        self._adopt_step(p, st, slot)
+                entries.append((gi, p, g))
+                slots.append(self._slots[id(p)])
+        if not entries:
+            return loss
+
+        # step_t += 1 for every param with a grad (adam.py:414), in one op.
+        if len(slots) == len(self._step_views):
+            self._steps += 1
+        else:
+            idx = torch.as_tensor(slots, dtype=torch.long)
+            self._steps[idx] += 1
+        steps_np = self._steps.numpy()
+
+        device = entries[0][1].device
+        if any(p.device != device for _, p, _ in entries):
+            raise NotImplementedError("FusedAdamW: all parameters must be on one device")
+
+        # One hyperparameter set per distinct (group, step value).
+        keys: dict[tuple[int, float], int] = {}
+        hyper_idx = []
+        for (gi, _, _), slot in zip(entries, slots):
+            k = (gi, float(steps_np[slot]))
+            h = keys.get(k)
+            if h is None:
+                h = keys[k] = len(keys)
+            hyper_idx.append(h)
+        hypers = [_hyper(self.param_groups[gi], step) for (gi, step) in keys]
+
+        with torch.cuda.device(device):
+            self._launch(entries, hyper_idx, hypers, device)
+        return loss
+
+    def _adopt_step(self, p, st, slot):
+        """state["step"] was replaced from outside: copy its value into the buffer."""
+        step = st["step"]
+        self._steps[slot] = float(step.item()) if isinstance(step, torch.Tensor) else float(step)
+        self._step_views[slot] = self._steps[slot]
+        st["step"] = self._step_views[slot]
+
+    # ------------------------------------------------------------------ launches
+
+    def _ws(self, device: torch.device):
+        ws = self._workspace.get(device)
+        if ws is None:
+            partials = torch.zeros(_lib.MAX_NORM_BLOCKS, dtype=torch.float64, device=device)
+            counter = torch.zeros(1, dtype=torch.int32, device=device)
+            coef = torch.zeros(1, dtype=torch.float32, device=device)
+            ws = self._workspace[device] = (partials, counter, coef)
+        return ws
+
+    def _rows(self, entries, hyper_idx) -> np.ndarray:
+        if self._flat is not None:
+            return self._flat_rows(entries, hyper_idx)
+        return self._tensor_rows(entries, hyper_idx)
+
+    def _flat_rows(self, entries, hyper_idx) -> np.ndarray:
+        """One row per param group whose every param steps with one hyper set."""
+        by_group: dict[int, list[int]] = {}
+        for i, (gi, _, _) in enumerate(entries):
+            by_group.setdefault(gi, []).append(i)
+        rows = []
+        for gi, idx in by_group.items():
+            hs = {hyper_idx[i] for i in idx}
+            if len(idx) == len(self.param_groups[gi]["params"]) and len(hs) == 1:
+                pp, gp, mp, vp, cp, n = self._flat.group_row(gi)
+                r = np.zeros(1, dtype=_ROW_DTYPE)
+                r[0] = (pp, gp, mp, vp, cp, n, hs.pop(), _lib.T_VEC)
+                rows.append(r)
+            else:
+                rows.append(self._tensor_rows([entries[i] for i in idx],
+                                              [hyper_idx[i] for i in idx]))
+        return np.concatenate(rows) if rows else np.zeros(0, dtype=_ROW_DTYPE)
+
+    def _tensor_rows(self, entries, hyper_idx) -> np.ndarray:
+        rows = np.zeros(len(entries), dtype=_ROW_DTYPE)
+        bf16_state = self.state_dtype == torch.bfloat16
+        for i, ((_, p, g), h) in enumerate(zip(entries, hyper_idx)):
+            st = self.state[p]
+            m, v = st["exp_avg"], st["exp_avg_sq"]
+            c = self._copy_for(p) if self.bf16_copy else None
+            pp, gp, mp, vp, cp = p.data_ptr(), g.data_ptr(), m.data_ptr(), v.data_ptr(), _ptr(c)
+            n = p.numel() * (2 if torch.is_complex(p) else 1)
+            sa = 8 if bf16_state else 16
+            vec = (pp % 16 == 0 and gp % 16 == 0 and mp % sa == 0 and vp % sa == 0
+                   and cp % 8 == 0)
+            rows[i] = (pp, gp, mp, vp, cp, n, h, _lib.T_VEC if vec else 0)
+        return rows[rows["numel"] > 0]
+
+    def _copy_for(self, p):
+        if self._flat is not None:
+            return self._flat.copy_view(p)
+        return self._copies[id(p)]
+
+    def _signature(self, entries, hyper_idx) -> list:
+        sig = []
+        for (_, p, g), h in zip(entries, hyper_idx):
+            st = self.state[p]
+            sig += (p.data_ptr(), g.data_ptr(), st["exp_avg"].data_ptr(),
+                    st["exp_avg_sq"].data_ptr(), h)
+        return sig
+
+    def _launch(self, entries, hyper_idx, hypers, device) -> None:
+        lib = _lib.load()
+        stream = torch.cuda.current_stream(device).cuda_stream
+        partials, counter, coef = self._ws(device)
+        flags = 0
+        if self.bf16_copy:
+            flags |= _lib.F_BF16_COPY
+        state_code = _lib.STATE_BF16 if self.state_dtype == torch.bfloat16 else _lib.STATE_F32
+
+        # Partition into launches of at most MAX_HYPER hyperparameter sets.
+        if len(hypers) > _lib.MAX_HYPER:
+            parts = []
+            for start in range(0, len(hypers), _lib.MAX_HYPER):
+                sel = [i for i, h in enumerate(hyper_idx) if start <= h < start + _lib.MAX_HYPER]
+                parts.append(([entries[i] for i in sel],
+                              [hyper_idx[i] - start for i in sel],
+                              hypers[start:start + _lib.MAX_HYPER]))
+        else:
+            parts = [(entries, hyper_idx, hypers)]
+
+        # Tables: reused while pointers and hyperparameter assignment are unchanged.
+        sig = self._signature(entries, hyper_idx)
+        cache = self._launch_cache
+        if cache is not None and cache[0] == sig and cache[1] == device:
+            launches, norm_launch = cache[2], cache[3]
+        else:
+            launches = [_Launch(self._rows(e, hi), self.chunk_elems, device) for e, hi, _ in parts]
+            if len(parts) == 1:
+                norm_launch = launches[0]
+            else:
+                norm_launch = _Launch(self._rows(entries, [0] * len(entries)),
+                                      self.chunk_elems, device)
+            self._launch_cache = (sig, device, launches, norm_launch)
+
+        ev = self.timing_events
+        if ev is not None:
+            ev[0].record()
+        if self.max_grad_norm is not None:
+            norm = torch.empty((), dtype=torch.float32, device=device)
+            if norm_launch.n_chunks > 0:
+                _lib.check(lib.mi_adamw_grad_norm(
+                    norm_launch.rows.data_ptr(), norm_launch.chunks.data_ptr(),
+                    norm_launch.n_chunks, self.chunk_elems, float(self.max_grad_norm),
+                    partials.data_ptr(), counter.data_ptr(), norm.data_ptr(), coef.data_ptr(),
+                    stream), "mi_adamw_grad_norm")
+            else:
+                norm.zero_()
+                coef.fill_(1.0)
+            self.last_grad_norm = norm
+            flags |= _lib.F_CLIP
+            if self.clip_write_grads:
+                flags |= _lib.F_WRITE_GRAD
+        if ev is not None:
+            ev[1].record()
+        for launch, (_, _, hs) in zip(launches, parts):
+            if launch.n_chunks == 0:
+                continue
+            harr = (_lib.Hyper * len(hs))(*hs)
+            _lib.check(lib.mi_adamw_step(
+                launch.rows.data_ptr(), launch.chunks.data_ptr(), launch.n_chunks,
+                self.chunk_elems, harr, len(hs), coef.data_ptr(), state_code, flags,
+                self.max_blocks, stream), "mi_adamw_step")
+        if ev is not None:
+            ev[2].record()

@@ -1,0 +1,212 @@
+/*
+ * adamw_oracle.c -- CPU restatement of the AdamW optimizer step and the global
+ * gradient-norm clip, used ONLY as test infrastructure (the checker).
+ *
+ * Nothing in the product links or calls this file.  The pytest suite, the smoke
+ * check and the CPU-baseline leg of the benchmark load it through oracle.py.
+ *
+ * What it restates (torch 2.10.0+rocm7.0, the third-party code mini-megatron's
+ * training loop calls; the reference itself contains no optimizer arithmetic):
+ *   - torch/optim/adam.py:396-547  `_single_tensor_adam`, the path that
+ *     mini-megatron's main.py:177 (AdamW(..., fused=False)) takes, as the
+ *     per-element op chain of the 7 ATen kernels it launches per tensor:
+ *       adam.py:419  p  = p * f32(1 - lr*wd)                       (mul_)
+ *       adam.py:457  m  = lerp(m, g, f32(1 - beta1))                 (lerp_)
+ *       adam.py:476  v  = v * f32(beta2); v = v + f32(1-beta2)*g*g   (mul_, addcmul_)
+ *       adam.py:545  d  = sqrt(v) / bc2_sqrt; d = d + f32(eps)       (sqrt, div, add_)
+ *       adam.py:547  p  = p + f32(-step_size) * (m / d)              (addcdiv_)
+ *   - torch/include/ATen/native/Lerp.h:21-35  the two-branch lerp formula.
+ *   - torch/nn/utils/clip_grad.py:50-117,121-183  global L2 norm, then
+ *     coef = clamp(max_norm * reciprocal(norm + 1e-6), max=1), g *= coef.
+ *
+ * Every ATen kernel rounds its result to fp32, so each step above is one fp32
+ * rounding.  Whether the compiler that built a given torch binary contracted
+ * `a + b*c` into one fused multiply-add, and whether division by a host scalar
+ * runs as a true division or as a multiply by an fp32 reciprocal, differs
+ * between torch's CPU and GPU builds.  Those choices are the fields of
+ * `oracle_opmodel`; the tests pin one op model against torch on the CPU
+ * (golden fixtures) and one against torch on the GPU (per-op probes).
+ *
+ * Build: gcc -O2 -ffp-contract=off (Makefile beside this file).  Contraction
+ * must stay off so that every fused multiply-add here is an explicit fmaf().
+ */
+#include <math.h>
+#include <stdint.h>
+#include <string.h>
+
+typedef struct oracle_opmodel {
+    int lerp_fma;     /* 1: self + w*(end-self) evaluated as fmaf(w, end-self, self)    */
+    int addcmul_mode; /* v + s*g*g:  0 = v + (s*(g*g)) rounded per op,
+                                      1 = fmaf(s, g*g, v),
+                                      2 = fmaf(s*g, g, v),
+                                      3 = v + ((s*g)*g) rounded per op               */
+    int addcdiv_mode; /* p + s*m/d:  0 = p + (s*(m/d)) rounded per op,
+                                      1 = fmaf(s, m/d, p),
+                                      2 = p + ((s*m)/d) rounded per op               */
+    int div_recip;    /* 1: x / c evaluated as x * f32(1.0 / c), the reciprocal taken
+                            in float64 on the host (host scalar c); 0: x / f32(c)      */
+} oracle_opmodel;
+
+/* Host scalars of one AdamW step, already reduced the way adam.py:414-536 and
+ * ATen's scalar handling reduce them (float64 on the host, then cast to fp32). */
+typedef struct oracle_hyper {
+    float wd_factor;       /* f32(1 - lr*wd); 1.0f when weight_decay == 0 (adam.py:417-419) */
+    float lerp_w;          /* f32(1 - beta1)                         (adam.py:457)          */
+    float beta2;           /* f32(beta2)                             (adam.py:476)          */
+    float one_minus_beta2; /* f32(1 - beta2)                         (adam.py:476)          */
+    double bc2_sqrt;       /* (1 - beta2**step) ** 0.5 in float64    (adam.py:532,536)      */
+    float eps;             /* f32(eps)                               (adam.py:545)          */
+    float neg_step_size;   /* f32(-(lr / (1 - beta1**step)))         (adam.py:534,547)      */
+    float grad_sign;       /* -1.0f when maximize (adam.py:397), else 1.0f                  */
+} oracle_hyper;
+
+static inline uint32_t f2u(float x) { uint32_t u; memcpy(&u, &x, 4); return u; }
+static inline float u2f(uint32_t u) { float x; memcpy(&x, &u, 4); return x; }
+
+/* fp32 -> bf16, round to nearest even; every NaN becomes 0x7FC0, the value
+ * torch's Tensor.to(torch.bfloat16) produces for NaN. */
+uint16_t oracle_f32_to_bf16(float x)
+{
+    uint32_t u = f2u(x);
+    if ((u & 0x7f800000u) == 0x7f800000u && (u & 0x007fffffu))
+        return (uint16_t)0x7fc0u;
+    uint32_t lsb = (u >> 16) & 1u;
+    u += 0x7fffu + lsb;
+    return (uint16_t)(u >> 16);
+}
+
+float oracle_bf16_to_f32(uint16_t h) { return u2f((uint32_t)h << 16); }
+
+/* Lerp.h:21-35 with fp32 opmath. */
+static inline float lerp_f32(float self, float end, float w, int use_fma)
+{
+    float diff = end - self;
+    if (fabsf(w) < 0.5f)
+        return use_fma ? fmaf(w, diff, self) : self + w * diff;
+    float omw = 1.0f - w;
+    return use_fma ? fmaf(-diff, omw, end) : end - diff * omw;
+}
+
+static inline float addcmul_f32(float v, float s, float g, int mode)
+{
+    switch (mode) {
+    case 1: return fmaf(s, g * g, v);
+    case 2: return fmaf(s * g, g, v);
+    case 3: { float sg = s * g; float t = sg * g; return v + t; }
+    default: { float gg = g * g; float t = s * gg; return v + t; }
+    }
+}
+
+/* One element of the op chain above.  p, m, v are updated in place. */
+static inline void adamw_elem(float *p, float g, float *m, float *v,
+                              const oracle_hyper *h, const oracle_opmodel *om,
+                              float inv_bc2, float bc2f)
+{
+    float pp = *p * h->wd_factor;                           /* adam.py:419 */
+    float mm = lerp_f32(*m, g, h->lerp_w, om->lerp_fma);    /* adam.py:457 */
+    float vv = *v * h->beta2;                               /* adam.py:476 */
+    vv = addcmul_f32(vv, h->one_minus_beta2, g, om->addcmul_mode);
+    float d = sqrtf(vv);                                    /* adam.py:545 */
+    d = om->div_recip ? d * inv_bc2 : d / bc2f;
+    d = d + h->eps;
+                                                            /* adam.py:547 */
+    if (om->addcdiv_mode == 2) {
+        float sm = h->neg_step_size * mm;
+        pp = pp + sm / d;
+    } else {
+        float q = mm / d;
+        pp = om->addcdiv_mode == 1 ? fmaf(h->neg_step_size, q, pp) : pp + h->neg_step_size * q;
+    }
+    *p = pp; *m = mm; *v = vv;
+}
+
+/* fp32 state: p, g, m, v are n contiguous floats.  grad_scale multiplies the
+ * gradient first (clip_grad.py:174, g *= coef), then grad_sign applies
+ * `maximize` (adam.py:397).  Pass grad_scale = 1 for "no clip". */
+void oracle_adamw_f32(float *p, const float *g, float *m, float *v, int64_t n,
+                      const oracle_hyper *h, const oracle_opmodel *om, float grad_scale,
+                      int apply_scale)
+{
+    float bc2f = (float)h->bc2_sqrt;
+    float inv_bc2 = (float)(1.0 / h->bc2_sqrt);
+    for (int64_t i = 0; i < n; ++i) {
+        float gi = g[i];
+        if (apply_scale) gi = gi * grad_scale;
+        gi = gi * h->grad_sign;
+        adamw_elem(&p[i], gi, &m[i], &v[i], h, om, inv_bc2, bc2f);
+    }
+}
+
+/* bf16 state variant: m and v are stored as bf16, widened to fp32, updated with
+ * the same fp32 op chain, and stored back rounded to nearest even.  If copy is
+ * non-NULL the updated fp32 parameter is also written as a bf16 model copy. */
+void oracle_adamw_bf16state(float *p, const float *g, uint16_t *m, uint16_t *v, int64_t n,
+                            const oracle_hyper *h, const oracle_opmodel *om, float grad_scale,
+                            int apply_scale)
+{
+    float bc2f = (float)h->bc2_sqrt;
+    float inv_bc2 = (float)(1.0 / h->bc2_sqrt);
+    for (int64_t i = 0; i < n; ++i) {
+        float gi = g[i];
+        if (apply_scale) gi = gi * grad_scale;
+        gi = gi * h->grad_sign;
+        float mm = oracle_bf16_to_f32(m[i]);
+        float vv = oracle_bf16_to_f32(v[i]);
+        adamw_elem(&p[i], gi, &mm, &vv, h, om, inv_bc2, bc2f);
+        m[i] = oracle_f32_to_bf16(mm);
+        v[i] = oracle_f32_to_bf16(vv);
+    }
+}
+
+void oracle_to_bf16(const float *x, uint16_t *out, int64_t n)
+{
+    for (int64_t i = 0; i < n; ++i) out[i] = oracle_f32_to_bf16(x[i]);
+}
+
+/* Sum of squares in float64.  Each square of an fp32 value is exact in
+ * float64; blocks of 4096 are summed first so the rounding error stays far
+ * below fp32 resolution even for 1e10 terms. */
+double oracle_sumsq_f64(const float *g, int64_t n)
+{
+    double total = 0.0;
+    for (int64_t b = 0; b < n; b += 4096) {
+        int64_t e = b + 4096 < n ? b + 4096 : n;
+        double s = 0.0;
+        for (int64_t i = b; i < e; ++i) { double x = (double)g[i]; s += x * x; }
+        total += s;
+    }
+    return total;
+}
+
+/* clip_grad.py:165-169 on a 0-d fp32 tensor `norm`:
+ *   t = norm + f32(1e-6); r = 1/t (Tensor.__rtruediv__ = reciprocal * other);
+ *   coef = r * f32(max_norm); clamp(max=1.0) keeps NaN. */
+float oracle_clip_coef(float total_norm, double max_norm)
+{
+    float t = total_norm + (float)1e-6;
+    float r = 1.0f / t;
+    float c = r * (float)max_norm;
+    return (c > 1.0f) ? 1.0f : c;
+}
+
+/* ulp distance between two fp32 arrays, as the number of representable floats
+ * between them (sign-magnitude mapped to a monotone integer line).  NaN vs NaN
+ * counts as 0, NaN vs number as INT64_MAX. */
+int64_t oracle_max_ulp(const float *a, const float *b, int64_t n, int64_t *argmax)
+{
+    int64_t worst = 0, where = -1;
+    for (int64_t i = 0; i < n; ++i) {
+        int an = isnan(a[i]), bn = isnan(b[i]);
+        int64_t d;
+        if (an || bn) d = (an && bn) ? 0 : INT64_MAX;
+        else {
+            int32_t ia = (int32_t)f2u(a[i]), ib = (int32_t)f2u(b[i]);
+            int64_t la = ia < 0 ? (int64_t)INT32_MIN - ia : ia;
+            int64_t lb = ib < 0 ? (int64_t)INT32_MIN - ib : ib;
+            d = la > lb ? la - lb : lb - la;
+        }
+        if (d > worst) { worst = d; where = i; }
+    }
+    if (argmax) *argmax = where;
+    return worst;
+}

@@ -1,0 +1,245 @@
+"""CPU oracle for the fused clip + AdamW step -- TEST INFRASTRUCTURE ONLY.
+
+The product never imports this module.  Only the pytest suite, the smoke check
+(``__graft_entry__.smoke``) and the CPU-baseline leg of ``bench.py`` may load
+it, and there only as the checker.
+
+It restates, in NumPy plus the C kernels of ``adamw_oracle.c``:
+
+* ``hyper_from_group`` -- the host-side float64 scalar arithmetic of
+  ``torch/optim/adam.py:414-536`` (step += 1, bias corrections, step size,
+  ``bc2 ** 0.5``) and ATen's cast of each Python scalar to the fp32 opmath
+  type of the kernel that consumes it.
+* ``adamw_step`` / ``adamw_step_bf16state`` -- the per-element op chain of
+  ``_single_tensor_adam`` (``adam.py:419,457,476,545,547``) and
+  ``ATen/native/Lerp.h:21-35``, one fp32 rounding per ATen kernel.
+* ``total_norm`` / ``clip_coef`` -- ``torch/nn/utils/clip_grad.py:50-117``
+  (global L2 norm over all gradients) and ``:165-169`` (the clamped
+  coefficient), the clip mini-megatron defines at ``config.py:16``
+  (``MAX_GRAD_NORM = 1.0``).
+
+How each function is pinned (none of it is trusted on its own):
+
+* The op chain: ``OPMODEL_TORCH_CPU`` is checked bit-for-bit against golden
+  fixtures written by ``torch.optim.AdamW(foreach=False)`` on the CPU
+  (``tests/golden/make_golden.py``), and ``OPMODEL_TORCH_ROCM`` bit-for-bit
+  against each ATen op of the same chain run by torch on the MI355X (a GPU
+  test).  Closed forms pin the rest: ``lr = 0`` leaves p bitwise unchanged,
+  step 1 from zero state gives ``m = f32(0.1 g)``, ``g = 0`` decays m and v
+  geometrically, ``wd = 0`` is the identity on the first op.
+* The clip norm: fixtures from ``clip_grad_norm_`` (rel 1e-6), the closed form
+  ``|c| sqrt(N)`` for constant gradients, and an exact float64 brute force on
+  tiny inputs.
+* The bf16 paths: a brute-force round-to-nearest-even check of
+  ``oracle_f32_to_bf16`` over every rounding boundary class, and torch's own
+  ``Tensor.to(torch.bfloat16)`` on the same values.
+"""
+from __future__ import annotations
+
+import ctypes
+import math
+import os
+from dataclasses import dataclass
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_LIB_PATH = os.path.join(_HERE, "liboracle.so")
+
+
+class OpModel(ctypes.Structure):
+    """Which ATen ops were compiled with fused multiply-adds (see adamw_oracle.c)."""
+
+    _fields_ = [
+        ("lerp_fma", ctypes.c_int),
+        ("addcmul_mode", ctypes.c_int),
+        ("addcdiv_mode", ctypes.c_int),
+        ("div_recip", ctypes.c_int),
+    ]
+
+    def __repr__(self) -> str:  # pragma: no cover - debugging aid
+        return (f"OpModel(lerp_fma={self.lerp_fma}, addcmul_mode={self.addcmul_mode}, "
+                f"addcdiv_mode={self.addcdiv_mode}, div_recip={self.div_recip})")
+
+
+class Hyper(ctypes.Structure):
+    _fields_ = [
+        ("wd_factor", ctypes.c_float),
+        ("lerp_w", ctypes.c_float),
+        ("beta2", ctypes.c_float),
+        ("one_minus_beta2", ctypes.c_float),
+        ("bc2_sqrt", ctypes.c_double),
+        ("eps", ctypes.c_float),
+        ("neg_step_size", ctypes.c_float),
+        ("grad_sign", ctypes.c_float),
+    ]
+
+
+# torch 2.10 CPU build (AVX-512 vectorised ATen kernels): lerp is fused
+# (fma(w, end-self, self)), addcmul is fma(s*g, g, v), addcdiv is
+# p + (s*m)/d rounded per op, and the division by a Python scalar is a true
+# fp32 division.  Its vectorised sqrt is not always correctly rounded (about
+# 0.6% of inputs differ by 1 ulp from IEEE sqrt), so the oracle, which uses the
+# IEEE sqrt, matches it exactly on m and v and within 1 ulp on p.
+# Pinned by tests/test_oracle.py against the tests/golden fixtures.
+OPMODEL_TORCH_CPU = OpModel(lerp_fma=1, addcmul_mode=2, addcdiv_mode=2, div_recip=0)
+
+# torch 2.10.0+rocm7.0 on gfx950: lerp, addcmul (fma(s, g*g, v)) and addcdiv
+# (fma(s, m/d, p)) are fused multiply-adds; sqrt and division are correctly
+# rounded; a tensor divided by a Python scalar c runs as a multiply by
+# f32(1.0 / c) with the reciprocal taken in float64.  Pinned bit-for-bit by the
+# GPU test tests/test_gpu_torch_opmodel.py.
+OPMODEL_TORCH_ROCM = OpModel(lerp_fma=1, addcmul_mode=1, addcdiv_mode=1, div_recip=1)
+
+
+def _load():
+    if not os.path.exists(_LIB_PATH):
+        raise RuntimeError(f"oracle library missing: build it with `make -C {_HERE}`")
+    lib = ctypes.CDLL(_LIB_PATH)
+    f32p = ctypes.POINTER(ctypes.c_float)
+    u16p = ctypes.POINTER(ctypes.c_uint16)
+    i64 = ctypes.c_int64
+    lib.oracle_adamw_f32.argtypes = [f32p, f32p, f32p, f32p, i64, ctypes.POINTER(Hyper),
+                                     ctypes.POINTER(OpModel), ctypes.c_float, ctypes.c_int]
+    lib.oracle_adamw_f32.restype = None
+    lib.oracle_adamw_bf16state.argtypes = [f32p, f32p, u16p, u16p, i64, ctypes.POINTER(Hyper),
+                                           ctypes.POINTER(OpModel), ctypes.c_float, ctypes.c_int]
+    lib.oracle_adamw_bf16state.restype = None
+    lib.oracle_to_bf16.argtypes = [f32p, u16p, i64]
+    lib.oracle_to_bf16.restype = None
+    lib.oracle_sumsq_f64.argtypes = [f32p, i64]
+    lib.oracle_sumsq_f64.restype = ctypes.c_double
+    lib.oracle_clip_coef.argtypes = [ctypes.c_float, ctypes.c_double]
+    lib.oracle_clip_coef.restype = ctypes.c_float
+    lib.oracle_max_ulp.argtypes = [f32p, f32p, i64, ctypes.POINTER(i64)]
+    lib.oracle_max_ulp.restype = i64
+    lib.oracle_f32_to_bf16.argtypes = [ctypes.c_float]
+    lib.oracle_f32_to_bf16.restype = ctypes.c_uint16
+    return lib
+
+
+_lib = None
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        _lib = _load()
+    return _lib
+
+
+def _f32(a: np.ndarray):
+    if a.dtype != np.float32 or not a.flags.c_contiguous:
+        raise TypeError("oracle expects C-contiguous float32 arrays")
+    return a.ctypes.data_as(ctypes.POINTER(ctypes.c_float))
+
+
+def _u16(a: np.ndarray):
+    if a.dtype != np.uint16 or not a.flags.c_contiguous:
+        raise TypeError("oracle expects C-contiguous uint16 (bf16 bit) arrays")
+    return a.ctypes.data_as(ctypes.POINTER(ctypes.c_uint16))
+
+
+@dataclass
+class GroupScalars:
+    """Float64 host values of one step, before the casts to fp32."""
+
+    step: float
+    bias_correction1: float
+    bias_correction2: float
+    step_size: float
+    bias_correction2_sqrt: float
+
+
+def group_scalars(lr: float, beta1: float, beta2: float, step: float) -> GroupScalars:
+    """adam.py:529-536 (the non-capturable branch): Python float64 arithmetic."""
+    bc1 = 1 - beta1 ** step
+    bc2 = 1 - beta2 ** step
+    step_size = lr / bc1
+    bc2_sqrt = bc2 ** 0.5
+    return GroupScalars(step, bc1, bc2, step_size, bc2_sqrt)
+
+
+def hyper_from_group(lr, beta1, beta2, eps, weight_decay, step, maximize=False) -> Hyper:
+    """Host scalars for step number ``step`` (the value after ``step_t += 1``).
+
+    ``step`` is what ``_get_value(step_t)`` returns: the fp32 step tensor read
+    back as a Python float (adam.py:414,529; optimizer.py:91-96).
+    """
+    s = group_scalars(float(lr), float(beta1), float(beta2), float(np.float32(step)))
+    wd_factor = np.float32(1 - lr * weight_decay) if weight_decay != 0 else np.float32(1.0)
+    return Hyper(
+        wd_factor=float(wd_factor),
+        lerp_w=float(np.float32(1 - beta1)),
+        beta2=float(np.float32(beta2)),
+        one_minus_beta2=float(np.float32(1 - beta2)),
+        bc2_sqrt=s.bias_correction2_sqrt,
+        eps=float(np.float32(eps)),
+        neg_step_size=float(np.float32(-s.step_size)),
+        grad_sign=-1.0 if maximize else 1.0,
+    )
+
+
+def adamw_step(p, g, m, v, *, lr, betas, eps, weight_decay, step, maximize=False,
+               grad_scale=None, opmodel=OPMODEL_TORCH_ROCM) -> None:
+    """One AdamW step on fp32 numpy arrays, in place (p, m, v)."""
+    h = hyper_from_group(lr, betas[0], betas[1], eps, weight_decay, step, maximize)
+    n = p.size
+    if not (g.size == m.size == v.size == n):
+        raise ValueError("p, g, m, v sizes differ")
+    scale = 1.0 if grad_scale is None else float(np.float32(grad_scale))
+    lib().oracle_adamw_f32(_f32(p), _f32(g), _f32(m), _f32(v), n, ctypes.byref(h),
+                           ctypes.byref(opmodel), scale, 0 if grad_scale is None else 1)
+
+
+def adamw_step_bf16state(p, g, m_bits, v_bits, *, lr, betas, eps, weight_decay, step,
+                         maximize=False, grad_scale=None, opmodel=OPMODEL_TORCH_ROCM) -> None:
+    """AdamW step with bf16-stored moments (uint16 bit arrays), fp32 math."""
+    h = hyper_from_group(lr, betas[0], betas[1], eps, weight_decay, step, maximize)
+    n = p.size
+    scale = 1.0 if grad_scale is None else float(np.float32(grad_scale))
+    lib().oracle_adamw_bf16state(_f32(p), _f32(g), _u16(m_bits), _u16(v_bits), n,
+                                 ctypes.byref(h), ctypes.byref(opmodel), scale,
+                                 0 if grad_scale is None else 1)
+
+
+def to_bf16_bits(x: np.ndarray) -> np.ndarray:
+    """fp32 -> bf16 bit patterns, round to nearest even."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.empty(x.shape, dtype=np.uint16)
+    lib().oracle_to_bf16(_f32(x), _u16(out), x.size)
+    return out
+
+
+def bf16_bits_to_f32(b: np.ndarray) -> np.ndarray:
+    return (np.asarray(b, dtype=np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+def sumsq(grads) -> float:
+    """Sum of squares of every gradient, float64 (exact squares, blocked sums)."""
+    total = 0.0
+    for g in grads:
+        g = np.ascontiguousarray(g, dtype=np.float32).reshape(-1)
+        total += lib().oracle_sumsq_f64(_f32(g), g.size)
+    return total
+
+
+def total_norm(grads) -> np.float32:
+    """clip_grad.py:50-117 for norm_type 2: the L2 norm of all gradients as one vector."""
+    return np.float32(math.sqrt(sumsq(grads)))
+
+
+def clip_coef(norm, max_norm: float) -> np.float32:
+    """clip_grad.py:165-169: clamp(max_norm * reciprocal(norm + 1e-6), max=1)."""
+    return np.float32(lib().oracle_clip_coef(float(np.float32(norm)), float(max_norm)))
+
+
+def max_ulp(a: np.ndarray, b: np.ndarray) -> tuple[int, int]:
+    """(largest ulp distance, index of it) between two fp32 arrays."""
+    a = np.ascontiguousarray(a, dtype=np.float32).reshape(-1)
+    b = np.ascontiguousarray(b, dtype=np.float32).reshape(-1)
+    if a.size != b.size:
+        raise ValueError("size mismatch")
+    where = ctypes.c_int64(-1)
+    d = lib().oracle_max_ulp(_f32(a), _f32(b), a.size, ctypes.byref(where))
+    return int(d), int(where.value)

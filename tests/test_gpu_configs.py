@@ -1,0 +1,249 @@
+"""The five benchmark configurations at full size, on one MI355X.
+
+1. gpt-125m fp32, one step from zero state, no clip: bit-exact vs torch.
+2. gpt-125m fp32 + clip, 100 chained steps from step 1000: bit-exact vs torch
+   driven by the kernel's norm at every step; rel 1e-5 vs torch end to end;
+   norm rel 1e-6 vs clip_grad_norm_.
+3. gpt-350m fp32 master + clip + bf16 model copy, step 1000: bit-exact, copy ==
+   RNE(p).
+4. gpt-1.3b bf16 moments + bf16 copy (with and without clip): bit-exact vs the
+   oracle's bf16-state model on sampled tensors; within the bf16 rounding bound
+   of the fp32-state torch reference everywhere.
+5. gpt-6.7b flat buffer + clip + bf16 copy, step 1000: norm vs float64 and
+   torch; sampled tensors bit-exact vs torch stepped with the same norm.
+"""
+from __future__ import annotations
+
+import gc
+
+import numpy as np
+import pytest
+import torch
+
+from _helpers import (clone_params, close_rel, gpt_params, load_states, max_ulp, max_ulp_all,
+                      midtrain_state, rel_err, rms, set_grads, to_np)
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+HP = dict(lr=3e-4, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.1)
+
+
+@pytest.fixture
+def dev():
+    if not torch.cuda.is_available():
+        pytest.fail("GPU test run without a ROCm GPU")
+    yield torch.device("cuda", 0)
+    gc.collect()
+    torch.cuda.empty_cache()
+
+
+def _same_state(ref, ours, topt, oopt):
+    du = max_ulp_all(list(ref), list(ours))
+    dm = max_ulp_all([topt.state[p]["exp_avg"] for p in ref], [oopt.state[q]["exp_avg"] for q in ours])
+    dv = max_ulp_all([topt.state[p]["exp_avg_sq"] for p in ref],
+                     [oopt.state[q]["exp_avg_sq"] for q in ours])
+    return du, dm, dv
+
+
+def test_config1_125m_fp32_step1(dev):
+    import mi_adamw
+    from mi_adamw.workloads import GPT_125M
+    ref = gpt_params(GPT_125M, dev)
+    ours = clone_params(ref)
+    set_grads(ref, 0, 1e-3)
+    for p, q in zip(ref, ours):
+        q.grad = p.grad.clone()
+    topt = torch.optim.AdamW(ref, foreach=False, **HP)
+    oopt = mi_adamw.FusedAdamW(ours, **HP)
+    topt.step()
+    oopt.step()
+    torch.cuda.synchronize()
+    d = _same_state(ref, ours, topt, oopt)
+    print("config1 ulp (p, m, v):", d, flush=True)
+    assert max(d) == 0
+
+
+def test_config2_125m_clip_100_chained(dev):
+    import mi_adamw
+    from mi_adamw.workloads import GPT_125M
+    ref_a = gpt_params(GPT_125M, dev)
+    ref_b = clone_params(ref_a)
+    ours = clone_params(ref_a)
+    ta = torch.optim.AdamW(ref_a, foreach=False, **HP)
+    tb = torch.optim.AdamW(ref_b, foreach=False, **HP)
+    oo = mi_adamw.FusedAdamW(ours, max_grad_norm=1.0, **HP)
+    states = midtrain_state(ref_a, 1000.0)
+    for opt, ps in ((ta, ref_a), (tb, ref_b), (oo, ours)):
+        load_states(opt, ps, states)
+    del states
+    worst_norm = 0.0
+    for step in range(100):
+        set_grads(ref_a, step, 1e-2)
+        for p, q, r in zip(ref_a, ref_b, ours):
+            q.grad.copy_(p.grad) if q.grad is not None else setattr(q, "grad", p.grad.clone())
+            r.grad.copy_(p.grad) if r.grad is not None else setattr(r, "grad", p.grad.clone())
+        oo.step()
+        tn = torch.nn.utils.clip_grad_norm_(ref_a, 1.0)
+        ta.step()
+        torch.nn.utils.clip_grads_with_norm_(ref_b, 1.0, oo.last_grad_norm.clone())
+        tb.step()
+        worst_norm = max(worst_norm, rel_err(oo.last_grad_norm, tn))
+        if step % 20 == 19:
+            torch.cuda.synchronize()
+            print(f"step {1001 + step}: worst norm rel {worst_norm:.3g}", flush=True)
+    torch.cuda.synchronize()
+    assert worst_norm <= 1e-6
+    d = _same_state(ref_b, ours, tb, oo)
+    print("config2 ulp vs torch with the same norms (p, m, v):", d, flush=True)
+    assert max(d) == 0
+    # Elementwise |ours - torch| <= 1e-5 (|torch| + rms(torch tensor)): p, m and
+    # v pass through zero, and a difference of a few ulp picked up while a value
+    # was of typical size stays when it later gets close to zero.
+    wp = wm = wv = 0.0
+    for p, q in zip(ref_a, ours):
+        mr, vr = ta.state[p]["exp_avg"], ta.state[p]["exp_avg_sq"]
+        wp = max(wp, close_rel(q, p, 1e-5, 1e-5 * rms(p)))
+        wm = max(wm, close_rel(oo.state[q]["exp_avg"], mr, 1e-5, 1e-5 * rms(mr)))
+        wv = max(wv, close_rel(oo.state[q]["exp_avg_sq"], vr, 1e-5, 1e-5 * rms(vr)))
+    print(f"config2 vs torch clip_grad_norm_ path, worst |d|/tol: p {wp:.3g} m {wm:.3g} v {wv:.3g}",
+          flush=True)
+    assert max(wp, wm, wv) <= 1
+
+
+def test_config3_350m_master_clip_bf16_copy(dev):
+    import mi_adamw
+    from mi_adamw.workloads import GPT_350M
+    ref = gpt_params(GPT_350M, dev)
+    ours = clone_params(ref)
+    topt = torch.optim.AdamW(ref, foreach=False, **HP)
+    oopt = mi_adamw.FusedAdamW(ours, max_grad_norm=1.0, bf16_copy=True, **HP)
+    states = midtrain_state(ref, 1000.0)
+    load_states(topt, ref, states)
+    load_states(oopt, ours, states)
+    del states
+    set_grads(ref, 0, 1e-3)
+    for p, q in zip(ref, ours):
+        q.grad = p.grad.clone()
+    tn = torch.nn.utils.get_total_norm([p.grad for p in ref])
+    oopt.step()
+    torch.nn.utils.clip_grads_with_norm_(ref, 1.0, oopt.last_grad_norm.clone())
+    topt.step()
+    torch.cuda.synchronize()
+    print("config3 norm", tn.item(), oopt.last_grad_norm.item(), flush=True)
+    assert rel_err(oopt.last_grad_norm, tn) <= 1e-6
+    d = _same_state(ref, ours, topt, oopt)
+    print("config3 ulp (p, m, v):", d, flush=True)
+    assert max(d) == 0
+    for q in ours:
+        assert torch.equal(oopt.bf16_param(q), q.detach().to(torch.bfloat16))
+
+
+@pytest.mark.parametrize("clip", [False, True])
+def test_config4_1p3b_bf16_state(dev, clip):
+    import mi_adamw
+    from mi_adamw.workloads import GPT_1P3B
+    ref = gpt_params(GPT_1P3B, dev)
+    ours = clone_params(ref)
+    topt = torch.optim.AdamW(ref, foreach=False, **HP)
+    oopt = mi_adamw.FusedAdamW(ours, state_dtype=torch.bfloat16, bf16_copy=True,
+                               max_grad_norm=1.0 if clip else None, **HP)
+    states = midtrain_state(ref, 1000.0)
+    load_states(topt, ref, states)
+    load_states(oopt, ours, states)
+    sample = [0, 2, 3, 4, 98, len(ref) - 3, len(ref) - 1]
+    before = {i: (to_np(ref[i]).reshape(-1).copy(),
+                  O.to_bf16_bits(to_np(states[i]["exp_avg"]).reshape(-1)),
+                  O.to_bf16_bits(to_np(states[i]["exp_avg_sq"]).reshape(-1))) for i in sample}
+    m_old = [st["exp_avg"] for st in states]
+    del states
+    set_grads(ref, 0, 1e-3)
+    for p, q in zip(ref, ours):
+        q.grad = p.grad.clone()
+    p_before = [p.detach().clone() for p in ref]
+    oopt.step()
+    if clip:
+        torch.nn.utils.clip_grads_with_norm_(ref, 1.0, oopt.last_grad_norm.clone())
+    topt.step()
+    torch.cuda.synchronize()
+    coef = O.clip_coef(np.float32(oopt.last_grad_norm.item()), 1.0) if clip else None
+    # Bit-exact against the oracle's bf16-state model on sampled tensors.
+    for i in sample:
+        pn, mb, vb = before[i]
+        g = to_np(ours[i].grad).reshape(-1)
+        O.adamw_step_bf16state(pn, g, mb, vb, step=1001.0, grad_scale=coef, **HP)
+        q = ours[i]
+        assert O.max_ulp(pn, to_np(q).reshape(-1))[0] == 0
+        assert np.array_equal(mb, to_np(oopt.state[q]["exp_avg"].view(torch.int16)).view(np.uint16).reshape(-1))
+        assert np.array_equal(vb, to_np(oopt.state[q]["exp_avg_sq"].view(torch.int16)).view(np.uint16).reshape(-1))
+    # Against the fp32-state torch reference, bounds from bf16 rounding: bf16
+    # keeps 8 significant bits, so round-to-nearest-even is off by at most 2^-8
+    # relative.  The old moments were rounded when stored, the new ones are
+    # rounded on store:
+    #   m: |dm| <= (beta1 |m_old| + |m_new|) 2^-8
+    #   v: all terms positive, |dv| <= 2 * 2^-8 |v_new|
+    #   p: |dp| <= step_size (|dm| / d + |m| |dd| / d^2) + 2 ulp
+    #         <= lr (|m_old| + |m_new|) 2^-7 / d + |u| 2^-7 + 2 ulp, u = the update
+    worst_m = worst_v = worst_p = 0.0
+    wd_factor = float(np.float32(1 - HP["lr"] * HP["weight_decay"]))
+    inv_bc2 = float(np.float32(1.0 / (1 - 0.95 ** 1001) ** 0.5))
+    for p, q, pb, mo in zip(ref, ours, p_before, m_old):
+        mr = topt.state[p]["exp_avg"].double()
+        vr = topt.state[p]["exp_avg_sq"].double()
+        mq = oopt.state[q]["exp_avg"].double()
+        vq = oopt.state[q]["exp_avg_sq"].double()
+        mo = mo.double()
+        worst_m = max(worst_m, float(((mq - mr).abs() / ((0.9 * mo.abs() + mr.abs()) * 2 ** -8 + 1e-30)).max()))
+        worst_v = max(worst_v, float(((vq - vr).abs() / (vr * 2 ** -7 + 1e-30)).max()))
+        d = vr.sqrt() * inv_bc2 + 1e-8
+        u = (p.detach().double() - pb.double() * wd_factor).abs()
+        bound = (HP["lr"] * (mo.abs() + mr.abs()) * 2 ** -7 / d + u * 2 ** -7
+                 + 2 * p.detach().double().abs() * 2 ** -23 + 1e-30)
+        worst_p = max(worst_p, float(((q.detach().double() - p.detach().double()).abs() / bound).max()))
+        assert torch.equal(oopt.bf16_param(q), q.detach().to(torch.bfloat16))
+    print(f"config4 clip={clip}: worst/bound m {worst_m:.3g} v {worst_v:.3g} p {worst_p:.3g}",
+          flush=True)
+    assert worst_m <= 1 and worst_v <= 1 and worst_p <= 1
+
+
+def test_config5_6p7b_flat_clip_bf16_copy(dev):
+    import mi_adamw
+    from mi_adamw.workloads import GPT_6P7B
+    params = gpt_params(GPT_6P7B, dev)
+    sample = [0, 2, 4, 7, 250, len(params) - 3, len(params) - 1]
+    ref = [torch.nn.Parameter(params[i].detach().clone()) for i in sample]
+    opt = mi_adamw.FusedAdamW(params, max_grad_norm=1.0, bf16_copy=True, flat_buffer=True, **HP)
+    print("flat buffer elements", opt._flat.total, flush=True)
+    assert opt._flat.total == GPT_6P7B.numel()  # 128-byte alignment adds no padding here
+    for i, p in enumerate(params):
+        st = midtrain_state([p], 1000.0)[0]
+        st["exp_avg"] = st["exp_avg"]
+        opt.state[p]["step"] = st["step"]
+        m, v = opt._flat.state_views(p)
+        m.copy_(st["exp_avg"])
+        v.copy_(st["exp_avg_sq"])
+        opt.state[p]["exp_avg"], opt.state[p]["exp_avg_sq"] = m, v
+    tref = torch.optim.AdamW(ref, foreach=False, **HP)
+    load_states(tref, ref, [{"step": torch.tensor(1000.0),
+                             "exp_avg": opt.state[params[i]]["exp_avg"].clone(),
+                             "exp_avg_sq": opt.state[params[i]]["exp_avg_sq"].clone()} for i in sample])
+    set_grads(params, 0, 1e-3)   # writes into the flat gradient views
+    for j, i in enumerate(sample):
+        ref[j].grad = params[i].grad.clone()
+    tn = torch.nn.utils.get_total_norm([p.grad for p in params])
+    exact = float(sum(float((p.grad.double() ** 2).sum().item()) for p in params)) ** 0.5
+    opt.step()
+    torch.nn.utils.clip_grads_with_norm_(ref, 1.0, opt.last_grad_norm.clone())
+    tref.step()
+    torch.cuda.synchronize()
+    on = opt.last_grad_norm.item()
+    print(f"config5 norm ours={on:.9g} torch={tn.item():.9g} float64={exact:.12g}", flush=True)
+    assert abs(on - exact) <= 1e-7 * exact
+    assert rel_err(opt.last_grad_norm, tn) <= 1e-6
+    for j, i in enumerate(sample):
+        q, p = params[i], ref[j]
+        assert max_ulp(q, p) == 0
+        assert max_ulp(opt.state[q]["exp_avg"], tref.state[p]["exp_avg"]) == 0
+        assert max_ulp(opt.state[q]["exp_avg_sq"], tref.state[p]["exp_avg_sq"]) == 0
+        assert float(opt.state[q]["step"]) == 1001.0
+        assert torch.equal(opt.bf16_param(q), q.detach().to(torch.bfloat16))

@@ -1,0 +1,347 @@
+"""GPU parity: FusedAdamW / the C ABI against torch.optim.AdamW(foreach=False) and the oracle.
+
+Tolerances (fp32): parameters and moments within 2 ulp of torch after one
+step; relative error 1e-5 after chained steps; clip norm relative 1e-6.  The
+kernels follow torch-ROCm's op chain, so the observed distance is 0 ulp and
+the tests also assert bit-equality with the oracle's ROCm op model.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from _helpers import (clone_params, close_rel, gen, load_states, make_params, max_ulp,
+                      max_ulp_all, midtrain_state, rel_err, rms, set_grads, to_np)
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+# A miniature of the GPT layout: LayerNorm vectors, ragged matrices, sizes that
+# are not multiples of 4 (scalar tail) or of the chunk size (partial chunks).
+MINI_SHAPES = [(64, 48), (48,), (48,), (144, 48), (48, 48), (4099,), (3,), (1,), (7, 5),
+               (70001,), (1024,), (65536 + 12,)]
+
+
+@pytest.fixture(scope="module")
+def dev():
+    if not torch.cuda.is_available():
+        pytest.fail("GPU test run without a ROCm GPU")
+    import mi_adamw
+    print("mi_adamw", mi_adamw.version(), flush=True)
+    return torch.device("cuda", 0)
+
+
+def _pair(dev, shapes=MINI_SHAPES, **kw):
+    import mi_adamw
+    ref = make_params(shapes, dev)
+    ours = clone_params(ref)
+    hp = dict(lr=kw.pop("lr", 3e-4), betas=kw.pop("betas", (0.9, 0.95)), eps=kw.pop("eps", 1e-8),
+              weight_decay=kw.pop("weight_decay", 0.1), maximize=kw.pop("maximize", False))
+    topt = torch.optim.AdamW(ref, foreach=False, **hp)
+    oopt = mi_adamw.FusedAdamW(ours, **hp, **kw)
+    return ref, ours, topt, oopt
+
+
+def _assert_same(ref, ours, topt, oopt, max_allowed=0):
+    du = max_ulp_all([p for p in ref], [p for p in ours])
+    dm = max_ulp_all([topt.state[p]["exp_avg"] for p in ref], [oopt.state[p]["exp_avg"] for p in ours])
+    dv = max_ulp_all([topt.state[p]["exp_avg_sq"] for p in ref],
+                     [oopt.state[p]["exp_avg_sq"] for p in ours])
+    print(f"ulp p={du} m={dm} v={dv}", flush=True)
+    assert du <= max_allowed and dm <= max_allowed and dv <= max_allowed
+    for p, q in zip(ref, ours):
+        assert float(topt.state[p]["step"]) == float(oopt.state[q]["step"])
+
+
+@pytest.mark.parametrize("betas,lr,wd,maximize", [
+    ((0.9, 0.95), 3e-4, 0.1, False),     # BASELINE hyperparameters
+    ((0.9, 0.999), 6e-4, 0.1, False),    # mini-megatron's defaults (config.py:11,13)
+    ((0.9, 0.999), 6e-4, 0.0, False),    # no weight decay: first op is skipped
+    ((0.3, 0.95), 1e-3, 0.01, False),    # lerp weight 0.7: the other Lerp.h branch
+    ((0.9, 0.95), 3e-4, 0.1, True),      # maximize
+    ((0.9, 0.95), 0.0, 0.1, False),      # lr = 0, the reference's first step (main.py:39-40)
+])
+def test_chained_steps_match_torch_bitwise(dev, betas, lr, wd, maximize):
+    """Steps 1..10 from zero state: bias corrections change every step."""
+    ref, ours, topt, oopt = _pair(dev, betas=betas, lr=lr, weight_decay=wd, maximize=maximize)
+    for step in range(1, 11):
+        set_grads(ref, step, 1e-3)
+        for p, q in zip(ref, ours):
+            q.grad = p.grad.clone()
+        topt.step()
+        oopt.step()
+        torch.cuda.synchronize()
+        print(f"step {step}", flush=True)
+        _assert_same(ref, ours, topt, oopt, max_allowed=0)
+
+
+def test_kernel_matches_oracle_bitwise(dev):
+    """The HIP update equals the oracle's ROCm op model, element for element."""
+    import mi_adamw
+    shapes = [(1,), (3,), (5,), (1023,), (1025,), (4096,), (65537,)]
+    params = make_params(shapes, dev)
+    init = [to_np(p).copy() for p in params]
+    states = midtrain_state(params, step=7.0)
+    opt = mi_adamw.FusedAdamW(params, lr=6e-4, betas=(0.9, 0.999), eps=1e-8, weight_decay=0.1)
+    load_states(opt, params, states)
+    set_grads(params, 8, 1e-3)
+    grads = [to_np(p.grad).copy() for p in params]
+    opt.step()
+    torch.cuda.synchronize()
+    for i, p in enumerate(params):
+        pn, mn, vn = init[i].copy(), to_np(states[i]["exp_avg"]).copy(), to_np(states[i]["exp_avg_sq"]).copy()
+        O.adamw_step(pn, grads[i], mn, vn, lr=6e-4, betas=(0.9, 0.999), eps=1e-8,
+                     weight_decay=0.1, step=8.0, opmodel=O.OPMODEL_TORCH_ROCM)
+        assert O.max_ulp(pn.reshape(-1), to_np(p).reshape(-1))[0] == 0
+        assert O.max_ulp(mn.reshape(-1), to_np(opt.state[p]["exp_avg"]).reshape(-1))[0] == 0
+        assert O.max_ulp(vn.reshape(-1), to_np(opt.state[p]["exp_avg_sq"]).reshape(-1))[0] == 0
+
+
+def test_torch_rocm_matches_oracle_opmodel(dev):
+    """Pins the oracle's ROCm op model: torch's own GPU AdamW equals it bit for bit."""
+    n = 1 << 20
+    for betas, step in (((0.9, 0.95), 1), ((0.9, 0.999), 3), ((0.3, 0.95), 50), ((0.9, 0.95), 1000)):
+        p = torch.nn.Parameter(torch.randn(n, device=dev, generator=gen(dev, 1)) * 0.02)
+        st = midtrain_state([p], step=float(step - 1))[0]
+        p.grad = torch.randn(n, device=dev, generator=gen(dev, 2)) * 1e-3
+        pn, gn = to_np(p).copy(), to_np(p.grad).copy()
+        mn, vn = to_np(st["exp_avg"]).copy(), to_np(st["exp_avg_sq"]).copy()
+        opt = torch.optim.AdamW([p], lr=3e-4, betas=betas, eps=1e-8, weight_decay=0.1, foreach=False)
+        load_states(opt, [p], [st])
+        opt.step()
+        O.adamw_step(pn, gn, mn, vn, lr=3e-4, betas=betas, eps=1e-8, weight_decay=0.1,
+                     step=float(step), opmodel=O.OPMODEL_TORCH_ROCM)
+        assert O.max_ulp(pn, to_np(p))[0] == 0, (betas, step)
+        assert O.max_ulp(mn, to_np(opt.state[p]["exp_avg"]))[0] == 0, (betas, step)
+        assert O.max_ulp(vn, to_np(opt.state[p]["exp_avg_sq"]))[0] == 0, (betas, step)
+
+
+def test_clip_matches_torch(dev):
+    """Fused clip + AdamW, 5 chained mid-training steps, against two torch references.
+
+    A: torch.nn.utils.clip_grad_norm_ then AdamW(foreach=False) -- the norm may
+       differ by an ulp (torch sums fp32 per-tensor norms; the kernel sums
+       squares in float64), so p, m, v are compared elementwise with
+       |d| <= 1e-6 (|ref| + rms(ref)).
+    B: torch.nn.utils.clip_grads_with_norm_ with the kernel's norm, then AdamW --
+       the same coefficient, so everything must be bit-identical.
+    """
+    import mi_adamw
+    ref_a = make_params(MINI_SHAPES, dev)
+    ref_b = clone_params(ref_a)
+    ours = clone_params(ref_a)
+    hp = dict(lr=3e-4, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.1)
+    ta = torch.optim.AdamW(ref_a, foreach=False, **hp)
+    tb = torch.optim.AdamW(ref_b, foreach=False, **hp)
+    oo = mi_adamw.FusedAdamW(ours, max_grad_norm=1.0, **hp)
+    states = midtrain_state(ref_a, 1000.0)
+    for opt, ps in ((ta, ref_a), (tb, ref_b), (oo, ours)):
+        load_states(opt, ps, states)
+    for step in range(5):
+        set_grads(ref_a, step, 1e-2)
+        for p, q, r in zip(ref_a, ref_b, ours):
+            q.grad = p.grad.clone()
+            r.grad = p.grad.clone()
+        oo.step()
+        on = oo.last_grad_norm
+        tn = torch.nn.utils.clip_grad_norm_(ref_a, 1.0)
+        ta.step()
+        torch.nn.utils.clip_grads_with_norm_(ref_b, 1.0, on.clone())
+        tb.step()
+        torch.cuda.synchronize()
+        exact = O.total_norm([to_np(p.grad) for p in ours])
+        print(f"norm torch={tn.item():.9g} ours={on.item():.9g} float64={float(exact):.9g}",
+              flush=True)
+        assert rel_err(on, tn) <= 1e-6
+        assert on.item() == float(exact)
+        _assert_same(ref_b, ours, tb, oo, max_allowed=0)
+        for p, q in zip(ref_a, ours):
+            assert close_rel(q, p, 1e-6, 1e-6 * rms(p)) <= 1
+            for k in ("exp_avg", "exp_avg_sq"):
+                r = ta.state[p][k]
+                assert close_rel(oo.state[q][k], r, 1e-6, 1e-6 * rms(r)) <= 1
+
+
+def test_clip_grad_norm_dropin(dev):
+    import mi_adamw
+    ref = make_params(MINI_SHAPES, dev)
+    set_grads(ref, 3, 1e-2)
+    ours = clone_params(ref)
+    tn = torch.nn.utils.clip_grad_norm_(ref, 1.0)
+    on = mi_adamw.clip_grad_norm_(ours, 1.0)
+    assert rel_err(on, tn) <= 1e-6
+    exact = float(np.sqrt(sum(float((to_np(p.grad).astype(np.float64) ** 2).sum()) for p in ours)))
+    print("norm", tn.item(), on.item(), exact, flush=True)
+    assert max_ulp_all([p.grad for p in ref], [q.grad for q in ours]) <= 1
+
+
+def test_bf16_copy_and_state(dev):
+    import mi_adamw
+    params = make_params(MINI_SHAPES, dev)
+    ref = clone_params(params)
+    opt = mi_adamw.FusedAdamW(params, lr=3e-4, betas=(0.9, 0.95), weight_decay=0.1,
+                              state_dtype=torch.bfloat16, bf16_copy=True, max_grad_norm=1.0)
+    states = midtrain_state(params, 1000.0)
+    load_states(opt, params, states)
+    for p in params:
+        assert opt.state[p]["exp_avg"].dtype == torch.bfloat16
+    set_grads(params, 0, 1e-3)
+    grads = [to_np(p.grad).copy() for p in params]
+    opt.step()
+    torch.cuda.synchronize()
+    coef = float(opt.last_grad_norm.item())
+    coef = O.clip_coef(np.float32(coef), 1.0)
+    for i, p in enumerate(params):
+        pn = to_np(ref[i]).copy()
+        mb = O.to_bf16_bits(to_np(states[i]["exp_avg"]))
+        vb = O.to_bf16_bits(to_np(states[i]["exp_avg_sq"]))
+        O.adamw_step_bf16state(pn.reshape(-1), grads[i].reshape(-1), mb.reshape(-1), vb.reshape(-1),
+                               lr=3e-4, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.1,
+                               step=1001.0, grad_scale=coef)
+        assert O.max_ulp(pn, to_np(p))[0] == 0
+        got_m = to_np(opt.state[p]["exp_avg"].view(torch.int16)).view(np.uint16)
+        got_v = to_np(opt.state[p]["exp_avg_sq"].view(torch.int16)).view(np.uint16)
+        assert np.array_equal(got_m, mb) and np.array_equal(got_v, vb)
+        copy = opt.bf16_param(p)
+        assert torch.equal(copy, p.detach().to(torch.bfloat16))
+
+
+def test_flat_buffer_matches_per_tensor(dev):
+    """Flat-buffer mode (one contiguous range per group) against torch with the same norm.
+
+    Flat mode keeps gradients allocated, which is torch's zero_grad(set_to_none=False).
+    """
+    import mi_adamw
+    ref, ours, topt, oopt = _pair(dev, flat_buffer=True, max_grad_norm=1.0, bf16_copy=True)
+    states = midtrain_state(ref, 1000.0)
+    load_states(topt, ref, states)
+    load_states(oopt, ours, states)
+    for step in range(3):
+        oopt.zero_grad()
+        set_grads(ref, step, 1e-2)
+        for p, q in zip(ref, ours):
+            q.grad.copy_(p.grad)
+        oopt.step()
+        torch.nn.utils.clip_grads_with_norm_(ref, 1.0, oopt.last_grad_norm.clone())
+        topt.step()
+        torch.cuda.synchronize()
+        exact = O.total_norm([to_np(p.grad) for p in ours])
+        assert oopt.last_grad_norm.item() == float(exact)
+        _assert_same(ref, ours, topt, oopt, max_allowed=0)
+    for p in ours:
+        assert torch.equal(oopt.bf16_param(p), p.detach().to(torch.bfloat16))
+
+
+def test_state_dict_roundtrip_with_torch(dev):
+    """A FusedAdamW checkpoint loads into torch.optim.AdamW and back (checkpoint.py:9,19).
+
+    Both optimizers are built as main.py:177 builds its AdamW, with fused=False:
+    the saved param_groups carry that flag, which keeps torch on its
+    per-tensor path after loading (with fused=foreach=None torch would pick its
+    foreach path, whose rounding differs).
+    """
+    import mi_adamw
+    hp = dict(lr=3e-4, betas=(0.9, 0.95), weight_decay=0.1, fused=False)
+    ref = make_params(MINI_SHAPES, dev)
+    ours = clone_params(ref)
+    topt = torch.optim.AdamW(ref, **hp)
+    oopt = mi_adamw.FusedAdamW(ours, **hp)
+    for step in range(1, 4):
+        set_grads(ref, step, 1e-3)
+        for p, q in zip(ref, ours):
+            q.grad = p.grad.clone()
+        topt.step()
+        oopt.step()
+    _assert_same(ref, ours, topt, oopt)
+    sd = oopt.state_dict()
+    # Independent step tensors, torch's keys and layout.
+    steps = [st["step"] for st in sd["state"].values()]
+    assert len({id(s) for s in steps}) == len(steps)
+    assert all(s.device.type == "cpu" and s.dtype == torch.float32 for s in steps)
+    assert set(sd["param_groups"][0]) == set(topt.state_dict()["param_groups"][0])
+    assert set(sd["state"][0]) == set(topt.state_dict()["state"][0])
+    t2 = torch.optim.AdamW(clone_params(ours), **hp)
+    t2.load_state_dict(sd)
+    o2 = mi_adamw.FusedAdamW(clone_params(ref), **hp)
+    o2.load_state_dict(topt.state_dict())
+    p_t2 = t2.param_groups[0]["params"]
+    p_o2 = o2.param_groups[0]["params"]
+    for step in range(4, 6):
+        set_grads(p_t2, step, 1e-3)
+        for p, q in zip(p_t2, p_o2):
+            q.grad = p.grad.clone()
+        t2.step()
+        o2.step()
+    torch.cuda.synchronize()
+    _assert_same(p_t2, p_o2, t2, o2)
+    for p, q in zip(p_t2, p_o2):
+        assert float(t2.state[p]["step"]) == float(o2.state[q]["step"]) == 5.0
+
+
+def test_params_without_grad_are_skipped(dev):
+    ref, ours, topt, oopt = _pair(dev)
+    set_grads(ref, 1, 1e-3)
+    for p, q in zip(ref, ours):
+        q.grad = p.grad.clone()
+    for i in (1, 5):
+        ref[i].grad = None
+        ours[i].grad = None
+    topt.step()
+    oopt.step()
+    torch.cuda.synchronize()
+    assert len(oopt.state[ours[1]]) == 0
+    _assert_same([p for i, p in enumerate(ref) if i not in (1, 5)],
+                 [p for i, p in enumerate(ours) if i not in (1, 5)], topt, oopt)
+    # A later step with every grad: the skipped params start at step 1.
+    set_grads(ref, 2, 1e-3)
+    for p, q in zip(ref, ours):
+        q.grad = p.grad.clone()
+    topt.step()
+    oopt.step()
+    torch.cuda.synchronize()
+    _assert_same(ref, ours, topt, oopt)
+
+
+def test_nonfinite_grads_propagate_like_torch(dev):
+    ref, ours, topt, oopt = _pair(dev, max_grad_norm=1.0)
+    set_grads(ref, 1, 1e-3)
+    ref[3].grad[0, 0] = float("inf")
+    ref[5].grad[7] = float("nan")
+    for p, q in zip(ref, ours):
+        q.grad = p.grad.clone()
+    tn = torch.nn.utils.clip_grad_norm_(ref, 1.0)
+    topt.step()
+    oopt.step()
+    torch.cuda.synchronize()
+    assert torch.isnan(tn) == torch.isnan(oopt.last_grad_norm)
+    for p, q in zip(ref, ours):
+        assert torch.equal(torch.isnan(p), torch.isnan(q))
+
+
+def test_misaligned_views_take_scalar_path(dev):
+    """Params that are views at odd offsets (not 16-byte aligned) still match torch."""
+    import mi_adamw
+    base = torch.randn(10007, device=dev, generator=gen(dev, 5)) * 0.02
+    ref_views = [torch.nn.Parameter(base[1:4001].clone()), torch.nn.Parameter(base[3:1030].clone())]
+    store = torch.zeros(10007, device=dev)
+    ours = []
+    for off, p in ((1, ref_views[0]), (4003, ref_views[1])):
+        v = store[off:off + p.numel()]
+        v.copy_(p.detach())
+        q = torch.nn.Parameter(v)
+        ours.append(q)
+    topt = torch.optim.AdamW(ref_views, lr=3e-4, betas=(0.9, 0.95), weight_decay=0.1, foreach=False)
+    oopt = mi_adamw.FusedAdamW(ours, lr=3e-4, betas=(0.9, 0.95), weight_decay=0.1)
+    for step in range(1, 4):
+        set_grads(ref_views, step, 1e-3)
+        gstore = torch.zeros(10007, device=dev)
+        for (off, p), q in zip(((1, ref_views[0]), (4003, ref_views[1])), ours):
+            gv = gstore[off:off + p.numel()]
+            gv.copy_(p.grad)
+            q.grad = gv
+        topt.step()
+        oopt.step()
+    torch.cuda.synchronize()
+    assert ours[0].data_ptr() % 16 != 0
+    _assert_same(ref_views, ours, topt, oopt)

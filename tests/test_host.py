@@ -1,0 +1,231 @@
+"""CPU tests of the drop-in boundary: constructor, param_groups, state_dict, C ABI exports.
+
+No GPU work runs here.  The library is loaded (it links the HIP runtime but
+touches no device) to check that every symbol include/mi_adamw.h declares is
+exported and that the host-side chunk-table helper is right.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+
+import numpy as np
+import pytest
+import torch
+
+import mi_adamw
+from mi_adamw import _lib
+from mi_adamw.optimizer import _hyper
+from oracle import oracle as O
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "mi_adamw.h")
+
+
+def _params():
+    return [torch.nn.Parameter(torch.randn(10, 3)), torch.nn.Parameter(torch.randn(4))]
+
+
+def test_defaults_and_param_groups_match_torch():
+    ours = mi_adamw.FusedAdamW(_params(), lr=6e-4, weight_decay=0.1, fused=False)
+    ref = torch.optim.AdamW(_params(), lr=6e-4, weight_decay=0.1, fused=False)
+    assert ours.defaults == ref.defaults
+    assert ours.param_groups[0].keys() == ref.param_groups[0].keys()
+    for k in ref.param_groups[0]:
+        if k != "params":
+            assert ours.param_groups[0][k] == ref.param_groups[0][k]
+    assert ours.state_dict() == ref.state_dict()
+    assert mi_adamw.AdamW is mi_adamw.FusedAdamW
+    assert isinstance(ours, torch.optim.Optimizer)
+
+
+@pytest.mark.parametrize("kwargs", [
+    dict(lr=-1.0), dict(eps=-1e-8), dict(betas=(1.0, 0.999)), dict(betas=(0.9, -0.1)),
+    dict(weight_decay=-0.1), dict(betas=(0.9, torch.tensor(0.99))),
+    dict(lr=torch.tensor([1e-3, 2e-3])),
+    dict(lr=torch.tensor(1e-3), foreach=True),
+])
+def test_invalid_arguments_raise_like_torch(kwargs):
+    with pytest.raises((ValueError, RuntimeError)) as ref:
+        torch.optim.AdamW(_params(), **kwargs)
+    with pytest.raises(type(ref.value)) as ours:
+        mi_adamw.FusedAdamW(_params(), **kwargs)
+    assert str(ours.value) == str(ref.value)
+
+
+@pytest.mark.parametrize("kwargs", [dict(amsgrad=True), dict(capturable=True),
+                                    dict(differentiable=True)])
+def test_unsupported_flags_fail_loudly(kwargs):
+    with pytest.raises(NotImplementedError):
+        mi_adamw.FusedAdamW(_params(), **kwargs)
+
+
+def test_extra_options_are_validated():
+    with pytest.raises(ValueError):
+        mi_adamw.FusedAdamW(_params(), max_grad_norm=0.0)
+    with pytest.raises(ValueError):
+        mi_adamw.FusedAdamW(_params(), state_dtype=torch.float16)
+    with pytest.raises(ValueError):
+        mi_adamw.FusedAdamW(_params(), chunk_elems=1000)
+
+
+def test_step_on_cpu_params_raises_before_touching_state():
+    params = _params()
+    opt = mi_adamw.FusedAdamW(params)
+    for p in params:
+        p.grad = torch.randn_like(p)
+    with pytest.raises(RuntimeError, match="ROCm GPU"):
+        opt.step()
+    assert len(opt.state) == 0
+
+
+def test_step_without_grads_is_a_noop():
+    opt = mi_adamw.FusedAdamW(_params())
+    assert opt.step() is None
+    assert opt.step(lambda: 3.0) == 3.0
+    assert len(opt.state) == 0
+
+
+def test_sparse_grad_raises_like_torch():
+    p = torch.nn.Parameter(torch.randn(4, 3))
+    p.grad = torch.randn(4, 3).to_sparse()
+    with pytest.raises(RuntimeError, match="sparse"):
+        mi_adamw.FusedAdamW([p]).step()
+
+
+def test_add_param_group_and_zero_grad():
+    params = _params()
+    opt = mi_adamw.FusedAdamW(params, lr=1e-3)
+    opt.add_param_group({"params": [torch.nn.Parameter(torch.randn(5))], "lr": 2e-3})
+    assert len(opt.param_groups) == 2
+    assert opt.param_groups[1]["lr"] == 2e-3
+    assert opt.param_groups[1]["betas"] == (0.9, 0.999)
+    for g in opt.param_groups:
+        for p in g["params"]:
+            p.grad = torch.ones_like(p)
+    opt.zero_grad()
+    assert all(p.grad is None for g in opt.param_groups for p in g["params"])
+
+
+def test_load_torch_state_dict_on_cpu_keeps_torch_layout():
+    """A torch AdamW state dict (CPU) loads; steps live in the packed CPU buffer."""
+    ref_params = _params()
+    ref = torch.optim.AdamW(ref_params, lr=1e-3, fused=False)
+    for p in ref_params:
+        p.grad = torch.randn_like(p)
+    ref.step()
+    ref.step()
+    ours = mi_adamw.FusedAdamW([torch.nn.Parameter(p.detach().clone()) for p in ref_params],
+                               lr=1e-3, fused=False)
+    ours.load_state_dict(ref.state_dict())
+    sd = ours.state_dict()
+    for i, st in sd["state"].items():
+        assert float(st["step"]) == 2.0
+        assert st["step"].dtype == torch.float32 and st["step"].device.type == "cpu"
+        assert torch.equal(st["exp_avg"], ref.state[ref_params[i]]["exp_avg"])
+    # Steps of different params are independent tensors in the saved dict.
+    assert sd["state"][0]["step"] is not sd["state"][1]["step"]
+    sd["state"][0]["step"] += 1
+    assert float(sd["state"][1]["step"]) == 2.0
+
+
+def test_bf16_state_dict_loads_as_bf16():
+    ref_params = _params()
+    ref = torch.optim.AdamW(ref_params, lr=1e-3)
+    for p in ref_params:
+        p.grad = torch.randn_like(p)
+    ref.step()
+    ours = mi_adamw.FusedAdamW([torch.nn.Parameter(p.detach().clone()) for p in ref_params],
+                               lr=1e-3, state_dtype=torch.bfloat16)
+    ours.load_state_dict(ref.state_dict())
+    for p in ours.param_groups[0]["params"]:
+        assert ours.state[p]["exp_avg"].dtype == torch.bfloat16
+        assert ours.state[p]["exp_avg_sq"].dtype == torch.bfloat16
+
+
+@pytest.mark.parametrize("lr,betas,eps,wd,step,maximize", [
+    (3e-4, (0.9, 0.95), 1e-8, 0.1, 1.0, False),
+    (6e-4, (0.9, 0.999), 1e-8, 0.1, 7.0, False),
+    (1e-3, (0.3, 0.95), 1e-6, 0.0, 1000.0, True),
+    (0.0, (0.9, 0.999), 1e-8, 0.1, 2.0, False),
+    (3e-4, (0.9, 0.95), 1e-8, 0.1, 16777217.0, False),
+])
+def test_product_scalars_equal_oracle_scalars(lr, betas, eps, wd, step, maximize):
+    """The product's per-step fp32 scalars equal the oracle's (pinned by the golden tests)."""
+    group = dict(lr=lr, betas=betas, eps=eps, weight_decay=wd, maximize=maximize)
+    step = float(np.float32(step))
+    ours = _hyper(group, step)
+    ref = O.hyper_from_group(lr, betas[0], betas[1], eps, wd, step, maximize)
+    assert ours.wd_factor == ref.wd_factor
+    assert ours.lerp_w == ref.lerp_w
+    assert ours.beta2 == ref.beta2
+    assert ours.one_minus_beta2 == ref.one_minus_beta2
+    assert ours.inv_bc2_sqrt == float(np.float32(1.0 / ref.bc2_sqrt))
+    assert ours.eps == ref.eps
+    assert ours.neg_step_size == ref.neg_step_size
+    assert ours.grad_sign == ref.grad_sign
+
+
+def _header_functions():
+    text = open(HEADER).read()
+    return re.findall(r"^\s*(?:const\s+)?[a-z_0-9]+\s*\*?\s*(mi_adamw_[a-z_0-9]+)\s*\(", text, re.M)
+
+
+def test_library_exports_every_header_symbol():
+    lib = _lib.load()
+    names = _header_functions()
+    assert set(names) == set(_lib.EXPORTS)
+    for name in names:
+        assert hasattr(lib, name), name
+    assert _lib.version().startswith("mi_adamw 1 gfx950")
+
+
+def test_header_structs_match_bindings():
+    text = open(HEADER).read()
+    assert f"#define MI_ADAMW_ABI_VERSION {_lib.ABI_VERSION}" in text
+    assert f"#define MI_ADAMW_MAX_HYPER {_lib.MAX_HYPER}" in text
+    assert f"#define MI_ADAMW_MAX_NORM_BLOCKS {_lib.MAX_NORM_BLOCKS}" in text
+    assert ctypes.sizeof(_lib.TensorRow) == 56
+    assert ctypes.sizeof(_lib.Hyper) == 8 * 4
+
+
+def test_build_chunks_helper():
+    lib = _lib.load()
+    numels = np.array([0, 1, 65536, 65537, 3 * 65536 - 5], dtype=np.int64)
+    n = lib.mi_adamw_build_chunks(numels.ctypes.data, len(numels), 65536, None, 0)
+    assert n == 0 + 1 + 1 + 2 + 3
+    out = np.zeros(2 * n, dtype=np.int32)
+    assert lib.mi_adamw_build_chunks(numels.ctypes.data, len(numels), 65536, out.ctypes.data, n) == n
+    rows = out.reshape(-1, 2).tolist()
+    assert rows == [[1, 0], [2, 0], [3, 0], [3, 1], [4, 0], [4, 1], [4, 2]]
+    # Rejected: chunk size not a multiple of 1024, too small a buffer, negative sizes.
+    assert lib.mi_adamw_build_chunks(numels.ctypes.data, len(numels), 1000, None, 0) == _lib.E_INVALID
+    assert lib.mi_adamw_build_chunks(numels.ctypes.data, len(numels), 65536, out.ctypes.data,
+                                     n - 1) == _lib.E_INVALID
+    bad = np.array([-1], dtype=np.int64)
+    assert lib.mi_adamw_build_chunks(bad.ctypes.data, 1, 65536, None, 0) == _lib.E_INVALID
+
+
+def test_abi_rejects_bad_arguments_without_launching():
+    lib = _lib.load()
+    h = (_lib.Hyper * 1)()
+    # NULL tables, zero chunks, too many hyper sets, bad chunk size: all rejected on the host.
+    assert lib.mi_adamw_step(None, None, 1, 65536, h, 1, None, 0, 0, 0, None) == _lib.E_INVALID
+    assert lib.mi_adamw_step(1, 1, 1, 65536, h, 17, None, 0, 0, 0, None) == _lib.E_INVALID
+    assert lib.mi_adamw_step(1, 1, 1, 1000, h, 1, None, 0, 0, 0, None) == _lib.E_INVALID
+    assert lib.mi_adamw_step(1, 1, 0, 65536, h, 1, None, 0, 0, 0, None) == _lib.E_INVALID
+    assert lib.mi_adamw_step(1, 1, 1, 65536, h, 1, None, 7, 0, 0, None) == _lib.E_INVALID
+    assert lib.mi_adamw_step(1, 1, 1, 65536, h, 1, None, 0, _lib.F_CLIP, 0, None) == _lib.E_INVALID
+    assert lib.mi_adamw_step(1, 1, 1, 65536, h, 1, None, 0, 1 << 5, 0, None) == _lib.E_INVALID
+    assert lib.mi_adamw_grad_norm(1, 1, 0, 65536, 1.0, 1, 1, 1, 1, None) == _lib.E_INVALID
+    assert lib.mi_adamw_grad_norm_flat(None, 10, 65536, 1.0, 1, 1, 1, 1, None) == _lib.E_INVALID
+    assert lib.mi_adamw_scale_grads(1, 1, 1, 65536, None, None) == _lib.E_INVALID
+    row = _lib.TensorRow(param=16, grad=32, exp_avg=48, exp_avg_sq=64, param_copy=0, numel=10,
+                         hyper=0, flags=_lib.T_VEC)
+    # Flat entry: a bf16 copy requested without a copy pointer, and a misaligned pointer.
+    assert lib.mi_adamw_step_flat(ctypes.byref(row), h, None, 65536, 0, _lib.F_BF16_COPY, 0,
+                                  None) == _lib.E_INVALID
+    row.grad = 36
+    assert lib.mi_adamw_step_flat(ctypes.byref(row), h, None, 65536, 0, 0, 0, None) == _lib.E_ALIGN
+    assert "invalid" in _lib.strerror(_lib.E_INVALID)
