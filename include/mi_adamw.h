@@ -27,7 +27,7 @@
  * Numerics.  Each element follows the fp32 op chain of adam.py:419-547, with
  * one fp32 rounding per ATen op, in the contraction pattern torch-ROCm's kernels
  * use (lerp, addcmul and addcdiv as fused multiply-adds; division by the host
- * scalar bc2_sqrt as a multiply by its fp32 reciprocal).  The caller computes
+ * scalar bc2_sqrt as a multiply by its reciprocal rounded to fp32).  The caller computes
  * the per-step scalars on the host in float64 (adam.py:529-536) and passes them
  * rounded to fp32 in mi_adamw_hyper.
  */
@@ -85,8 +85,9 @@ typedef struct mi_adamw_hyper {
     float lerp_w;          /* 1 - beta1                                      (adam.py:457) */
     float beta2;           /* beta2                                          (adam.py:476) */
     float one_minus_beta2; /* 1 - beta2                                      (adam.py:476) */
-    float inv_bc2_sqrt;    /* 1.0f / (float)((1 - beta2**step) ** 0.5), an fp32 division
-                              (adam.py:536,545: tensor / host scalar)                        */
+    float inv_bc2_sqrt;    /* (float)(1.0 / (1 - beta2**step) ** 0.5): the reciprocal taken in
+                              float64, as torch-ROCm divides a tensor by a host scalar
+                              (adam.py:536,545)                                              */
     float eps;             /* eps                                            (adam.py:545) */
     float neg_step_size;   /* -(lr / (1 - beta1**step))                      (adam.py:534,547) */
     float grad_sign;       /* -1 with maximize=True, else 1                  (adam.py:397) */
@@ -105,22 +106,20 @@ const char *mi_adamw_strerror(int code);
 int64_t mi_adamw_build_chunks(const int64_t *numels, int32_t n_tensors, int64_t chunk_elems,
                               mi_adamw_chunk *out, int64_t cap);
 
-/* Global gradient L2 norm and clip coefficient (one launch).
+/* Global gradient L2 norm and clip coefficient (two launches: the float64
+ * sum-of-squares pass over a fixed grid, then a one-workgroup reduction).
  * Replaces clip_grad.py:50-117 (_get_total_norm, norm_type 2) and :165-169.
  *   d_norm  <- fp32(sqrt(sum of g*g over every grad)), summed in float64;
  *   d_coef  <- min(max_norm * (1 / (norm + 1e-6)), 1) in fp32 (NaN propagates).
- * `d_partials` holds MI_ADAMW_MAX_NORM_BLOCKS doubles; `d_counter` one uint32
- * that must be zero before the first call (each call leaves it zero).  The
+ * `d_partials` holds MI_ADAMW_MAX_NORM_BLOCKS doubles of scratch.  The
  * partial-sum assignment is fixed, so the result is bitwise reproducible. */
 int mi_adamw_grad_norm(const mi_adamw_tensor *d_tensors, const mi_adamw_chunk *d_chunks,
                        int64_t n_chunks, int64_t chunk_elems, float max_norm,
-                       double *d_partials, uint32_t *d_counter, float *d_norm, float *d_coef,
-                       void *stream);
+                       double *d_partials, float *d_norm, float *d_coef, void *stream);
 
 /* Same over one contiguous fp32 gradient range of n elements. */
 int mi_adamw_grad_norm_flat(const float *d_grad, int64_t n, int64_t chunk_elems, float max_norm,
-                            double *d_partials, uint32_t *d_counter, float *d_norm,
-                            float *d_coef, void *stream);
+                            double *d_partials, float *d_norm, float *d_coef, void *stream);
 
 /* Multiply every gradient of the tables by *d_coef in place.
  * Replaces clip_grad.py:170-183 (_clip_grads_with_norm_'s foreach mul). */

@@ -95,8 +95,8 @@ _SIGNATURES = {
     "mi_adamw_version": ([], ctypes.c_char_p),
     "mi_adamw_strerror": ([ctypes.c_int], ctypes.c_char_p),
     "mi_adamw_build_chunks": ([_vp, _i32, _i64, _vp, _i64], _i64),
-    "mi_adamw_grad_norm": ([_vp, _vp, _i64, _i64, _f32, _vp, _vp, _vp, _vp, _vp], ctypes.c_int),
-    "mi_adamw_grad_norm_flat": ([_vp, _i64, _i64, _f32, _vp, _vp, _vp, _vp, _vp], ctypes.c_int),
+    "mi_adamw_grad_norm": ([_vp, _vp, _i64, _i64, _f32, _vp, _vp, _vp, _vp], ctypes.c_int),
+    "mi_adamw_grad_norm_flat": ([_vp, _i64, _i64, _f32, _vp, _vp, _vp, _vp], ctypes.c_int),
     "mi_adamw_scale_grads": ([_vp, _vp, _i64, _i64, _vp, _vp], ctypes.c_int),
     "mi_adamw_step": ([_vp, _vp, _i64, _i64, _vp, _i32, _vp, _i32, _i32, _i32, _vp], ctypes.c_int),
     "mi_adamw_step_flat": ([_vp, _vp, _vp, _i64, _i32, _i32, _i32, _vp], ctypes.c_int),

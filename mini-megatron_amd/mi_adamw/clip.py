@@ -17,7 +17,7 @@ import torch
 
 from . import _lib
 
-_CHUNK = 65536
+_CHUNK = 4096
 _workspace: dict[torch.device, tuple] = {}
 _cache: dict[tuple, tuple] = {}
 
@@ -27,7 +27,6 @@ def _ws(device):
     if ws is None:
         ws = _workspace[device] = (
             torch.zeros(_lib.MAX_NORM_BLOCKS, dtype=torch.float64, device=device),
-            torch.zeros(1, dtype=torch.int32, device=device),
             torch.zeros(1, dtype=torch.float32, device=device),
         )
     return ws
@@ -45,7 +44,7 @@ def _tables(grads, device):
         n = g.numel() * (2 if torch.is_complex(g) else 1)
         rows[i] = (ptr, ptr, 0, 0, 0, n, 0, _lib.T_VEC if ptr % 16 == 0 else 0)
     rows = rows[rows["numel"] > 0]
-    launch = _Launch(rows, _CHUNK, device)
+    launch = _Launch(rows, _CHUNK, device, tables=True)
     if len(_cache) > 8:
         _cache.clear()
     _cache[key] = launch
@@ -71,7 +70,7 @@ def clip_grad_norm_(parameters, max_norm: float, norm_type: float = 2.0,
             raise NotImplementedError("mi_adamw.clip_grad_norm_ supports dense contiguous fp32 "
                                       "gradients only")
     lib = _lib.load()
-    partials, counter, coef = _ws(device)
+    partials, coef = _ws(device)
     norm = torch.empty((), dtype=torch.float32, device=device)
     with torch.cuda.device(device):
         launch = _tables(grads, device)
@@ -81,7 +80,7 @@ def clip_grad_norm_(parameters, max_norm: float, norm_type: float = 2.0,
             return norm
         _lib.check(lib.mi_adamw_grad_norm(
             launch.rows.data_ptr(), launch.chunks.data_ptr(), launch.n_chunks, _CHUNK,
-            float(max_norm), partials.data_ptr(), counter.data_ptr(), norm.data_ptr(),
+            float(max_norm), partials.data_ptr(), norm.data_ptr(),
             coef.data_ptr(), stream), "mi_adamw_grad_norm")
         if error_if_nonfinite and bool(torch.logical_or(norm.isnan(), norm.isinf())):
             raise RuntimeError(

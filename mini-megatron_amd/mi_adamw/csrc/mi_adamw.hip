@@ -2,10 +2,11 @@
 //
 // Kernels (all HBM-streaming, no MFMA: the step is ~15 fp32 ops per 22-34 bytes):
 //   mi_adamw_sumsq_kernel  pass 1 of the clip: float64 sum of g*g over every
-//                          gradient, reduced wave (DPP/shuffle) -> LDS -> one
-//                          partial per workgroup; the last workgroup to finish
-//                          reduces the partials in a fixed order and writes the
-//                          norm and the clip coefficient (no host sync).
+//                          gradient, reduced wave (shuffle) -> LDS -> one
+//                          partial per workgroup;
+//   mi_adamw_norm_finalize_kernel  one workgroup reduces the partials in a fixed
+//                          order and writes the norm and the clip coefficient
+//                          to device memory (no host sync).
 //   mi_adamw_update_kernel pass 2: p, g, m, v streamed with dwordx4 loads and
 //                          stores, the AdamW op chain in fp32 registers, optional
 //                          bf16 moments, bf16 model copy and gradient write-back.
@@ -32,7 +33,6 @@ namespace {
 constexpr int kThreads = 256;            // 4 wave64 per workgroup
 constexpr int kVec = 4;                  // fp32 elements per lane per access
 constexpr int kTile = kThreads * kVec;   // elements one workgroup covers per access
-constexpr int kUnroll = 2;               // tiles in flight per lane
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
@@ -234,83 +234,129 @@ __device__ __forceinline__ double block_sum(double x) {
 
 // ---------------------------------------------------------------------------
 // Pass 1: float64 sum of squares and the clip coefficient.
+//
+// A fixed grid of at most kNormBlocks workgroups strides over the chunks:
+// workgroup b sums chunks b, b + grid, b + 2*grid, ...  Small chunks (4096
+// elements by default) keep every workgroup's share within one chunk of the
+// others, and the fixed assignment makes the sum bitwise reproducible.  The
+// next chunk's table entry is fetched before the current chunk's loads are
+// consumed, so the scalar-load latency of the lookup overlaps the stream.
+
+__device__ __forceinline__ void sumsq4(f32x4 a, double& acc0, double& acc1) {
+    acc0 += (double)a.x * a.x + (double)a.y * a.y;
+    acc1 += (double)a.z * a.z + (double)a.w * a.w;
+}
 
 template <class Src>
 __global__ __launch_bounds__(kThreads) void mi_adamw_sumsq_kernel(
-    Src src, int64_t n_chunks, int64_t chunk_elems, float max_norm, double* __restrict__ partials,
-    uint32_t* __restrict__ counter, float* __restrict__ norm_out, float* __restrict__ coef_out) {
+    Src src, int64_t n_chunks, int64_t chunk_elems, double* __restrict__ partials) {
     double acc0 = 0.0, acc1 = 0.0;
-    for (int64_t c = blockIdx.x; c < n_chunks; c += gridDim.x) {
-        mi_adamw_tensor t;
-        int64_t begin, end;
-        src.get(c, chunk_elems, t, begin, end);
+    int64_t c = blockIdx.x;
+    mi_adamw_tensor t;
+    int64_t begin = 0, end = 0;
+    if (c < n_chunks) src.get(c, chunk_elems, t, begin, end);
+    for (; c < n_chunks; c += gridDim.x) {
         const float* __restrict__ g = t.grad;
-        if (t.flags & MI_ADAMW_T_VEC) {
-            const int64_t vend = begin + ((end - begin) & ~static_cast<int64_t>(kVec - 1));
-            int64_t i = begin + threadIdx.x * kVec;
-            for (; i + kTile < vend; i += 2 * kTile) {
-                f32x4 a = ld4(g + i), b = ld4(g + i + kTile);
-                acc0 += (double)a.x * a.x + (double)a.y * a.y;
-                acc1 += (double)a.z * a.z + (double)a.w * a.w;
-                acc0 += (double)b.x * b.x + (double)b.y * b.y;
-                acc1 += (double)b.z * b.z + (double)b.w * b.w;
-            }
-            for (; i < vend; i += kTile) {
-                f32x4 a = ld4(g + i);
-                acc0 += (double)a.x * a.x + (double)a.y * a.y;
-                acc1 += (double)a.z * a.z + (double)a.w * a.w;
-            }
-            for (int64_t j = vend + threadIdx.x; j < end; j += kThreads) {
-                double x = ld1(g + j);
-                acc0 += x * x;
-            }
-        } else {
-            for (int64_t j = begin + threadIdx.x; j < end; j += kThreads) {
-                double x = ld1(g + j);
-                acc0 += x * x;
+        const bool vec = t.flags & MI_ADAMW_T_VEC;
+        const int64_t vend = vec ? begin + ((end - begin) & ~static_cast<int64_t>(kVec - 1)) : begin;
+        int64_t i = begin + threadIdx.x * kVec;
+        // Issue the first four tiles of this chunk (a whole 4096-element chunk)...
+        f32x4 a{}, b{}, d{}, e{};
+        const bool full = i + 3 * kTile < vend;
+        if (full) {
+            a = ld4(g + i);
+            b = ld4(g + i + kTile);
+            d = ld4(g + i + 2 * kTile);
+            e = ld4(g + i + 3 * kTile);
+        }
+        // ...then look up the next chunk while those loads are in flight; the
+        // barrier keeps the scheduler from hoisting the lookup (and its waits)
+        // above the vector loads.
+        __builtin_amdgcn_sched_barrier(0);
+        mi_adamw_tensor tn;
+        int64_t bn = 0, en = 0;
+        const bool more = c + gridDim.x < n_chunks;
+        if (more) src.get(c + gridDim.x, chunk_elems, tn, bn, en);
+        __builtin_amdgcn_sched_barrier(0);
+        if (full) {
+            sumsq4(a, acc0, acc1);
+            sumsq4(b, acc0, acc1);
+            sumsq4(d, acc0, acc1);
+            sumsq4(e, acc0, acc1);
+            i += 4 * kTile;
+            for (; i + 3 * kTile < vend; i += 4 * kTile) {
+                a = ld4(g + i);
+                b = ld4(g + i + kTile);
+                d = ld4(g + i + 2 * kTile);
+                e = ld4(g + i + 3 * kTile);
+                sumsq4(a, acc0, acc1);
+                sumsq4(b, acc0, acc1);
+                sumsq4(d, acc0, acc1);
+                sumsq4(e, acc0, acc1);
             }
         }
+        for (; i < vend; i += kTile) sumsq4(ld4(g + i), acc0, acc1);
+        for (int64_t j = vend + threadIdx.x; j < end; j += kThreads) {
+            double x = ld1(g + j);
+            acc0 += x * x;
+        }
+        if (more) {
+            t = tn;
+            begin = bn;
+            end = en;
+        }
     }
-    double total = block_sum(acc0 + acc1);
+    const double total = block_sum(acc0 + acc1);
+    if (threadIdx.x == 0) partials[blockIdx.x] = total;
+}
 
-    __shared__ bool is_last;
-    if (threadIdx.x == 0) {
-        __hip_atomic_store(&partials[blockIdx.x], total, __ATOMIC_RELAXED,
-                           __HIP_MEMORY_SCOPE_AGENT);
-        __threadfence();  // release this partial before the count
-        uint32_t prev = atomicAdd(counter, 1u);
-        is_last = (prev == gridDim.x - 1);
-    }
-    __syncthreads();
-    if (!is_last) return;
-
-    // Last workgroup: every partial is visible (acquire), reduce them in a
-    // fixed order so the result does not depend on which workgroup ran last.
-    __threadfence();
+// One workgroup: reduce the partial sums in a fixed order, then the norm and
+// the clip coefficient.  Running as its own launch, it sees every partial
+// through the kernel boundary; no fence or completion counter is needed.
+__global__ __launch_bounds__(kThreads) void mi_adamw_norm_finalize_kernel(
+    const double* __restrict__ partials, int n_partials, float max_norm,
+    float* __restrict__ norm_out, float* __restrict__ coef_out) {
     double s = 0.0;
-    for (uint32_t i = threadIdx.x; i < gridDim.x; i += kThreads)
-        s += __hip_atomic_load(&partials[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    for (int i = threadIdx.x; i < n_partials; i += kThreads) s += partials[i];
     s = block_sum(s);
     if (threadIdx.x == 0) {
         const float norm = static_cast<float>(__builtin_sqrt(s));
         // clip_grad.py:165-169: t = norm + 1e-6; coef = max_norm * (1/t); clamp(max=1)
-        const float t = norm + 1e-6f;
-        const float r = 1.0f / t;
+        const float tt = norm + 1e-6f;
+        const float r = 1.0f / tt;
         const float coef = r * max_norm;
         *norm_out = norm;
         *coef_out = coef > 1.0f ? 1.0f : coef;  // NaN stays NaN, as torch.clamp
-        __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
 }
 
 // ---------------------------------------------------------------------------
 // Pass 2: the AdamW update.
+//
+// One chunk per workgroup (grid = number of chunks): the hardware dispatcher
+// hands the next chunk to whichever CU frees a slot, which balances ragged
+// tensors.  Within a chunk the tiles are software-pipelined: the loads of tile
+// k+1 are issued before tile k is computed and stored, so each lane keeps a
+// tile of reads in flight while its stores drain.
+
+template <typename StateT, bool kClip, bool kWriteGrad>
+struct Tile {
+    f32x4 p, g, m, v;
+    __device__ __forceinline__ void load(const float* P, const float* G, const void* M,
+                                         const void* V, int64_t k) {
+        g = ld4(G + k);
+        p = ld4(P + k);
+        m = StateIO<StateT>::ld(M, k);
+        v = StateIO<StateT>::ld(V, k);
+    }
+};
 
 template <class Src, typename StateT, bool kClip, bool kCopy, bool kWriteGrad>
 __global__ __launch_bounds__(kThreads) void mi_adamw_update_kernel(
     Src src, int64_t n_chunks, int64_t chunk_elems, HyperPack hp,
     const float* __restrict__ grad_scale) {
     using IO = StateIO<StateT>;
+    using T = Tile<StateT, kClip, kWriteGrad>;
     const float scale = kClip ? *grad_scale : 1.0f;
     for (int64_t c = blockIdx.x; c < n_chunks; c += gridDim.x) {
         mi_adamw_tensor t;
@@ -328,41 +374,27 @@ __global__ __launch_bounds__(kThreads) void mi_adamw_update_kernel(
         if (t.flags & MI_ADAMW_T_VEC) {
             vend = begin + ((end - begin) & ~static_cast<int64_t>(kVec - 1));
             int64_t i = begin + threadIdx.x * kVec;
-            for (; i + (kUnroll - 1) * kTile < vend; i += kUnroll * kTile) {
-                f32x4 p[kUnroll], g[kUnroll], m[kUnroll], v[kUnroll];
-#pragma unroll
-                for (int u = 0; u < kUnroll; ++u) {
-                    const int64_t k = i + u * kTile;
-                    g[u] = ld4(G + k);
-                    p[u] = ld4(P + k);
-                    m[u] = IO::ld(M, k);
-                    v[u] = IO::ld(V, k);
-                }
-#pragma unroll
-                for (int u = 0; u < kUnroll; ++u) {
-                    const int64_t k = i + u * kTile;
-                    f32x4 gs = g[u];
+            if (i < vend) {
+                T cur;
+                cur.load(P, G, M, V, i);
+                while (true) {
+                    const int64_t j = i + kTile;
+                    const bool more = j < vend;
+                    T nxt = cur;
+                    if (more) nxt.load(P, G, M, V, j);
+                    f32x4 gs = cur.g;
                     if (kClip) gs = f32x4{gs.x * scale, gs.y * scale, gs.z * scale, gs.w * scale};
-                    if (kWriteGrad) st4(G + k, gs);
+                    if (kWriteGrad) st4(G + i, gs);
                     gs = f32x4{gs.x * gmul, gs.y * gmul, gs.z * gmul, gs.w * gmul};
-                    adamw_vec(p[u], gs, m[u], v[u], h);
-                    st4(P + k, p[u]);
-                    IO::st(M, k, m[u]);
-                    IO::st(V, k, v[u]);
-                    if (kCopy) st4_bf16(C + k, p[u]);
+                    adamw_vec(cur.p, gs, cur.m, cur.v, h);
+                    st4(P + i, cur.p);
+                    IO::st(M, i, cur.m);
+                    IO::st(V, i, cur.v);
+                    if (kCopy) st4_bf16(C + i, cur.p);
+                    if (!more) break;
+                    cur = nxt;
+                    i = j;
                 }
-            }
-            for (; i < vend; i += kTile) {
-                f32x4 g1 = ld4(G + i), p1 = ld4(P + i);
-                f32x4 m1 = IO::ld(M, i), v1 = IO::ld(V, i);
-                if (kClip) g1 = f32x4{g1.x * scale, g1.y * scale, g1.z * scale, g1.w * scale};
-                if (kWriteGrad) st4(G + i, g1);
-                g1 = f32x4{g1.x * gmul, g1.y * gmul, g1.z * gmul, g1.w * gmul};
-                adamw_vec(p1, g1, m1, v1, h);
-                st4(P + i, p1);
-                IO::st(M, i, m1);
-                IO::st(V, i, v1);
-                if (kCopy) st4_bf16(C + i, p1);
             }
         }
         // Scalar path: the ragged tail of a vector tensor, or a whole tensor
@@ -408,7 +440,7 @@ __global__ __launch_bounds__(kThreads) void mi_adamw_scale_kernel(
 // ---------------------------------------------------------------------------
 // Host side
 
-constexpr int kNormBlocks = 2048;   // partial sums of the norm pass (<= MAX_NORM_BLOCKS)
+constexpr int kNormBlocks = 1024;   // workgroups (and partial sums) of the norm pass
 
 bool chunk_elems_ok(int64_t chunk_elems) {
     return chunk_elems > 0 && (chunk_elems % kTile) == 0 && chunk_elems <= (int64_t(1) << 30);
@@ -430,12 +462,16 @@ bool aligned(const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p
 
 template <class Src>
 int launch_norm(const Src& src, int64_t n_chunks, int64_t chunk_elems, float max_norm,
-                double* partials, uint32_t* counter, float* norm, float* coef, hipStream_t s) {
-    if (n_chunks <= 0 || !chunk_elems_ok(chunk_elems) || !partials || !counter || !norm || !coef)
+                double* partials, float* norm, float* coef, hipStream_t s) {
+    if (n_chunks <= 0 || !chunk_elems_ok(chunk_elems) || !partials || !norm || !coef)
         return MI_ADAMW_E_INVALID;
-    unsigned grid = grid_for(n_chunks, kNormBlocks);
+    const unsigned grid = grid_for(n_chunks, kNormBlocks);
     hipLaunchKernelGGL(mi_adamw_sumsq_kernel<Src>, dim3(grid), dim3(kThreads), 0, s, src,
-                       n_chunks, chunk_elems, max_norm, partials, counter, norm, coef);
+                       n_chunks, chunk_elems, partials);
+    int rc = launch_status();
+    if (rc != MI_ADAMW_OK) return rc;
+    hipLaunchKernelGGL(mi_adamw_norm_finalize_kernel, dim3(1), dim3(kThreads), 0, s, partials,
+                       static_cast<int>(grid), max_norm, norm, coef);
     return launch_status();
 }
 
@@ -537,16 +573,15 @@ int64_t mi_adamw_build_chunks(const int64_t* numels, int32_t n_tensors, int64_t 
 
 int mi_adamw_grad_norm(const mi_adamw_tensor* d_tensors, const mi_adamw_chunk* d_chunks,
                        int64_t n_chunks, int64_t chunk_elems, float max_norm, double* d_partials,
-                       uint32_t* d_counter, float* d_norm, float* d_coef, void* stream) {
+                       float* d_norm, float* d_coef, void* stream) {
     if (!d_tensors || !d_chunks) return MI_ADAMW_E_INVALID;
     TableSource src{d_tensors, d_chunks};
-    return launch_norm(src, n_chunks, chunk_elems, max_norm, d_partials, d_counter, d_norm,
-                       d_coef, static_cast<hipStream_t>(stream));
+    return launch_norm(src, n_chunks, chunk_elems, max_norm, d_partials, d_norm, d_coef,
+                       static_cast<hipStream_t>(stream));
 }
 
 int mi_adamw_grad_norm_flat(const float* d_grad, int64_t n, int64_t chunk_elems, float max_norm,
-                            double* d_partials, uint32_t* d_counter, float* d_norm, float* d_coef,
-                            void* stream) {
+                            double* d_partials, float* d_norm, float* d_coef, void* stream) {
     if (!d_grad || n <= 0 || !chunk_elems_ok(chunk_elems)) return MI_ADAMW_E_INVALID;
     FlatSource src;
     memset(&src.t, 0, sizeof(src.t));
@@ -554,7 +589,7 @@ int mi_adamw_grad_norm_flat(const float* d_grad, int64_t n, int64_t chunk_elems,
     src.t.numel = n;
     src.t.flags = aligned(d_grad, 16) ? MI_ADAMW_T_VEC : 0;
     const int64_t n_chunks = (n + chunk_elems - 1) / chunk_elems;
-    return launch_norm(src, n_chunks, chunk_elems, max_norm, d_partials, d_counter, d_norm, d_coef,
+    return launch_norm(src, n_chunks, chunk_elems, max_norm, d_partials, d_norm, d_coef,
                        static_cast<hipStream_t>(stream));
 }
 

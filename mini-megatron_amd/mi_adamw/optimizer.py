@@ -26,7 +26,8 @@ host in float64 exactly as adam.py:414-536 computes them.
 """
 from __future__ import annotations
 
-from typing import Any, Iterable
+import ctypes
+from typing import Any
 
 import numpy as np
 import torch
@@ -35,7 +36,7 @@ from torch.optim import Optimizer
 from . import _lib
 from .flat import FlatLayout
 
-DEFAULT_CHUNK_ELEMS = 65536
+DEFAULT_CHUNK_ELEMS = 4096
 
 _ROW_DTYPE = np.dtype([
     ("param", "<u8"), ("grad", "<u8"), ("exp_avg", "<u8"), ("exp_avg_sq", "<u8"),
@@ -87,10 +88,19 @@ def _ptr(t: torch.Tensor | None) -> int:
 class _Launch:
     """Device-resident tensor and chunk tables for one kernel launch."""
 
-    __slots__ = ("rows", "chunks", "n_chunks", "n_rows")
+    __slots__ = ("rows", "chunks", "n_chunks", "n_rows", "host_rows")
 
-    def __init__(self, rows: np.ndarray, chunk_elems: int, device: torch.device):
+    def __init__(self, rows: np.ndarray, chunk_elems: int, device: torch.device,
+                 tables: bool = False):
         lib = _lib.load()
+        self.n_rows = len(rows)
+        self.host_rows = rows.copy()
+        if len(rows) == 1 and not tables:
+            # One contiguous range: launched through the flat entry points,
+            # which derive chunk bounds arithmetically and need no tables.
+            self.n_chunks = -(-int(rows["numel"][0]) // chunk_elems)
+            self.rows = self.chunks = None
+            return
         numels = np.ascontiguousarray(rows["numel"], dtype=np.int64)
         n = lib.mi_adamw_build_chunks(numels.ctypes.data, len(numels), chunk_elems, None, 0)
         _lib.check(int(n) if n < 0 else 0, "mi_adamw_build_chunks")
@@ -100,7 +110,6 @@ class _Launch:
         if n2 != n:
             raise _lib.MiAdamwError("mi_adamw_build_chunks: inconsistent chunk count")
         self.n_chunks = int(n)
-        self.n_rows = len(rows)
         self.rows = torch.from_numpy(rows.view(np.uint8).copy()).to(device)
         self.chunks = torch.from_numpy(chunks.view(np.uint8)).to(device)
 
@@ -297,6 +306,21 @@ class FusedAdamW(Optimizer):
             return self._flat.copy_view(p)
         return self._copies[id(p)]
 
+    @torch.no_grad()
+    def set_state(self, p: torch.Tensor, step: float, exp_avg: torch.Tensor,
+                  exp_avg_sq: torch.Tensor) -> None:
+        """Install one parameter's state in place (like load_state_dict for one
+        entry, without materialising a whole state dict): the step count and
+        the moments, copied into this optimizer's own storage and dtype."""
+        slot = self._slots[id(p)]
+        st = self.state[p]
+        if "exp_avg" not in st:
+            self._init_state(p, st)
+        self._steps[slot] = float(step)
+        st["step"] = self._step_views[slot]
+        st["exp_avg"].copy_(exp_avg)
+        st["exp_avg_sq"].copy_(exp_avg_sq)
+
     def state_dict(self) -> dict[str, Any]:
         sd = super().state_dict()
         # The packed step buffer is an implementation detail: hand out
@@ -445,9 +469,8 @@ class FusedAdamW(Optimizer):
         ws = self._workspace.get(device)
         if ws is None:
             partials = torch.zeros(_lib.MAX_NORM_BLOCKS, dtype=torch.float64, device=device)
-            counter = torch.zeros(1, dtype=torch.int32, device=device)
             coef = torch.zeros(1, dtype=torch.float32, device=device)
-            ws = self._workspace[device] = (partials, counter, coef)
+            ws = self._workspace[device] = (partials, coef)
         return ws
 
     def _rows(self, entries, hyper_idx) -> np.ndarray:
@@ -501,10 +524,18 @@ class FusedAdamW(Optimizer):
                     st["exp_avg_sq"].data_ptr(), h)
         return sig
 
+    @staticmethod
+    def _row_struct(launch: _Launch) -> _lib.TensorRow:
+        r = launch.host_rows[0]
+        return _lib.TensorRow(param=int(r["param"]), grad=int(r["grad"]),
+                              exp_avg=int(r["exp_avg"]), exp_avg_sq=int(r["exp_avg_sq"]),
+                              param_copy=int(r["param_copy"]), numel=int(r["numel"]),
+                              hyper=0, flags=int(r["flags"]))
+
     def _launch(self, entries, hyper_idx, hypers, device) -> None:
         lib = _lib.load()
         stream = torch.cuda.current_stream(device).cuda_stream
-        partials, counter, coef = self._ws(device)
+        partials, coef = self._ws(device)
         flags = 0
         if self.bf16_copy:
             flags |= _lib.F_BF16_COPY
@@ -540,11 +571,17 @@ class FusedAdamW(Optimizer):
             ev[0].record()
         if self.max_grad_norm is not None:
             norm = torch.empty((), dtype=torch.float32, device=device)
-            if norm_launch.n_chunks > 0:
+            if norm_launch.n_rows == 1:
+                row = self._row_struct(norm_launch)
+                _lib.check(lib.mi_adamw_grad_norm_flat(
+                    row.grad, row.numel, self.chunk_elems, float(self.max_grad_norm),
+                    partials.data_ptr(), norm.data_ptr(), coef.data_ptr(),
+                    stream), "mi_adamw_grad_norm_flat")
+            elif norm_launch.n_chunks > 0:
                 _lib.check(lib.mi_adamw_grad_norm(
                     norm_launch.rows.data_ptr(), norm_launch.chunks.data_ptr(),
                     norm_launch.n_chunks, self.chunk_elems, float(self.max_grad_norm),
-                    partials.data_ptr(), counter.data_ptr(), norm.data_ptr(), coef.data_ptr(),
+                    partials.data_ptr(), norm.data_ptr(), coef.data_ptr(),
                     stream), "mi_adamw_grad_norm")
             else:
                 norm.zero_()
@@ -559,6 +596,13 @@ class FusedAdamW(Optimizer):
             if launch.n_chunks == 0:
                 continue
             harr = (_lib.Hyper * len(hs))(*hs)
+            if launch.n_rows == 1:
+                row = self._row_struct(launch)
+                row_h = hs[int(launch.host_rows[0]["hyper"])]
+                _lib.check(lib.mi_adamw_step_flat(
+                    ctypes.byref(row), ctypes.byref(row_h), coef.data_ptr(), self.chunk_elems,
+                    state_code, flags, self.max_blocks, stream), "mi_adamw_step_flat")
+                continue
             _lib.check(lib.mi_adamw_step(
                 launch.rows.data_ptr(), launch.chunks.data_ptr(), launch.n_chunks,
                 self.chunk_elems, harr, len(hs), coef.data_ptr(), state_code, flags,

@@ -218,8 +218,8 @@ def test_abi_rejects_bad_arguments_without_launching():
     assert lib.mi_adamw_step(1, 1, 1, 65536, h, 1, None, 7, 0, 0, None) == _lib.E_INVALID
     assert lib.mi_adamw_step(1, 1, 1, 65536, h, 1, None, 0, _lib.F_CLIP, 0, None) == _lib.E_INVALID
     assert lib.mi_adamw_step(1, 1, 1, 65536, h, 1, None, 0, 1 << 5, 0, None) == _lib.E_INVALID
-    assert lib.mi_adamw_grad_norm(1, 1, 0, 65536, 1.0, 1, 1, 1, 1, None) == _lib.E_INVALID
-    assert lib.mi_adamw_grad_norm_flat(None, 10, 65536, 1.0, 1, 1, 1, 1, None) == _lib.E_INVALID
+    assert lib.mi_adamw_grad_norm(1, 1, 0, 65536, 1.0, 1, 1, 1, None) == _lib.E_INVALID
+    assert lib.mi_adamw_grad_norm_flat(None, 10, 65536, 1.0, 1, 1, 1, None) == _lib.E_INVALID
     assert lib.mi_adamw_scale_grads(1, 1, 1, 65536, None, None) == _lib.E_INVALID
     row = _lib.TensorRow(param=16, grad=32, exp_avg=48, exp_avg_sq=64, param_copy=0, numel=10,
                          hyper=0, flags=_lib.T_VEC)
