@@ -275,6 +275,10 @@ def main() -> int:
                     help="one of %s, or 'all'" % ", ".join(CONFIGS))
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-context", action="store_true", help="skip torch's GPU rows")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="after the timed steps, run 3 plain 1 GiB device copies (torch copy_) "
+                         "so a counter run (rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE) sees a "
+                         "kernel of known traffic next to the update kernel")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures the optimizer step on one GPU; this build has no multi-GPU "
@@ -290,6 +294,13 @@ def main() -> int:
     names = list(CONFIGS) if args.config == "all" else [args.config]
     results = [run_config(nm, args.steps, args.warmup, device,
                           with_context=not args.no_context and nm == names[0]) for nm in names]
+    if args.calibrate_copy:
+        src = torch.ones(1 << 28, device=device)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
     head = results[0]
     shape_name, clip, state, copy, flat, start_step, gstd = CONFIGS[head["config"]]
     traffic = load_traffic(head["config"])

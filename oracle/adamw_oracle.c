@@ -2,8 +2,8 @@
  * adamw_oracle.c -- CPU restatement of the AdamW optimizer step and the global
  * gradient-norm clip, used ONLY as test infrastructure (the checker).
  *
- * Nothing in the product links or calls this file.  The pytest suite, the smoke
- * check and the CPU-baseline leg of the benchmark load it through oracle.py.
+ * Nothing in the product links or calls this file.  The pytest suite and the
+ * smoke check load it through oracle.py.
  *
  * What it restates (torch 2.10.0+rocm7.0, the third-party code mini-megatron's
  * training loop calls; the reference itself contains no optimizer arithmetic):

@@ -1,8 +1,7 @@
 """CPU oracle for the fused clip + AdamW step -- TEST INFRASTRUCTURE ONLY.
 
-The product never imports this module.  Only the pytest suite, the smoke check
-(``__graft_entry__.smoke``) and the CPU-baseline leg of ``bench.py`` may load
-it, and there only as the checker.
+The product never imports this module.  Only the pytest suite and the smoke
+check (``__graft_entry__.smoke``) load it, and there only as the checker.
 
 It restates, in NumPy plus the C kernels of ``adamw_oracle.c``:
 

@@ -55,7 +55,7 @@ def _assert_same(ref, ours, topt, oopt, max_allowed=0):
 
 
 @pytest.mark.parametrize("betas,lr,wd,maximize", [
-    ((0.9, 0.95), 3e-4, 0.1, False),     # BASELINE hyperparameters
+    ((0.9, 0.95), 3e-4, 0.1, False),     # the benchmark workloads' hyperparameters
     ((0.9, 0.999), 6e-4, 0.1, False),    # mini-megatron's defaults (config.py:11,13)
     ((0.9, 0.999), 6e-4, 0.0, False),    # no weight decay: first op is skipped
     ((0.3, 0.95), 1e-3, 0.01, False),    # lerp weight 0.7: the other Lerp.h branch
