@@ -315,7 +315,7 @@ def main() -> int:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f32" if state == "fp32" else "f32",
+        "dtype": "f32",
         "data": "synthetic: seeded N(0, 0.02) params (LayerNorm 1/0), resident seeded grads, "
                 "mid-training moments",
         "config": {

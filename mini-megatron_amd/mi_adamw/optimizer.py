@@ -45,13 +45,6 @@ _ROW_DTYPE = np.dtype([
 assert _ROW_DTYPE.itemsize == 56
 
 
-def _to_scalar(x):
-    """torch/optim/optimizer.py _to_scalar: a 1-element tensor becomes its Python value."""
-    if isinstance(x, torch.Tensor):
-        return x.item()
-    return x
-
-
 def _hyper(group: dict, step: float) -> _lib.Hyper:
     """The fp32 scalars one (group, step) hands the kernel.
 
@@ -59,24 +52,34 @@ def _hyper(group: dict, step: float) -> _lib.Hyper:
     are Python floats; bias corrections, step size and ``bc2 ** 0.5`` are
     float64; each scalar reaches its ATen kernel cast to fp32, and the division
     of ``sqrt(v)`` by the host scalar ``bc2_sqrt`` runs on the GPU as a multiply
-    by the reciprocal taken in float64.
+    by the reciprocal taken in float64.  A tensor lr stays a tensor in torch
+    (optimizer.py ``_to_scalar`` only squeezes it), so ``1 - lr * wd`` and
+    ``lr / bc1`` are then tensor ops in lr's dtype; they are evaluated here with
+    the same torch ops on the CPU.
     """
-    lr = float(_to_scalar(group["lr"]))
-    beta1, beta2 = (float(_to_scalar(b)) for b in group["betas"])
+    lr = group["lr"]
+    beta1, beta2 = (float(b) for b in group["betas"])
     wd = group["weight_decay"]
     bias_correction1 = 1 - beta1 ** step
     bias_correction2 = 1 - beta2 ** step
-    step_size = lr / bias_correction1
     bias_correction2_sqrt = bias_correction2 ** 0.5
     f32 = np.float32
+    if isinstance(lr, torch.Tensor):
+        lr_t = lr.detach().reshape(()).cpu()
+        wd_factor = float(f32((1 - lr_t * wd).item())) if wd != 0 else 1.0
+        neg_step_size = float(f32((-(lr_t / bias_correction1)).item()))
+    else:
+        lr = float(lr)
+        wd_factor = float(f32(1 - lr * wd)) if wd != 0 else 1.0
+        neg_step_size = float(f32(-(lr / bias_correction1)))
     return _lib.Hyper(
-        wd_factor=float(f32(1 - lr * wd)) if wd != 0 else 1.0,
+        wd_factor=wd_factor,
         lerp_w=float(f32(1 - beta1)),
         beta2=float(f32(beta2)),
         one_minus_beta2=float(f32(1 - beta2)),
         inv_bc2_sqrt=float(f32(1.0 / bias_correction2_sqrt)),
         eps=float(f32(group["eps"])),
-        neg_step_size=float(f32(-step_size)),
+        neg_step_size=neg_step_size,
         grad_sign=-1.0 if group["maximize"] else 1.0,
     )
 
@@ -189,7 +192,9 @@ class FusedAdamW(Optimizer):
                                      "capturable=False and foreach=True")
                 if b.numel() != 1:
                     raise ValueError(f"Tensor betas[{i}] must be 1-element")
-        betas = tuple(map(_to_scalar, betas))
+        if any(isinstance(b, torch.Tensor) for b in betas):
+            raise NotImplementedError("FusedAdamW: betas as Tensors are not supported "
+                                      "(torch steps them through tensor-weight kernels)")
         if fused and differentiable:
             raise RuntimeError("`fused` does not support `differentiable`")
         if fused and foreach:

@@ -1,0 +1,197 @@
+"""GPU: FusedAdamW in a training loop shaped like mini-megatron's (main.py:177-211).
+
+A small pre-LN GPT in the reference's parameter order (token and position
+embeddings, per layer ln1 / qkv / o / ln2 / fc1 / fc2 with bias-free linears,
+ln_f, an untied lm_head) trains with torch.optim.AdamW(fused=False) in one copy
+and FusedAdamW in another, both driven by LambdaLR with warm-up (lr is 0 at
+iteration 0, main.py:36-43), zero_grad -> forward -> backward -> step.  The
+two runs see identical forward/backward kernels, so parameters, moments and
+losses must stay bit-identical step after step.  Also: param groups with
+different hyperparameters (decay / no-decay), more distinct hyperparameter
+sets than one launch holds, a tensor lr, clip write-back and complex params.
+"""
+from __future__ import annotations
+
+import math
+
+import pytest
+import torch
+import torch.nn.functional as F
+
+from _helpers import clone_params, gen, make_params, max_ulp, max_ulp_all, set_grads
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def dev():
+    if not torch.cuda.is_available():
+        pytest.fail("GPU test run without a ROCm GPU")
+    return torch.device("cuda", 0)
+
+
+class TinyGPT(torch.nn.Module):
+    def __init__(self, vocab=512, hidden=64, heads=4, ffn=256, layers=2, positions=64):
+        super().__init__()
+        self.heads = heads
+        self.tok = torch.nn.Embedding(vocab, hidden)
+        self.pos = torch.nn.Embedding(positions, hidden)
+        self.blocks = torch.nn.ModuleList()
+        for _ in range(layers):
+            self.blocks.append(torch.nn.ModuleDict(dict(
+                ln1=torch.nn.LayerNorm(hidden),
+                qkv=torch.nn.Linear(hidden, 3 * hidden, bias=False),
+                o=torch.nn.Linear(hidden, hidden, bias=False),
+                ln2=torch.nn.LayerNorm(hidden),
+                fc1=torch.nn.Linear(hidden, ffn, bias=False),
+                fc2=torch.nn.Linear(ffn, hidden, bias=False))))
+        self.ln_f = torch.nn.LayerNorm(hidden)
+        self.lm_head = torch.nn.Linear(hidden, vocab, bias=False)
+
+    def forward(self, tokens):
+        b, s = tokens.shape
+        x = self.tok(tokens) + self.pos(torch.arange(s, device=tokens.device))
+        for blk in self.blocks:
+            h = blk["ln1"](x)
+            q, k, v = blk["qkv"](h).view(b, s, 3, self.heads, -1).unbind(2)
+            q, k, v = (t.transpose(1, 2) for t in (q, k, v))
+            att = (q @ k.transpose(-1, -2).contiguous()) / math.sqrt(q.shape[-1])
+            mask = torch.ones(s, s, device=tokens.device, dtype=torch.bool).tril()
+            att = att.masked_fill(~mask, float("-inf")).softmax(-1)
+            x = x + blk["o"]((att @ v).transpose(1, 2).reshape(b, s, -1))
+            x = x + blk["fc2"](F.gelu(blk["fc1"](blk["ln2"](x))))
+        return self.lm_head(self.ln_f(x))
+
+
+def _lr_lambda(warmup, total):
+    # Cosine schedule with linear warm-up, as main.py:36-43 defines it.
+    def f(step):
+        if step < warmup:
+            return step / max(warmup, 1)
+        progress = (step - warmup) / max(total - warmup, 1)
+        return 0.5 * (1.0 + math.cos(progress * math.pi))
+    return f
+
+
+def test_training_loop_bit_identical(dev):
+    import mi_adamw
+    torch.manual_seed(0)
+    ref = TinyGPT().to(dev)
+    ours = TinyGPT().to(dev)
+    ours.load_state_dict(ref.state_dict())
+    topt = torch.optim.AdamW(ref.parameters(), lr=6e-4, weight_decay=0.1, fused=False)
+    oopt = mi_adamw.AdamW(ours.parameters(), lr=6e-4, weight_decay=0.1, fused=False)
+    tsch = torch.optim.lr_scheduler.LambdaLR(topt, _lr_lambda(3, 20))
+    osch = torch.optim.lr_scheduler.LambdaLR(oopt, _lr_lambda(3, 20))
+    g = gen(dev, 7)
+    for step in range(12):
+        tokens = torch.randint(0, 512, (4, 32), device=dev, generator=g)
+        losses = []
+        for model, opt in ((ref, topt), (ours, oopt)):
+            opt.zero_grad()
+            logits = model(tokens)
+            loss = F.cross_entropy(logits.view(-1, logits.shape[-1]), tokens.view(-1))
+            loss.backward()
+            losses.append(loss.item())
+        # Same parameters in, same kernels: forward and backward agree bitwise, so
+        # any later difference comes from the optimizer step.
+        assert losses[0] == losses[1]
+        assert max_ulp_all([p.grad for p in ref.parameters()], [q.grad for q in ours.parameters()]) == 0
+        topt.step()
+        oopt.step()
+        tsch.step()
+        osch.step()
+        print(f"step {step}: lr {topt.param_groups[0]['lr']:.3g} loss {losses[0]:.6f}", flush=True)
+        assert max_ulp_all(list(ref.parameters()), list(ours.parameters())) == 0
+    for p, q in zip(ref.parameters(), ours.parameters()):
+        assert max_ulp(topt.state[p]["exp_avg"], oopt.state[q]["exp_avg"]) == 0
+        assert max_ulp(topt.state[p]["exp_avg_sq"], oopt.state[q]["exp_avg_sq"]) == 0
+
+
+def test_decay_and_no_decay_groups(dev):
+    import mi_adamw
+    params = make_params([(128, 64), (64,), (64,), (300, 64), (7,)], dev)
+    ours = clone_params(params)
+    groups = lambda ps: [{"params": [ps[0], ps[3]], "weight_decay": 0.1},
+                         {"params": [ps[1], ps[2], ps[4]], "weight_decay": 0.0, "lr": 1e-3}]
+    topt = torch.optim.AdamW(groups(params), lr=3e-4, betas=(0.9, 0.95), fused=False)
+    oopt = mi_adamw.FusedAdamW(groups(ours), lr=3e-4, betas=(0.9, 0.95), fused=False)
+    for step in range(1, 6):
+        set_grads(params, step, 1e-3)
+        for p, q in zip(params, ours):
+            q.grad = p.grad.clone()
+        topt.param_groups[1]["lr"] *= 0.5
+        oopt.param_groups[1]["lr"] *= 0.5
+        topt.step()
+        oopt.step()
+    torch.cuda.synchronize()
+    assert max_ulp_all(params, ours) == 0
+
+
+def test_more_hyper_sets_than_one_launch(dev):
+    """20 groups with different lr: 20 distinct hyperparameter sets, two launches."""
+    import mi_adamw
+    params = make_params([(257,)] * 20, dev)
+    ours = clone_params(params)
+    tg = [{"params": [p], "lr": 1e-4 * (i + 1)} for i, p in enumerate(params)]
+    og = [{"params": [p], "lr": 1e-4 * (i + 1)} for i, p in enumerate(ours)]
+    topt = torch.optim.AdamW(tg, fused=False)
+    oopt = mi_adamw.FusedAdamW(og, fused=False, max_grad_norm=1.0)
+    for step in range(1, 4):
+        set_grads(params, step, 1e-1)
+        for p, q in zip(params, ours):
+            q.grad = p.grad.clone()
+        oopt.step()
+        torch.nn.utils.clip_grads_with_norm_(params, 1.0, oopt.last_grad_norm.clone())
+        topt.step()
+    torch.cuda.synchronize()
+    assert max_ulp_all(params, ours) == 0
+
+
+def test_tensor_lr(dev):
+    import mi_adamw
+    params = make_params([(1000,)], dev)
+    ours = clone_params(params)
+    topt = torch.optim.AdamW(params, lr=torch.tensor(3e-4), foreach=False)
+    oopt = mi_adamw.FusedAdamW(ours, lr=torch.tensor(3e-4))
+    for step in range(1, 4):
+        set_grads(params, step, 1e-3)
+        ours[0].grad = params[0].grad.clone()
+        topt.step()
+        oopt.step()
+    torch.cuda.synchronize()
+    assert max_ulp_all(params, ours) == 0
+
+
+def test_clip_write_grads_matches_clip_grad_norm(dev):
+    import mi_adamw
+    params = make_params([(4096,), (33, 17), (5,)], dev)
+    ours = clone_params(params)
+    topt = torch.optim.AdamW(params, lr=3e-4, foreach=False)
+    oopt = mi_adamw.FusedAdamW(ours, lr=3e-4, max_grad_norm=0.5, clip_write_grads=True)
+    set_grads(params, 1, 1e-1)
+    for p, q in zip(params, ours):
+        q.grad = p.grad.clone()
+    oopt.step()
+    torch.nn.utils.clip_grads_with_norm_(params, 0.5, oopt.last_grad_norm.clone())
+    topt.step()
+    torch.cuda.synchronize()
+    assert max_ulp_all([p.grad for p in params], [q.grad for q in ours]) == 0
+    assert max_ulp_all(params, ours) == 0
+
+
+def test_complex_params_follow_view_as_real(dev):
+    import mi_adamw
+    base = torch.randn(300, 2, device=dev, generator=gen(dev, 3)) * 0.02
+    p = torch.nn.Parameter(torch.view_as_complex(base.clone()))
+    q = torch.nn.Parameter(torch.view_as_complex(base.clone()))
+    topt = torch.optim.AdamW([p], lr=3e-4, foreach=False)
+    oopt = mi_adamw.FusedAdamW([q], lr=3e-4)
+    for step in range(1, 4):
+        g = torch.randn(300, 2, device=dev, generator=gen(dev, 10 + step)) * 1e-3
+        p.grad = torch.view_as_complex(g.clone())
+        q.grad = torch.view_as_complex(g.clone())
+        topt.step()
+        oopt.step()
+    torch.cuda.synchronize()
+    assert max_ulp(torch.view_as_real(p), torch.view_as_real(q)) == 0

@@ -55,7 +55,8 @@ def test_invalid_arguments_raise_like_torch(kwargs):
 
 
 @pytest.mark.parametrize("kwargs", [dict(amsgrad=True), dict(capturable=True),
-                                    dict(differentiable=True)])
+                                    dict(differentiable=True),
+                                    dict(betas=(torch.tensor(0.9), torch.tensor(0.999)))])
 def test_unsupported_flags_fail_loudly(kwargs):
     with pytest.raises(NotImplementedError):
         mi_adamw.FusedAdamW(_params(), **kwargs)
