@@ -99,10 +99,14 @@ const char *mi_adamw_version(void);
 /* Text for a return code (MI_ADAMW_E_* or hipError_t). */
 const char *mi_adamw_strerror(int code);
 
+/* Chunk sizes (chunk_elems) must be positive multiples of this (one update tile). */
+#define MI_ADAMW_CHUNK_QUANTUM 4096
+
 /* Host-side helper: fill `out` (capacity `cap` entries, host memory) with the
  * chunk table of `n_tensors` tensors of the given sizes.  Returns the number of
  * chunks written, or MI_ADAMW_E_INVALID if it would exceed `cap` or if
- * chunk_elems is not a positive multiple of 1024.  With out == NULL only counts. */
+ * chunk_elems is not a positive multiple of MI_ADAMW_CHUNK_QUANTUM.  With
+ * out == NULL only counts. */
 int64_t mi_adamw_build_chunks(const int64_t *numels, int32_t n_tensors, int64_t chunk_elems,
                               mi_adamw_chunk *out, int64_t cap);
 

@@ -19,6 +19,7 @@ LIB_PATH = os.path.join(HERE, "libmi_adamw.so")
 ABI_VERSION = 1
 MAX_HYPER = 16
 MAX_NORM_BLOCKS = 4096
+CHUNK_QUANTUM = 4096
 
 OK = 0
 E_INVALID = -1

@@ -138,7 +138,7 @@ class FusedAdamW(Optimizer):
                       buffers (each tensor at a 128-byte-aligned offset) and
                       step each param group as one contiguous range.  Gradients
                       stay allocated: zero_grad() zeroes them in place.
-    chunk_elems:      elements per work chunk (multiple of 1024).
+    chunk_elems:      elements per work chunk (multiple of 4096).
 
     Not supported (NotImplementedError at construction): amsgrad,
     capturable, differentiable.
@@ -209,8 +209,8 @@ class FusedAdamW(Optimizer):
             raise ValueError(f"Invalid max_grad_norm: {max_grad_norm}")
         if state_dtype not in (torch.float32, torch.bfloat16):
             raise ValueError(f"state_dtype must be torch.float32 or torch.bfloat16, got {state_dtype}")
-        if chunk_elems <= 0 or chunk_elems % 1024:
-            raise ValueError("chunk_elems must be a positive multiple of 1024")
+        if chunk_elems <= 0 or chunk_elems % _lib.CHUNK_QUANTUM:
+            raise ValueError(f"chunk_elems must be a positive multiple of {_lib.CHUNK_QUANTUM}")
 
         self.max_grad_norm = None if max_grad_norm is None else float(max_grad_norm)
         self.clip_write_grads = bool(clip_write_grads)

@@ -187,6 +187,7 @@ def test_header_structs_match_bindings():
     assert f"#define MI_ADAMW_ABI_VERSION {_lib.ABI_VERSION}" in text
     assert f"#define MI_ADAMW_MAX_HYPER {_lib.MAX_HYPER}" in text
     assert f"#define MI_ADAMW_MAX_NORM_BLOCKS {_lib.MAX_NORM_BLOCKS}" in text
+    assert f"#define MI_ADAMW_CHUNK_QUANTUM {_lib.CHUNK_QUANTUM}" in text
     assert ctypes.sizeof(_lib.TensorRow) == 56
     assert ctypes.sizeof(_lib.Hyper) == 8 * 4
 
@@ -200,8 +201,8 @@ def test_build_chunks_helper():
     assert lib.mi_adamw_build_chunks(numels.ctypes.data, len(numels), 65536, out.ctypes.data, n) == n
     rows = out.reshape(-1, 2).tolist()
     assert rows == [[1, 0], [2, 0], [3, 0], [3, 1], [4, 0], [4, 1], [4, 2]]
-    # Rejected: chunk size not a multiple of 1024, too small a buffer, negative sizes.
-    assert lib.mi_adamw_build_chunks(numels.ctypes.data, len(numels), 1000, None, 0) == _lib.E_INVALID
+    # Rejected: chunk size not a multiple of the quantum, too small a buffer, negative sizes.
+    assert lib.mi_adamw_build_chunks(numels.ctypes.data, len(numels), 1024, None, 0) == _lib.E_INVALID
     assert lib.mi_adamw_build_chunks(numels.ctypes.data, len(numels), 65536, out.ctypes.data,
                                      n - 1) == _lib.E_INVALID
     bad = np.array([-1], dtype=np.int64)
