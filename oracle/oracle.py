@@ -91,10 +91,10 @@ OPMODEL_TORCH_CPU = OpModel(lerp_fma=1, addcmul_mode=2, addcdiv_mode=2, div_reci
 OPMODEL_TORCH_ROCM = OpModel(lerp_fma=1, addcmul_mode=1, addcdiv_mode=1, div_recip=1)
 
 
-def _load():
-    if not os.path.exists(_LIB_PATH):
+def _load(path: str = _LIB_PATH):
+    if not os.path.exists(path):
         raise RuntimeError(f"oracle library missing: build it with `make -C {_HERE}`")
-    lib = ctypes.CDLL(_LIB_PATH)
+    lib = ctypes.CDLL(path)
     f32p = ctypes.POINTER(ctypes.c_float)
     u16p = ctypes.POINTER(ctypes.c_uint16)
     i64 = ctypes.c_int64
@@ -125,6 +125,15 @@ def lib():
     if _lib is None:
         _lib = _load()
     return _lib
+
+
+def use_library(path: str | None):
+    """Point the wrappers at another build of adamw_oracle.c (None: the default).
+
+    The mutation tests use this to run the oracle's own pinning checks against
+    copies of the oracle with a planted mistake."""
+    global _lib
+    _lib = None if path is None else _load(path)
 
 
 def _f32(a: np.ndarray):

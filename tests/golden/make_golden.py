@@ -61,7 +61,9 @@ def run_case(name, *, lr, betas, eps, wd, steps, gstd, maximize=False, clip=None
 
 def clip_cases(store):
     """clip_grad_norm_ on several gradient sets: returned norm and clipped grads."""
-    for c, (std, max_norm) in enumerate([(1e-2, 1.0), (1e-3, 1.0), (1.0, 0.5), (1e-4, 1.0)]):
+    # (std, max_norm): norms ~6.4 (clipped), ~0.064 (not clipped), ~64 (clipped), ~0.64
+    # against 0.25 (clipped, with the 1e-6 visible in fp32)
+    for c, (std, max_norm) in enumerate([(1e-1, 1.0), (1e-3, 1.0), (1.0, 0.5), (1e-2, 0.25)]):
         params = [torch.nn.Parameter(torch.zeros(s)) for s in SHAPES]
         for i, p in enumerate(params):
             p.grad = _randn(p.shape, 5000 + 10 * c + i, std)
@@ -80,8 +82,12 @@ def main():
     run_case("step1_zero", lr=3e-4, betas=(0.9, 0.95), wd=0.1, **base)
     run_case("chain10_refcfg", lr=6e-4, betas=(0.9, 0.999), wd=0.1, eps=1e-8, steps=10, gstd=1e-3,
              store=store)
-    run_case("midtrain_clip", lr=3e-4, betas=(0.9, 0.95), wd=0.1, eps=1e-8, steps=3, gstd=1e-2,
+    # grads N(0, 0.1) over 4112 elements: norm ~6.4, so the clip scales every step
+    run_case("midtrain_clip", lr=3e-4, betas=(0.9, 0.95), wd=0.1, eps=1e-8, steps=3, gstd=1e-1,
              clip=1.0, start_step=1000, store=store)
+    # norm ~0.64 against max_norm 0.25: the 1e-6 in norm + 1e-6 is 16 ulp of the norm here
+    run_case("small_norm_clip", lr=6e-4, betas=(0.9, 0.999), wd=0.1, eps=1e-8, steps=2, gstd=1e-2,
+             clip=0.25, start_step=0, store=store)
     run_case("lerp_big", lr=1e-3, betas=(0.3, 0.95), wd=0.01, eps=1e-8, steps=3, gstd=1e-3,
              store=store)
     run_case("maximize", lr=3e-4, betas=(0.9, 0.95), wd=0.1, eps=1e-8, steps=2, gstd=1e-3,

@@ -53,9 +53,10 @@ def _run_golden(gold, name, opmodel):
         grads = [gold[f"{name}/g/{t}/{i}"].reshape(-1) for i in range(N_SHAPES)]
         scale = None
         if clip > 0:
-            norm = O.total_norm(grads)
-            norms.append(norm)
-            scale = O.clip_coef(norm, clip)
+            # The update is pinned given torch's own norm (stored in the fixture);
+            # the oracle's float64 norm is compared with it separately.
+            norms.append(O.total_norm(grads))
+            scale = O.clip_coef(gold[f"{name}/norms"][t], clip)
         for i in range(N_SHAPES):
             p, m, v = out[i]
             O.adamw_step(p, grads[i].copy(), m, v, lr=lr, betas=(b1, b2), eps=eps, weight_decay=wd,
@@ -64,8 +65,11 @@ def _run_golden(gold, name, opmodel):
     return out, norms
 
 
-@pytest.mark.parametrize("name", ["step1_zero", "chain10_refcfg", "midtrain_clip", "lerp_big",
-                                  "maximize", "wd0", "lr0"])
+GOLDEN_CASES = ["step1_zero", "chain10_refcfg", "midtrain_clip", "small_norm_clip", "lerp_big",
+                "maximize", "wd0", "lr0"]
+
+
+@pytest.mark.parametrize("name", GOLDEN_CASES)
 def test_oracle_matches_torch_cpu_golden(gold, name):
     out, norms = _run_golden(gold, name, O.OPMODEL_TORCH_CPU)
     steps = int(gold[f"{name}/meta"][5])
@@ -96,16 +100,19 @@ def test_opmodels_differ_where_expected(gold):
 
 
 def test_golden_clip_cases(gold):
+    clipped = 0
     for c in range(4):
         grads = [gold[f"clip{c}/g/{i}"].reshape(-1) for i in range(N_SHAPES)]
         norm = O.total_norm(grads)
         ref = float(gold[f"clip{c}/norm"])
         assert abs(float(norm) - ref) <= 1e-6 * ref
         coef = O.clip_coef(np.float32(ref), float(gold[f"clip{c}/max_norm"]))
+        clipped += coef < 1
         for i in range(N_SHAPES):
             # torch multiplies by the clamped coefficient even when it is 1.
             assert np.array_equal((grads[i] * coef).astype(np.float32),
                                   gold[f"clip{c}/gc/{i}"].reshape(-1))
+    assert clipped == 3   # the cases exercise the scale, not only the clamp
 
 
 def _rand(n, seed, std):
@@ -218,6 +225,10 @@ def test_clip_closed_forms():
     assert O.clip_coef(np.float32(32.0), 1.0) == np.float32(np.float32(1.0) / np.float32(32.000001))
     # Below max_norm the coefficient clamps to exactly 1.
     assert O.clip_coef(np.float32(0.25), 1.0) == np.float32(1.0)
+    # Small norms: the 1e-6 is 16 ulp of 0.5, so coef = 0.25 / f32(0.500001) < 0.5.
+    t = np.float32(np.float32(0.5) + np.float32(1e-6))
+    assert t != np.float32(0.5)
+    assert O.clip_coef(np.float32(0.5), 0.25) == np.float32(np.float32(1.0) / t) * np.float32(0.25)
     # NaN propagates through the clamp, as torch.clamp does.
     assert np.isnan(O.clip_coef(np.float32(np.nan), 1.0))
     # inf norm: 1/(inf) = 0 coefficient.

@@ -1,0 +1,110 @@
+"""The oracle's pins catch planted mistakes (CPU only).
+
+Each case compiles a copy of oracle/adamw_oracle.c with one plausible mistake
+(a dropped term, a wrong sign, a swapped operand, a wrong constant, a missing
+clamp, truncation instead of rounding, an off-by-one), points the oracle's
+wrappers at it, and runs the pinning checks of tests/test_oracle.py: golden
+fixtures from torch, closed forms, the float64 bound, bf16 rounding against
+torch.  At least one check must fail for every mutant; the unmodified source
+compiled the same way must pass them all.
+"""
+from __future__ import annotations
+
+import os
+import subprocess
+
+import numpy as np
+import pytest
+
+import test_oracle as T
+from oracle import oracle as O
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+SOURCE = os.path.join(ROOT, "oracle", "adamw_oracle.c")
+
+MUTANTS = {
+    "no_weight_decay": ("float pp = *p * h->wd_factor;", "float pp = *p;"),
+    "lerp_weight_beta1": ("lerp_f32(*m, g, h->lerp_w, om->lerp_fma)",
+                          "lerp_f32(*m, g, 1.0f - h->lerp_w, om->lerp_fma)"),
+    "update_sign": ("pp = om->addcdiv_mode == 1 ? fmaf(h->neg_step_size, q, pp) : pp + h->neg_step_size * q;",
+                    "pp = om->addcdiv_mode == 1 ? fmaf(-h->neg_step_size, q, pp) : pp - h->neg_step_size * q;"),
+    "no_bias_correction2": ("d = om->div_recip ? d * inv_bc2 : d / bc2f;", "d = d;"),
+    "no_eps": ("d = d + h->eps;", "d = d;"),
+    "m_v_swapped": ("float q = mm / d;", "float q = vv / d;"),
+    "g_not_squared": ("vv = addcmul_f32(vv, h->one_minus_beta2, g, om->addcmul_mode);",
+                      "vv = vv + h->one_minus_beta2 * fabsf(g);"),
+    "beta2_swapped": ("float vv = *v * h->beta2;", "float vv = *v * h->one_minus_beta2;"),
+    "clip_not_clamped": ("return (c > 1.0f) ? 1.0f : c;", "return c;"),
+    "clip_eps_dropped": ("float t = total_norm + (float)1e-6;", "float t = total_norm;"),
+    "bf16_truncates": ("u += 0x7fffu + lsb;", "u += 0u * lsb;"),
+    "sumsq_off_by_one": ("for (int64_t i = b; i < e; ++i) { double x = (double)g[i]; s += x * x; }",
+                         "for (int64_t i = b; i + 1 < e; ++i) { double x = (double)g[i]; s += x * x; }"),
+    "grad_scale_ignored": ("if (apply_scale) gi = gi * grad_scale;\n        gi = gi * h->grad_sign;\n        adamw_elem",
+                           "gi = gi * h->grad_sign;\n        adamw_elem"),
+}
+
+
+def _checks(gold):
+    """Every pinning check of test_oracle, as (name, callable) pairs."""
+    out = []
+    for name in T.GOLDEN_CASES:
+        out.append((f"golden:{name}", lambda n=name: T.test_oracle_matches_torch_cpu_golden(gold, n)))
+    out.append(("golden:clip", lambda: T.test_golden_clip_cases(gold)))
+    for om in (O.OPMODEL_TORCH_CPU, O.OPMODEL_TORCH_ROCM):
+        out.append(("lr_zero", lambda om=om: T.test_lr_zero_leaves_params_unchanged(om)))
+        out.append(("first_step", lambda om=om: T.test_first_step_closed_form(om)))
+        for step, b1, b2 in ((1, 0.9, 0.95), (7, 0.9, 0.999), (1000, 0.9, 0.95), (3, 0.3, 0.95)):
+            out.append(("float64_bound",
+                        lambda om=om, s=step, a=b1, b=b2: T.test_float64_bound(om, s, a, b)))
+    out.append(("zero_grad", T.test_zero_grad_decays_state))
+    out.append(("clip_closed_forms", T.test_clip_closed_forms))
+    out.append(("sumsq_brute_force", T.test_sumsq_float64_brute_force))
+    out.append(("bf16_vs_torch", T.test_bf16_rounding_matches_torch))
+    out.append(("bf16_state", T.test_bf16state_with_exact_states_equals_fp32_then_round))
+    return out
+
+
+def _build(src_text: str, out_dir: str, name: str) -> str:
+    c_path = os.path.join(out_dir, f"{name}.c")
+    so_path = os.path.join(out_dir, f"lib{name}.so")
+    with open(c_path, "w") as f:
+        f.write(src_text)
+    subprocess.run(["gcc", "-O2", "-fPIC", "-ffp-contract=off", "-fno-fast-math", "-std=c11",
+                    "-shared", "-o", so_path, c_path, "-lm"], check=True)
+    return so_path
+
+
+def _failures(gold, so_path: str) -> list[str]:
+    O.use_library(so_path)
+    failed = []
+    try:
+        for name, check in _checks(gold):
+            try:
+                check()
+            except AssertionError:
+                failed.append(name)
+    finally:
+        O.use_library(None)
+    return failed
+
+
+@pytest.fixture(scope="module")
+def gold():
+    with np.load(T.GOLDEN, allow_pickle=False) as z:
+        return {k: z[k] for k in z.files}
+
+
+def test_unmodified_copy_passes_every_check(gold, tmp_path):
+    so = _build(open(SOURCE).read(), str(tmp_path), "oracle_copy")
+    assert _failures(gold, so) == []
+
+
+@pytest.mark.parametrize("mutant", sorted(MUTANTS))
+def test_mutant_is_caught(gold, tmp_path, mutant):
+    old, new = MUTANTS[mutant]
+    src = open(SOURCE).read()
+    assert src.count(old) == 1, f"mutation site for {mutant} not found exactly once"
+    so = _build(src.replace(old, new), str(tmp_path), f"oracle_{mutant}")
+    failed = _failures(gold, so)
+    print(f"{mutant}: caught by {failed}")
+    assert failed, f"planted mistake {mutant} passed every pinning check"
