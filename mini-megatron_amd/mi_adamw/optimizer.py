@@ -88,6 +88,18 @@ def _ptr(t: torch.Tensor | None) -> int:
     return 0 if t is None else t.data_ptr()
 
 
+class _Rec:
+    """One parameter's bookkeeping: group index, the parameter, its step slot, its state dict."""
+
+    __slots__ = ("gi", "p", "slot", "st")
+
+    def __init__(self, gi: int, p: torch.Tensor, slot: int):
+        self.gi = gi
+        self.p = p
+        self.slot = slot
+        self.st = None
+
+
 class _Launch:
     """Device-resident tensor and chunk tables for one kernel launch."""
 
@@ -225,6 +237,8 @@ class FusedAdamW(Optimizer):
         self._step_views: list[torch.Tensor | None] = []
         self._copies: dict[int, torch.Tensor] = {}
         self._launch_cache: tuple | None = None
+        self._recs: list | None = None
+        self._recs_key: tuple | None = None
         self._workspace: dict[torch.device, tuple] = {}
         self._flat: FlatLayout | None = None
         self.timing_events = None
@@ -256,6 +270,8 @@ class FusedAdamW(Optimizer):
             group.setdefault("differentiable", False)
             group.setdefault("fused", None)
             group["decoupled_weight_decay"] = True
+        self._recs = None
+        self._launch_cache = None
 
     def add_param_group(self, param_group: dict[str, Any]) -> None:
         if getattr(self, "_flat", None) is not None:
@@ -287,6 +303,7 @@ class FusedAdamW(Optimizer):
             for p in new:
                 self._copies[id(p)] = p.detach().to(torch.bfloat16)
         self._launch_cache = None
+        self._recs = None
 
     def zero_grad(self, set_to_none: bool = True) -> None:
         if self._flat is not None:
@@ -359,6 +376,7 @@ class FusedAdamW(Optimizer):
                         elif t.dtype != self._state_dtype_for(p):
                             st[key] = t.to(self._state_dtype_for(p)).contiguous()
         self._launch_cache = None
+        self._recs = None
 
     # ------------------------------------------------------------------ step
 
@@ -401,6 +419,16 @@ class FusedAdamW(Optimizer):
         if not (p.is_contiguous() and g.is_contiguous()):
             raise NotImplementedError("FusedAdamW: parameters and gradients must be contiguous")
 
+    def _records(self) -> list:
+        """Per-parameter bookkeeping in param_groups order, rebuilt when the groups change."""
+        key = tuple((id(g["params"]), len(g["params"])) for g in self.param_groups)
+        if self._recs is None or self._recs_key != key:
+            self._recs = [_Rec(gi, p, self._slots[id(p)])
+                          for gi, g in enumerate(self.param_groups) for p in g["params"]]
+            self._recs_key = key
+            self._launch_cache = None
+        return self._recs
+
     @torch.no_grad()
     def step(self, closure=None):
         """One optimizer step (adam.py:214-272), fused.  Returns closure's loss."""
@@ -411,52 +439,52 @@ class FusedAdamW(Optimizer):
                 loss = closure()
 
         # Gather params with grads (adam.py:148-153) and initialise their state.
-        entries = []   # (group index, param, grad)
-        slots = []
-        for gi, group in enumerate(self.param_groups):
-            for p in group["params"]:
-                g = p.grad
-                if g is None:
-                    continue
-                if self._flat is not None and not self._flat.is_grad_view(p, g):
-                    self._check_param(p, g)
-                    g = self._flat.absorb_grad(p)
-                self._check_param(p, g)
-                st = self.state[p]
-                if len(st) == 0:
-                    self._init_state(p, st)
-                else:
-                    slot = self._slots[id(p)]
-                    if st["step"] is not self._step_views[slot]:
-                        self._adopt_step(p, st, slot)
-                entries.append((gi, p, g))
-                slots.append(self._slots[id(p)])
+        entries = []   # (record, grad)
+        for rec in self._records():
+            g = rec.p.grad
+            if g is not None:
+                entries.append((rec, g))
         if not entries:
             return loss
+        flat = self._flat
+        for i, (rec, g) in enumerate(entries):
+            if flat is not None and not flat.is_grad_view(rec.p, g):
+                self._check_param(rec.p, g)
+                g = flat.absorb_grad(rec.p)
+                entries[i] = (rec, g)
+            if g.is_sparse:
+                raise RuntimeError("Adam does not support sparse gradients, please consider "
+                                   "SparseAdam instead")
+            st = rec.st
+            if st is None:
+                self._check_param(rec.p, g)   # before self.state gains an entry for p
+                st = rec.st = self.state[rec.p]
+            if len(st) == 0:
+                self._check_param(rec.p, g)
+                self._init_state(rec.p, st)
+            elif st["step"] is not self._step_views[rec.slot]:
+                self._adopt_step(rec.p, st, rec.slot)
 
         # step_t += 1 for every param with a grad (adam.py:414), in one op.
-        if len(slots) == len(self._step_views):
+        if len(entries) == len(self._step_views):
             self._steps += 1
         else:
-            idx = torch.as_tensor(slots, dtype=torch.long)
+            idx = torch.as_tensor([rec.slot for rec, _ in entries], dtype=torch.long)
             self._steps[idx] += 1
         steps_np = self._steps.numpy()
-
-        device = entries[0][1].device
-        if any(p.device != device for _, p, _ in entries):
-            raise NotImplementedError("FusedAdamW: all parameters must be on one device")
 
         # One hyperparameter set per distinct (group, step value).
         keys: dict[tuple[int, float], int] = {}
         hyper_idx = []
-        for (gi, _, _), slot in zip(entries, slots):
-            k = (gi, float(steps_np[slot]))
+        for rec, _ in entries:
+            k = (rec.gi, float(steps_np[rec.slot]))
             h = keys.get(k)
             if h is None:
                 h = keys[k] = len(keys)
             hyper_idx.append(h)
         hypers = [_hyper(self.param_groups[gi], step) for (gi, step) in keys]
 
+        device = entries[0][0].p.device
         with torch.cuda.device(device):
             self._launch(entries, hyper_idx, hypers, device)
         return loss
@@ -486,8 +514,8 @@ class FusedAdamW(Optimizer):
     def _flat_rows(self, entries, hyper_idx) -> np.ndarray:
         """One row per param group whose every param steps with one hyper set."""
         by_group: dict[int, list[int]] = {}
-        for i, (gi, _, _) in enumerate(entries):
-            by_group.setdefault(gi, []).append(i)
+        for i, (rec, _) in enumerate(entries):
+            by_group.setdefault(rec.gi, []).append(i)
         rows = []
         for gi, idx in by_group.items():
             hs = {hyper_idx[i] for i in idx}
@@ -504,8 +532,8 @@ class FusedAdamW(Optimizer):
     def _tensor_rows(self, entries, hyper_idx) -> np.ndarray:
         rows = np.zeros(len(entries), dtype=_ROW_DTYPE)
         bf16_state = self.state_dtype == torch.bfloat16
-        for i, ((_, p, g), h) in enumerate(zip(entries, hyper_idx)):
-            st = self.state[p]
+        for i, ((rec, g), h) in enumerate(zip(entries, hyper_idx)):
+            p, st = rec.p, rec.st
             m, v = st["exp_avg"], st["exp_avg_sq"]
             c = self._copy_for(p) if self.bf16_copy else None
             pp, gp, mp, vp, cp = p.data_ptr(), g.data_ptr(), m.data_ptr(), v.data_ptr(), _ptr(c)
@@ -521,12 +549,18 @@ class FusedAdamW(Optimizer):
             return self._flat.copy_view(p)
         return self._copies[id(p)]
 
-    def _signature(self, entries, hyper_idx) -> list:
-        sig = []
-        for (_, p, g), h in zip(entries, hyper_idx):
-            st = self.state[p]
-            sig += (p.data_ptr(), g.data_ptr(), st["exp_avg"].data_ptr(),
-                    st["exp_avg_sq"].data_ptr(), h)
+    @staticmethod
+    def _signature(entries, hyper_idx) -> list:
+        """Everything a launch's tables encode: the four pointers of each entry.
+
+        The grads are usually new tensors every step (zero_grad sets them to
+        None), so they are compared by address, as are params and moments.
+        """
+        sig = list(hyper_idx)
+        for rec, g in entries:
+            st = rec.st
+            sig += (rec.p.data_ptr(), g.data_ptr(), st["exp_avg"].data_ptr(),
+                    st["exp_avg_sq"].data_ptr())
         return sig
 
     @staticmethod
@@ -563,6 +597,10 @@ class FusedAdamW(Optimizer):
         if cache is not None and cache[0] == sig and cache[1] == device:
             launches, norm_launch = cache[2], cache[3]
         else:
+            for rec, g in entries:
+                self._check_param(rec.p, g)
+                if rec.p.device != device:
+                    raise NotImplementedError("FusedAdamW: all parameters must be on one device")
             launches = [_Launch(self._rows(e, hi), self.chunk_elems, device) for e, hi, _ in parts]
             if len(parts) == 1:
                 norm_launch = launches[0]
