@@ -195,3 +195,109 @@ def test_complex_params_follow_view_as_real(dev):
         oopt.step()
     torch.cuda.synchronize()
     assert max_ulp(torch.view_as_real(p), torch.view_as_real(q)) == 0
+
+
+def test_flat_buffer_training_loop(dev):
+    """flat_buffer=True in a real backward: grads accumulate into the flat views.
+
+    Flat mode keeps gradients allocated, so the torch reference runs
+    zero_grad(set_to_none=False)."""
+    import mi_adamw
+    torch.manual_seed(1)
+    ref = TinyGPT().to(dev)
+    ours = TinyGPT().to(dev)
+    ours.load_state_dict(ref.state_dict())
+    topt = torch.optim.AdamW(ref.parameters(), lr=6e-4, weight_decay=0.1, fused=False)
+    oopt = mi_adamw.AdamW(ours.parameters(), lr=6e-4, weight_decay=0.1, fused=False,
+                          flat_buffer=True, max_grad_norm=1.0, bf16_copy=True)
+    tsch = torch.optim.lr_scheduler.LambdaLR(topt, _lr_lambda(2, 10))
+    osch = torch.optim.lr_scheduler.LambdaLR(oopt, _lr_lambda(2, 10))
+    grad_base = oopt._flat.grad.data_ptr()
+    g = gen(dev, 11)
+    for step in range(8):
+        tokens = torch.randint(0, 512, (4, 32), device=dev, generator=g)
+        for model, opt in ((ref, topt), (ours, oopt)):
+            opt.zero_grad(set_to_none=False)
+            logits = model(tokens)
+            F.cross_entropy(logits.view(-1, logits.shape[-1]), tokens.view(-1)).backward()
+        assert max_ulp_all([p.grad for p in ref.parameters()], [q.grad for q in ours.parameters()]) == 0
+        oopt.step()
+        torch.nn.utils.clip_grads_with_norm_(list(ref.parameters()), 1.0, oopt.last_grad_norm.clone())
+        topt.step()
+        tsch.step()
+        osch.step()
+        assert max_ulp_all(list(ref.parameters()), list(ours.parameters())) == 0
+    # backward wrote into the flat buffer: every grad is still a view of it
+    assert all(oopt._flat.is_grad_view(q, q.grad) for q in ours.parameters())
+    assert oopt._flat.grad.data_ptr() == grad_base
+    for q in ours.parameters():
+        assert torch.equal(oopt.bf16_param(q), q.detach().to(torch.bfloat16))
+
+
+@pytest.mark.parametrize("flat", [False, True])
+def test_checkpoint_interchange_with_torch(dev, flat):
+    """save_checkpoint / load_checkpoint (checkpoint.py:5-21: torch.save, then
+    torch.load(weights_only=True)) across FusedAdamW and torch.optim.AdamW."""
+    import io
+    import mi_adamw
+    shapes = [(96, 64), (64,), (200,), (33, 7)]
+    hp = dict(lr=3e-4, betas=(0.9, 0.95), weight_decay=0.1, fused=False)
+    ours = make_params(shapes, dev)
+    ref = clone_params(ours)
+    oopt = mi_adamw.FusedAdamW(ours, flat_buffer=flat, **hp)
+    topt = torch.optim.AdamW(ref, **hp)
+    for step in range(1, 4):
+        set_grads(ref, step, 1e-3)
+        for p, q in zip(ref, ours):
+            if q.grad is None:
+                q.grad = p.grad.clone()
+            else:
+                q.grad.copy_(p.grad)
+        oopt.step()
+        topt.step()
+    assert max_ulp_all(ref, ours) == 0
+
+    def roundtrip(opt):
+        buf = io.BytesIO()
+        torch.save({"optimizer_state": opt.state_dict(), "step": 3}, buf)
+        buf.seek(0)
+        return torch.load(buf, map_location=dev, weights_only=True)["optimizer_state"]
+
+    # ours -> torch, torch -> ours; both continue two more steps in lockstep.
+    p_t = clone_params(ours)
+    t2 = torch.optim.AdamW(p_t, **hp)
+    t2.load_state_dict(roundtrip(oopt))
+    p_o = clone_params(ref)
+    o2 = mi_adamw.FusedAdamW(p_o, flat_buffer=flat, **hp)
+    o2.load_state_dict(roundtrip(topt))
+    for step in range(4, 6):
+        set_grads(p_t, step, 1e-3)
+        for p, q in zip(p_t, p_o):
+            if q.grad is None:
+                q.grad = p.grad.clone()
+            else:
+                q.grad.copy_(p.grad)
+        t2.step()
+        o2.step()
+    torch.cuda.synchronize()
+    assert max_ulp_all(p_t, p_o) == 0
+    for p, q in zip(p_t, p_o):
+        assert max_ulp(t2.state[p]["exp_avg"], o2.state[q]["exp_avg"]) == 0
+        assert max_ulp(t2.state[p]["exp_avg_sq"], o2.state[q]["exp_avg_sq"]) == 0
+        assert float(t2.state[p]["step"]) == float(o2.state[q]["step"]) == 5.0
+
+
+def test_clip_grad_norm_error_if_nonfinite(dev):
+    import mi_adamw
+    p = torch.nn.Parameter(torch.zeros(100, device=dev))
+    p.grad = torch.ones(100, device=dev)
+    p.grad[3] = float("inf")
+    with pytest.raises(RuntimeError, match="non-finite"):
+        mi_adamw.clip_grad_norm_([p], 1.0, error_if_nonfinite=True)
+    with pytest.raises(NotImplementedError):
+        mi_adamw.clip_grad_norm_([p], 1.0, norm_type=float("inf"))
+    q = torch.nn.Parameter(torch.zeros(100, device=dev))
+    q.grad = torch.full((100,), 0.5, device=dev)
+    n = mi_adamw.clip_grad_norm_([q], 1.0)
+    assert n.item() == 5.0                       # |0.5| * sqrt(100)
+    assert torch.all(q.grad == torch.tensor(0.5 * (1.0 / (5.0 + 1e-6)), device=dev).float())
