@@ -40,7 +40,7 @@
 extern "C" {
 #endif
 
-#define MI_ADAMW_ABI_VERSION 1
+#define MI_ADAMW_ABI_VERSION 2
 #define MI_ADAMW_MAX_HYPER 16      /* hyperparameter sets per launch */
 #define MI_ADAMW_MAX_NORM_BLOCKS 4096 /* partial sums per grad-norm launch */
 
@@ -57,6 +57,9 @@ extern "C" {
 #define MI_ADAMW_F_CLIP (1 << 0)       /* multiply every gradient by *grad_scale first */
 #define MI_ADAMW_F_BF16_COPY (1 << 1)  /* write the updated parameter to param_copy as bf16 */
 #define MI_ADAMW_F_WRITE_GRAD (1 << 2) /* store the scaled gradient back into grad */
+#define MI_ADAMW_F_AMSGRAD (1 << 3)    /* amsgrad: max_exp_avg_sq = maximum(max_exp_avg_sq,
+                                          exp_avg_sq), and the denominator is taken from it
+                                          (adam.py:538-543); every row needs max_exp_avg_sq */
 
 /* mi_adamw_tensor.flags */
 #define MI_ADAMW_T_VEC (1 << 0) /* fp32 pointers 16-byte aligned and bf16 pointers 8-byte
@@ -68,6 +71,8 @@ typedef struct mi_adamw_tensor {
     void *exp_avg;         /* first moment, fp32 or bf16 (state dtype of the launch)  */
     void *exp_avg_sq;      /* second moment, fp32 or bf16                             */
     uint16_t *param_copy;  /* bf16 model copy, or NULL without MI_ADAMW_F_BF16_COPY   */
+    void *max_exp_avg_sq;  /* running maximum of exp_avg_sq (state dtype), or NULL
+                              without MI_ADAMW_F_AMSGRAD                               */
     int64_t numel;         /* elements (a complex64 tensor counts 2 per value)        */
     int32_t hyper;         /* index of this tensor's mi_adamw_hyper in the launch     */
     int32_t flags;         /* MI_ADAMW_T_*                                            */

@@ -16,7 +16,7 @@ import torch
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libmi_adamw.so")
 
-ABI_VERSION = 1
+ABI_VERSION = 2
 MAX_HYPER = 16
 MAX_NORM_BLOCKS = 4096
 CHUNK_QUANTUM = 4096
@@ -31,6 +31,7 @@ STATE_BF16 = 1
 F_CLIP = 1 << 0
 F_BF16_COPY = 1 << 1
 F_WRITE_GRAD = 1 << 2
+F_AMSGRAD = 1 << 3
 
 T_VEC = 1 << 0
 
@@ -56,6 +57,7 @@ class TensorRow(ctypes.Structure):
         ("exp_avg", ctypes.c_void_p),
         ("exp_avg_sq", ctypes.c_void_p),
         ("param_copy", ctypes.c_void_p),
+        ("max_exp_avg_sq", ctypes.c_void_p),
         ("numel", ctypes.c_int64),
         ("hyper", ctypes.c_int32),
         ("flags", ctypes.c_int32),
@@ -83,7 +85,7 @@ class Hyper(ctypes.Structure):
     ]
 
 
-assert ctypes.sizeof(TensorRow) == 56
+assert ctypes.sizeof(TensorRow) == 64
 assert ctypes.sizeof(ChunkRow) == 8
 assert ctypes.sizeof(Hyper) == 32
 

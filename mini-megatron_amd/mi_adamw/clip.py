@@ -39,10 +39,12 @@ def _tables(grads, device):
         return hit
     from .optimizer import _ROW_DTYPE, _Launch
     rows = np.zeros(len(grads), dtype=_ROW_DTYPE)
-    for i, g in enumerate(grads):
-        ptr = g.data_ptr()
-        n = g.numel() * (2 if torch.is_complex(g) else 1)
-        rows[i] = (ptr, ptr, 0, 0, 0, n, 0, _lib.T_VEC if ptr % 16 == 0 else 0)
+    ptrs = np.array([g.data_ptr() for g in grads], dtype=np.uint64)
+    # Only the gradient pointer is read by the norm and scale kernels.
+    rows["param"] = ptrs
+    rows["grad"] = ptrs
+    rows["numel"] = [g.numel() * (2 if torch.is_complex(g) else 1) for g in grads]
+    rows["flags"] = np.where(ptrs % 16 == 0, _lib.T_VEC, 0)
     rows = rows[rows["numel"] > 0]
     launch = _Launch(rows, _CHUNK, device, tables=True)
     if len(_cache) > 8:

@@ -9,7 +9,8 @@
 //                          to device memory (no host sync).
 //   mi_adamw_update_kernel pass 2: p, g, m, v streamed with dwordx4 loads and
 //                          stores, the AdamW op chain in fp32 registers, optional
-//                          bf16 moments, bf16 model copy and gradient write-back.
+//                          bf16 moments, bf16 model copy, gradient write-back and
+//                          amsgrad's running maximum of v.
 //   mi_adamw_scale_kernel  g *= coef in place (clip_grad_norm_'s write-back).
 //
 // Every launch walks a chunk table (one entry per `chunk_elems` slice of a
@@ -51,8 +52,10 @@ struct HyperPack {
     mi_adamw_hyper h[MI_ADAMW_MAX_HYPER];
 };
 
-static_assert(sizeof(mi_adamw_tensor) == 56, "mi_adamw_tensor is read as 7 words");
-static_assert(offsetof(mi_adamw_tensor, hyper) == 48 && offsetof(mi_adamw_tensor, flags) == 52,
+static_assert(sizeof(mi_adamw_tensor) == 64, "mi_adamw_tensor is read as 8 words");
+static_assert(offsetof(mi_adamw_tensor, max_exp_avg_sq) == 40 &&
+              offsetof(mi_adamw_tensor, numel) == 48, "pointer words, then numel");
+static_assert(offsetof(mi_adamw_tensor, hyper) == 56 && offsetof(mi_adamw_tensor, flags) == 60,
               "hyper and flags share the last word");
 static_assert(sizeof(mi_adamw_chunk) == 8, "mi_adamw_chunk is two int32");
 
@@ -76,14 +79,29 @@ __device__ __forceinline__ float lerp_fused(float self, float end, float w) {
     return __builtin_fmaf(-diff, 1.0f - w, end);
 }
 
+// torch.maximum(a, b): NaN if either operand is NaN (a first), else the larger,
+// a on ties.
+__device__ __forceinline__ float maximum_nan(float a, float b) {
+    if (a != a) return a;
+    if (b != b) return b;
+    return a < b ? b : a;
+}
+
 // One element of adam.py:419-547.  g already carries the clip scale and sign.
-__device__ __forceinline__ void adamw_elem(float& p, float g, float& m, float& v,
+// With kAms, x is amsgrad's running maximum of v and the denominator uses it.
+template <bool kAms>
+__device__ __forceinline__ void adamw_elem(float& p, float g, float& m, float& v, float& x,
                                            const mi_adamw_hyper& h) {
     p = p * h.wd_factor;                                   // adam.py:419 mul_
     m = lerp_fused(m, g, h.lerp_w);                        // adam.py:457 lerp_
     v = v * h.beta2;                                       // adam.py:476 mul_
     v = __builtin_fmaf(h.one_minus_beta2, g * g, v);       // adam.py:476 addcmul_
-    float d = __builtin_sqrtf(v);                          // adam.py:545 sqrt
+    float dv = v;
+    if (kAms) {
+        x = maximum_nan(x, v);                             // adam.py:540 maximum(out=)
+        dv = x;
+    }
+    float d = __builtin_sqrtf(dv);                         // adam.py:543/545 sqrt
     d = d * h.inv_bc2_sqrt;                                //   / bc2_sqrt (reciprocal mul)
     d = d + h.eps;                                         //   add_(eps)
     p = __builtin_fmaf(h.neg_step_size, m / d, p);         // adam.py:547 addcdiv_
@@ -129,18 +147,21 @@ __device__ __forceinline__ void st4_bf16(uint16_t* p, f32x4 v) {
 }
 
 // adamw_elem on the four lanes of a dwordx4 group.
-__device__ __forceinline__ void adamw_vec(f32x4& p, f32x4 g, f32x4& m, f32x4& v,
+template <bool kAms>
+__device__ __forceinline__ void adamw_vec(f32x4& p, f32x4 g, f32x4& m, f32x4& v, f32x4& x,
                                           const mi_adamw_hyper& h) {
     float p0 = p.x, p1 = p.y, p2 = p.z, p3 = p.w;
     float m0 = m.x, m1 = m.y, m2 = m.z, m3 = m.w;
     float v0 = v.x, v1 = v.y, v2 = v.z, v3 = v.w;
-    adamw_elem(p0, g.x, m0, v0, h);
-    adamw_elem(p1, g.y, m1, v1, h);
-    adamw_elem(p2, g.z, m2, v2, h);
-    adamw_elem(p3, g.w, m3, v3, h);
+    float x0 = x.x, x1 = x.y, x2 = x.z, x3 = x.w;
+    adamw_elem<kAms>(p0, g.x, m0, v0, x0, h);
+    adamw_elem<kAms>(p1, g.y, m1, v1, x1, h);
+    adamw_elem<kAms>(p2, g.z, m2, v2, x2, h);
+    adamw_elem<kAms>(p3, g.w, m3, v3, x3, h);
     p = f32x4{p0, p1, p2, p3};
     m = f32x4{m0, m1, m2, m3};
     v = f32x4{v0, v1, v2, v3};
+    if (kAms) x = f32x4{x0, x1, x2, x3};
 }
 
 template <typename S> struct StateIO;
@@ -190,16 +211,17 @@ struct TableSource {
         const CONSTANT int32_t* ck = (const CONSTANT int32_t*)(chunks + c);
         const int32_t row = ck[0];
         const int32_t index = ck[1];
-        // mi_adamw_tensor is 7 eight-byte words: 5 pointers, numel, (hyper, flags).
+        // mi_adamw_tensor is 8 eight-byte words: 6 pointers, numel, (hyper, flags).
         const CONSTANT uint64_t* w = (const CONSTANT uint64_t*)(tensors + row);
         t.param = reinterpret_cast<float*>(w[0]);
         t.grad = reinterpret_cast<float*>(w[1]);
         t.exp_avg = reinterpret_cast<void*>(w[2]);
         t.exp_avg_sq = reinterpret_cast<void*>(w[3]);
         t.param_copy = reinterpret_cast<uint16_t*>(w[4]);
-        t.numel = static_cast<int64_t>(w[5]);
-        t.hyper = static_cast<int32_t>(w[6] & 0xffffffffu);
-        t.flags = static_cast<int32_t>(w[6] >> 32);
+        t.max_exp_avg_sq = reinterpret_cast<void*>(w[5]);
+        t.numel = static_cast<int64_t>(w[6]);
+        t.hyper = static_cast<int32_t>(w[7] & 0xffffffffu);
+        t.flags = static_cast<int32_t>(w[7] >> 32);
         begin = static_cast<int64_t>(index) * chunk_elems;
         end = begin + chunk_elems < t.numel ? begin + chunk_elems : t.numel;
     }
@@ -350,24 +372,25 @@ __global__ __launch_bounds__(kNormThreads) void mi_adamw_norm_finalize_kernel(
 // one tile.  Larger chunks are walked tile by tile, software-pipelined: the
 // loads of tile k+1 are issued before tile k is computed and stored.
 
-template <typename StateT, bool kClip, bool kWriteGrad>
+template <typename StateT, bool kAms>
 struct Tile {
-    f32x4 p, g, m, v;
+    f32x4 p, g, m, v, x;
     __device__ __forceinline__ void load(const float* P, const float* G, const void* M,
-                                         const void* V, int64_t k) {
+                                         const void* V, const void* X, int64_t k) {
         g = ld4(G + k);
         p = ld4(P + k);
         m = StateIO<StateT>::ld(M, k);
         v = StateIO<StateT>::ld(V, k);
+        if (kAms) x = StateIO<StateT>::ld(X, k);
     }
 };
 
-template <class Src, typename StateT, bool kClip, bool kCopy, bool kWriteGrad>
+template <class Src, typename StateT, bool kClip, bool kCopy, bool kWriteGrad, bool kAms>
 __global__ __launch_bounds__(kUpdThreads) void mi_adamw_update_kernel(
     Src src, int64_t n_chunks, int64_t chunk_elems, HyperPack hp,
     const float* __restrict__ grad_scale) {
     using IO = StateIO<StateT>;
-    using T = Tile<StateT, kClip, kWriteGrad>;
+    using T = Tile<StateT, kAms>;
     const float scale = kClip ? *grad_scale : 1.0f;
     for (int64_t c = blockIdx.x; c < n_chunks; c += gridDim.x) {
         mi_adamw_tensor t;
@@ -380,6 +403,7 @@ __global__ __launch_bounds__(kUpdThreads) void mi_adamw_update_kernel(
         void* __restrict__ M = t.exp_avg;
         void* __restrict__ V = t.exp_avg_sq;
         uint16_t* __restrict__ C = t.param_copy;
+        void* __restrict__ X = t.max_exp_avg_sq;
 
         int64_t vend = begin;
         if (t.flags & MI_ADAMW_T_VEC) {
@@ -387,20 +411,21 @@ __global__ __launch_bounds__(kUpdThreads) void mi_adamw_update_kernel(
             int64_t i = begin + threadIdx.x * kVec;
             if (i < vend) {
                 T cur;
-                cur.load(P, G, M, V, i);
+                cur.load(P, G, M, V, X, i);
                 while (true) {
                     const int64_t j = i + kUpdTile;
                     const bool more = j < vend;
                     T nxt = cur;
-                    if (more) nxt.load(P, G, M, V, j);
+                    if (more) nxt.load(P, G, M, V, X, j);
                     f32x4 gs = cur.g;
                     if (kClip) gs = f32x4{gs.x * scale, gs.y * scale, gs.z * scale, gs.w * scale};
                     if (kWriteGrad) st4(G + i, gs);
                     gs = f32x4{gs.x * gmul, gs.y * gmul, gs.z * gmul, gs.w * gmul};
-                    adamw_vec(cur.p, gs, cur.m, cur.v, h);
+                    adamw_vec<kAms>(cur.p, gs, cur.m, cur.v, cur.x, h);
                     st4(P + i, cur.p);
                     IO::st(M, i, cur.m);
                     IO::st(V, i, cur.v);
+                    if (kAms) IO::st(X, i, cur.x);
                     if (kCopy) st4_bf16(C + i, cur.p);
                     if (!more) break;
                     cur = nxt;
@@ -416,10 +441,12 @@ __global__ __launch_bounds__(kUpdThreads) void mi_adamw_update_kernel(
             if (kWriteGrad) st1(G + j, g1);
             g1 = g1 * gmul;
             float p1 = ld1(P + j), m1 = IO::ld1(M, j), v1 = IO::ld1(V, j);
-            adamw_elem(p1, g1, m1, v1, h);
+            float x1 = kAms ? IO::ld1(X, j) : 0.0f;
+            adamw_elem<kAms>(p1, g1, m1, v1, x1, h);
             st1(P + j, p1);
             IO::st1(M, j, m1);
             IO::st1(V, j, v1);
+            if (kAms) IO::st1(X, j, x1);
             if (kCopy) st1_u16(C + j, bf16_bits(p1));
         }
     }
@@ -487,24 +514,37 @@ int launch_norm(const Src& src, int64_t n_chunks, int64_t chunk_elems, float max
     return launch_status();
 }
 
+template <class Src, typename StateT, bool kClip, bool kCopy, bool kWriteGrad, bool kAms>
+int launch_update_k(const Src& src, int64_t n_chunks, int64_t chunk_elems, const HyperPack& hp,
+                    const float* scale, unsigned grid, hipStream_t s) {
+    hipLaunchKernelGGL((mi_adamw_update_kernel<Src, StateT, kClip, kCopy, kWriteGrad, kAms>),
+                       dim3(grid), dim3(kUpdThreads), 0, s, src, n_chunks, chunk_elems, hp, scale);
+    return launch_status();
+}
+
+// Runtime flags -> kernel template: one instantiation per (copy, write-grad, amsgrad).
 template <class Src, typename StateT, bool kClip>
 int launch_update_cw(const Src& src, int64_t n_chunks, int64_t chunk_elems, const HyperPack& hp,
                      const float* scale, int32_t flags, unsigned grid, hipStream_t s) {
-    const bool copy = flags & MI_ADAMW_F_BF16_COPY;
-    const bool wg = flags & MI_ADAMW_F_WRITE_GRAD;
-    if (copy && wg)
-        hipLaunchKernelGGL((mi_adamw_update_kernel<Src, StateT, kClip, true, true>), dim3(grid),
-                           dim3(kUpdThreads), 0, s, src, n_chunks, chunk_elems, hp, scale);
-    else if (copy)
-        hipLaunchKernelGGL((mi_adamw_update_kernel<Src, StateT, kClip, true, false>), dim3(grid),
-                           dim3(kUpdThreads), 0, s, src, n_chunks, chunk_elems, hp, scale);
-    else if (wg)
-        hipLaunchKernelGGL((mi_adamw_update_kernel<Src, StateT, kClip, false, true>), dim3(grid),
-                           dim3(kUpdThreads), 0, s, src, n_chunks, chunk_elems, hp, scale);
-    else
-        hipLaunchKernelGGL((mi_adamw_update_kernel<Src, StateT, kClip, false, false>), dim3(grid),
-                           dim3(kUpdThreads), 0, s, src, n_chunks, chunk_elems, hp, scale);
-    return launch_status();
+    const int sel = ((flags & MI_ADAMW_F_BF16_COPY) ? 1 : 0) |
+                    ((flags & MI_ADAMW_F_WRITE_GRAD) ? 2 : 0) |
+                    ((flags & MI_ADAMW_F_AMSGRAD) ? 4 : 0);
+#define MI_ADAMW_SEL(k, C, W, A)                                                              \
+    case k:                                                                                   \
+        return launch_update_k<Src, StateT, kClip, C, W, A>(src, n_chunks, chunk_elems, hp,  \
+                                                             scale, grid, s);
+    switch (sel) {
+        MI_ADAMW_SEL(0, false, false, false)
+        MI_ADAMW_SEL(1, true, false, false)
+        MI_ADAMW_SEL(2, false, true, false)
+        MI_ADAMW_SEL(3, true, true, false)
+        MI_ADAMW_SEL(4, false, false, true)
+        MI_ADAMW_SEL(5, true, false, true)
+        MI_ADAMW_SEL(6, false, true, true)
+        MI_ADAMW_SEL(7, true, true, true)
+    }
+#undef MI_ADAMW_SEL
+    return MI_ADAMW_E_INVALID;
 }
 
 template <class Src>
@@ -514,7 +554,8 @@ int launch_update(const Src& src, int64_t n_chunks, int64_t chunk_elems, const H
     if (n_chunks <= 0 || !chunk_elems_ok(chunk_elems)) return MI_ADAMW_E_INVALID;
     if (state_dtype != MI_ADAMW_STATE_F32 && state_dtype != MI_ADAMW_STATE_BF16)
         return MI_ADAMW_E_INVALID;
-    if (flags & ~(MI_ADAMW_F_CLIP | MI_ADAMW_F_BF16_COPY | MI_ADAMW_F_WRITE_GRAD))
+    if (flags & ~(MI_ADAMW_F_CLIP | MI_ADAMW_F_BF16_COPY | MI_ADAMW_F_WRITE_GRAD |
+                  MI_ADAMW_F_AMSGRAD))
         return MI_ADAMW_E_INVALID;
     const bool clip = flags & MI_ADAMW_F_CLIP;
     if (clip && !scale) return MI_ADAMW_E_INVALID;
@@ -535,11 +576,13 @@ int check_flat(const mi_adamw_tensor* t, int32_t state_dtype, int32_t flags) {
     if (!t || t->numel <= 0 || !t->param || !t->grad || !t->exp_avg || !t->exp_avg_sq)
         return MI_ADAMW_E_INVALID;
     if ((flags & MI_ADAMW_F_BF16_COPY) && !t->param_copy) return MI_ADAMW_E_INVALID;
+    if ((flags & MI_ADAMW_F_AMSGRAD) && !t->max_exp_avg_sq) return MI_ADAMW_E_INVALID;
     if (t->flags & MI_ADAMW_T_VEC) {
         const uintptr_t sa = state_dtype == MI_ADAMW_STATE_BF16 ? 8 : 16;
         if (!aligned(t->param, 16) || !aligned(t->grad, 16) || !aligned(t->exp_avg, sa) ||
             !aligned(t->exp_avg_sq, sa) ||
-            ((flags & MI_ADAMW_F_BF16_COPY) && !aligned(t->param_copy, 8)))
+            ((flags & MI_ADAMW_F_BF16_COPY) && !aligned(t->param_copy, 8)) ||
+            ((flags & MI_ADAMW_F_AMSGRAD) && !aligned(t->max_exp_avg_sq, sa)))
             return MI_ADAMW_E_ALIGN;
     }
     return MI_ADAMW_OK;
@@ -553,7 +596,7 @@ int check_flat(const mi_adamw_tensor* t, int32_t state_dtype, int32_t flags) {
 extern "C" {
 
 const char* mi_adamw_version(void) {
-    return "mi_adamw 1 gfx950 fused clip+adamw (fp32/bf16 state, bf16 copy, flat)";
+    return "mi_adamw 2 gfx950 fused clip+adamw (fp32/bf16 state, bf16 copy, amsgrad, flat)";
 }
 
 const char* mi_adamw_strerror(int code) {

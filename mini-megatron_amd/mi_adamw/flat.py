@@ -4,9 +4,10 @@ mini-megatron's ZeRO-1 optimizer (parallel/distributed_optimizer.py:7-48)
 assigns whole tensors to data-parallel ranks round-robin and steps a per-rank
 torch AdamW over them.  The flat layout here is the single-GPU building block
 of a range-sharded ZeRO-1: each param group occupies one contiguous range of
-four flat buffers (params, grads, exp_avg, exp_avg_sq, plus an optional bf16
-model copy), every tensor starts at a 128-byte-aligned offset (32 fp32
-elements), and the step of a group is one contiguous range for the kernel.
+four flat buffers (params, grads, exp_avg, exp_avg_sq), plus an optional bf16
+model copy and, once a group uses amsgrad, max_exp_avg_sq.  Every tensor starts
+at a 128-byte-aligned offset (32 fp32 elements), and the step of a group is
+one contiguous range for the kernel.
 
 Parameters become views of the flat parameter buffer (``p.data`` is replaced)
 and gradients stay allocated as views of the flat gradient buffer, so
@@ -56,6 +57,7 @@ class FlatLayout:
         self.exp_avg = torch.zeros(off, dtype=state_dtype, device=device)
         self.exp_avg_sq = torch.zeros(off, dtype=state_dtype, device=device)
         self.copy = torch.zeros(off, dtype=torch.bfloat16, device=device) if bf16_copy else None
+        self.max_exp_avg_sq: torch.Tensor | None = None   # allocated on first amsgrad use
         with torch.no_grad():
             for p in params:
                 view = self._view(self.param, p)
@@ -89,8 +91,17 @@ class FlatLayout:
     def state_views(self, p: torch.Tensor):
         return self._view(self.exp_avg, p), self._view(self.exp_avg_sq, p)
 
+    def vmax_view(self, p: torch.Tensor) -> torch.Tensor:
+        """p's slice of the max_exp_avg_sq buffer (amsgrad), allocating the buffer once."""
+        if self.max_exp_avg_sq is None:
+            self.max_exp_avg_sq = torch.zeros_like(self.exp_avg_sq)
+        return self._view(self.max_exp_avg_sq, p)
+
     def adopt_state(self, p: torch.Tensor, key: str, t: torch.Tensor) -> torch.Tensor:
-        view = self._view(self.exp_avg if key == "exp_avg" else self.exp_avg_sq, p)
+        if key == "max_exp_avg_sq":
+            view = self.vmax_view(p)
+        else:
+            view = self._view(self.exp_avg if key == "exp_avg" else self.exp_avg_sq, p)
         view.copy_(t)
         return view
 
@@ -104,12 +115,18 @@ class FlatLayout:
                 if p.grad is None or not self.is_grad_view(p, p.grad):
                     p.grad = self.grad_view(p)
 
-    def group_row(self, gi: int):
-        """(param, grad, exp_avg, exp_avg_sq, copy) pointers and length of group gi's range."""
+    def group_row(self, gi: int, amsgrad: bool = False):
+        """(param, grad, exp_avg, exp_avg_sq, copy, max_exp_avg_sq) pointers and length
+        of group gi's range; max_exp_avg_sq is 0 unless amsgrad."""
         start, end = self.group_ranges[gi]
         s_item = self.exp_avg.element_size()
+        vmax = 0
+        if amsgrad:
+            if self.max_exp_avg_sq is None:
+                raise RuntimeError("flat layout: amsgrad state was never initialised")
+            vmax = self.max_exp_avg_sq.data_ptr() + s_item * start
         return (self.param.data_ptr() + 4 * start, self.grad.data_ptr() + 4 * start,
                 self.exp_avg.data_ptr() + s_item * start,
                 self.exp_avg_sq.data_ptr() + s_item * start,
                 0 if self.copy is None else self.copy.data_ptr() + 2 * start,
-                end - start)
+                vmax, end - start)

@@ -17,7 +17,8 @@ replaces the per-tensor loop with the kernels of libmi_adamw:
   names MAX_GRAD_NORM; torch/nn/utils/clip_grad.py:186-233), computed and
   applied on the device with no host synchronisation;
 * ``mi_adamw_step`` / ``mi_adamw_step_flat`` -- the AdamW update of every
-  tensor, with fp32 or bf16 moments and an optional bf16 model copy.
+  tensor, with fp32 or bf16 moments, an optional bf16 model copy and amsgrad's
+  running maximum (adam.py:538-543) for the groups that set it.
 
 Per-element results match ``torch.optim.AdamW(foreach=False)`` on the same GPU
 tensors: the kernels follow the fp32 op chain and the fused multiply-adds of
@@ -40,9 +41,10 @@ DEFAULT_CHUNK_ELEMS = 4096
 
 _ROW_DTYPE = np.dtype([
     ("param", "<u8"), ("grad", "<u8"), ("exp_avg", "<u8"), ("exp_avg_sq", "<u8"),
-    ("param_copy", "<u8"), ("numel", "<i8"), ("hyper", "<i4"), ("flags", "<i4"),
+    ("param_copy", "<u8"), ("max_exp_avg_sq", "<u8"), ("numel", "<i8"), ("hyper", "<i4"),
+    ("flags", "<i4"),
 ])
-assert _ROW_DTYPE.itemsize == 56
+assert _ROW_DTYPE.itemsize == 64
 
 
 def _hyper(group: dict, step: float) -> _lib.Hyper:
@@ -152,8 +154,8 @@ class FusedAdamW(Optimizer):
                       stay allocated: zero_grad() zeroes them in place.
     chunk_elems:      elements per work chunk (multiple of 4096).
 
-    Not supported (NotImplementedError at construction): amsgrad,
-    capturable, differentiable.
+    Not supported (NotImplementedError at construction): capturable,
+    differentiable, betas as tensors.
     """
 
     def __init__(
@@ -211,8 +213,6 @@ class FusedAdamW(Optimizer):
             raise RuntimeError("`fused` does not support `differentiable`")
         if fused and foreach:
             raise RuntimeError("`fused` and `foreach` cannot be `True` together.")
-        if amsgrad:
-            raise NotImplementedError("FusedAdamW: amsgrad=True is not supported")
         if capturable:
             raise NotImplementedError("FusedAdamW: capturable=True is not supported")
         if differentiable:
@@ -330,18 +330,28 @@ class FusedAdamW(Optimizer):
 
     @torch.no_grad()
     def set_state(self, p: torch.Tensor, step: float, exp_avg: torch.Tensor,
-                  exp_avg_sq: torch.Tensor) -> None:
+                  exp_avg_sq: torch.Tensor, max_exp_avg_sq: torch.Tensor | None = None) -> None:
         """Install one parameter's state in place (like load_state_dict for one
         entry, without materialising a whole state dict): the step count and
         the moments, copied into this optimizer's own storage and dtype."""
         slot = self._slots[id(p)]
         st = self.state[p]
         if "exp_avg" not in st:
-            self._init_state(p, st)
+            self._init_state(p, st, self._amsgrad_of(p))
         self._steps[slot] = float(step)
         st["step"] = self._step_views[slot]
         st["exp_avg"].copy_(exp_avg)
         st["exp_avg_sq"].copy_(exp_avg_sq)
+        if max_exp_avg_sq is not None:
+            if "max_exp_avg_sq" not in st:
+                self._init_vmax(p, st)
+            st["max_exp_avg_sq"].copy_(max_exp_avg_sq)
+
+    def _amsgrad_of(self, p: torch.Tensor) -> bool:
+        for g in self.param_groups:
+            if any(q is p for q in g["params"]):
+                return bool(g["amsgrad"])
+        raise KeyError("parameter is not in any param group")
 
     def state_dict(self) -> dict[str, Any]:
         sd = super().state_dict()
@@ -368,7 +378,7 @@ class FusedAdamW(Optimizer):
                     self._steps[slot] = float(step)
                 self._step_views[slot] = self._steps[slot]
                 st["step"] = self._step_views[slot]
-                for key in ("exp_avg", "exp_avg_sq"):
+                for key in ("exp_avg", "exp_avg_sq", "max_exp_avg_sq"):
                     if key in st:
                         t = st[key]
                         if self._flat is not None:
@@ -383,8 +393,13 @@ class FusedAdamW(Optimizer):
     def _state_dtype_for(self, p: torch.Tensor) -> torch.dtype:
         return p.dtype if self.state_dtype == torch.float32 else self.state_dtype
 
-    def _init_state(self, p: torch.Tensor, st: dict) -> None:
-        """adam.py:160-184 lazy state, with the step kept in the packed CPU buffer."""
+    def _zeros_state(self, p: torch.Tensor) -> torch.Tensor:
+        if self.state_dtype == torch.float32:
+            return torch.zeros_like(p, memory_format=torch.preserve_format)
+        return torch.zeros_like(p, dtype=self.state_dtype, memory_format=torch.contiguous_format)
+
+    def _init_state(self, p: torch.Tensor, st: dict, amsgrad: bool) -> None:
+        """adam.py:160-190 lazy state, with the step kept in the packed CPU buffer."""
         slot = self._slots[id(p)]
         self._steps[slot] = 0.0
         self._step_views[slot] = self._steps[slot]
@@ -393,14 +408,19 @@ class FusedAdamW(Optimizer):
             st["exp_avg"], st["exp_avg_sq"] = self._flat.state_views(p)
             st["exp_avg"].zero_()
             st["exp_avg_sq"].zero_()
-        elif self.state_dtype == torch.float32:
-            st["exp_avg"] = torch.zeros_like(p, memory_format=torch.preserve_format)
-            st["exp_avg_sq"] = torch.zeros_like(p, memory_format=torch.preserve_format)
         else:
-            st["exp_avg"] = torch.zeros_like(p, dtype=self.state_dtype,
-                                             memory_format=torch.contiguous_format)
-            st["exp_avg_sq"] = torch.zeros_like(p, dtype=self.state_dtype,
-                                                memory_format=torch.contiguous_format)
+            st["exp_avg"] = self._zeros_state(p)
+            st["exp_avg_sq"] = self._zeros_state(p)
+        if amsgrad:
+            self._init_vmax(p, st)
+
+    def _init_vmax(self, p: torch.Tensor, st: dict) -> None:
+        """amsgrad's max_exp_avg_sq (adam.py:185-190), zero, in the state dtype."""
+        if self._flat is not None:
+            st["max_exp_avg_sq"] = self._flat.vmax_view(p)
+            st["max_exp_avg_sq"].zero_()
+        else:
+            st["max_exp_avg_sq"] = self._zeros_state(p)
 
     def _check_param(self, p: torch.Tensor, g: torch.Tensor) -> None:
         if g.is_sparse:
@@ -447,6 +467,7 @@ class FusedAdamW(Optimizer):
         if not entries:
             return loss
         flat = self._flat
+        ams_g = [bool(g["amsgrad"]) for g in self.param_groups]
         for i, (rec, g) in enumerate(entries):
             if flat is not None and not flat.is_grad_view(rec.p, g):
                 self._check_param(rec.p, g)
@@ -461,9 +482,12 @@ class FusedAdamW(Optimizer):
                 st = rec.st = self.state[rec.p]
             if len(st) == 0:
                 self._check_param(rec.p, g)
-                self._init_state(rec.p, st)
+                self._init_state(rec.p, st, ams_g[rec.gi])
             elif st["step"] is not self._step_views[rec.slot]:
                 self._adopt_step(rec.p, st, rec.slot)
+            if ams_g[rec.gi] and "max_exp_avg_sq" not in st:
+                # amsgrad switched on for a group after its state was created
+                self._init_vmax(rec.p, st)
 
         # step_t += 1 for every param with a grad (adam.py:414), in one op.
         if len(entries) == len(self._step_views):
@@ -483,10 +507,11 @@ class FusedAdamW(Optimizer):
                 h = keys[k] = len(keys)
             hyper_idx.append(h)
         hypers = [_hyper(self.param_groups[gi], step) for (gi, step) in keys]
+        hyper_ams = [ams_g[gi] for (gi, _) in keys]
 
         device = entries[0][0].p.device
         with torch.cuda.device(device):
-            self._launch(entries, hyper_idx, hypers, device)
+            self._launch(entries, hyper_idx, hypers, hyper_ams, device)
         return loss
 
     def _adopt_step(self, p, st, slot):
@@ -506,12 +531,12 @@ class FusedAdamW(Optimizer):
             ws = self._workspace[device] = (partials, coef)
         return ws
 
-    def _rows(self, entries, hyper_idx) -> np.ndarray:
+    def _rows(self, entries, hyper_idx, ams) -> np.ndarray:
         if self._flat is not None:
-            return self._flat_rows(entries, hyper_idx)
-        return self._tensor_rows(entries, hyper_idx)
+            return self._flat_rows(entries, hyper_idx, ams)
+        return self._tensor_rows(entries, hyper_idx, ams)
 
-    def _flat_rows(self, entries, hyper_idx) -> np.ndarray:
+    def _flat_rows(self, entries, hyper_idx, ams) -> np.ndarray:
         """One row per param group whose every param steps with one hyper set."""
         by_group: dict[int, list[int]] = {}
         for i, (rec, _) in enumerate(entries):
@@ -520,16 +545,16 @@ class FusedAdamW(Optimizer):
         for gi, idx in by_group.items():
             hs = {hyper_idx[i] for i in idx}
             if len(idx) == len(self.param_groups[gi]["params"]) and len(hs) == 1:
-                pp, gp, mp, vp, cp, n = self._flat.group_row(gi)
+                pp, gp, mp, vp, cp, xp, n = self._flat.group_row(gi, ams)
                 r = np.zeros(1, dtype=_ROW_DTYPE)
-                r[0] = (pp, gp, mp, vp, cp, n, hs.pop(), _lib.T_VEC)
+                r[0] = (pp, gp, mp, vp, cp, xp, n, hs.pop(), _lib.T_VEC)
                 rows.append(r)
             else:
                 rows.append(self._tensor_rows([entries[i] for i in idx],
-                                              [hyper_idx[i] for i in idx]))
+                                              [hyper_idx[i] for i in idx], ams))
         return np.concatenate(rows) if rows else np.zeros(0, dtype=_ROW_DTYPE)
 
-    def _tensor_rows(self, entries, hyper_idx) -> np.ndarray:
+    def _tensor_rows(self, entries, hyper_idx, ams) -> np.ndarray:
         rows = np.zeros(len(entries), dtype=_ROW_DTYPE)
         bf16_state = self.state_dtype == torch.bfloat16
         for i, ((rec, g), h) in enumerate(zip(entries, hyper_idx)):
@@ -537,11 +562,12 @@ class FusedAdamW(Optimizer):
             m, v = st["exp_avg"], st["exp_avg_sq"]
             c = self._copy_for(p) if self.bf16_copy else None
             pp, gp, mp, vp, cp = p.data_ptr(), g.data_ptr(), m.data_ptr(), v.data_ptr(), _ptr(c)
+            xp = st["max_exp_avg_sq"].data_ptr() if ams else 0
             n = p.numel() * (2 if torch.is_complex(p) else 1)
             sa = 8 if bf16_state else 16
             vec = (pp % 16 == 0 and gp % 16 == 0 and mp % sa == 0 and vp % sa == 0
-                   and cp % 8 == 0)
-            rows[i] = (pp, gp, mp, vp, cp, n, h, _lib.T_VEC if vec else 0)
+                   and cp % 8 == 0 and xp % sa == 0)
+            rows[i] = (pp, gp, mp, vp, cp, xp, n, h, _lib.T_VEC if vec else 0)
         return rows[rows["numel"] > 0]
 
     def _copy_for(self, p):
@@ -551,7 +577,7 @@ class FusedAdamW(Optimizer):
 
     @staticmethod
     def _signature(entries, hyper_idx) -> list:
-        """Everything a launch's tables encode: the four pointers of each entry.
+        """Everything a launch's tables encode: the pointers of each entry.
 
         The grads are usually new tensors every step (zero_grad sets them to
         None), so they are compared by address, as are params and moments.
@@ -559,8 +585,9 @@ class FusedAdamW(Optimizer):
         sig = list(hyper_idx)
         for rec, g in entries:
             st = rec.st
+            x = st.get("max_exp_avg_sq")
             sig += (rec.p.data_ptr(), g.data_ptr(), st["exp_avg"].data_ptr(),
-                    st["exp_avg_sq"].data_ptr())
+                    st["exp_avg_sq"].data_ptr(), 0 if x is None else x.data_ptr())
         return sig
 
     @staticmethod
@@ -568,10 +595,11 @@ class FusedAdamW(Optimizer):
         r = launch.host_rows[0]
         return _lib.TensorRow(param=int(r["param"]), grad=int(r["grad"]),
                               exp_avg=int(r["exp_avg"]), exp_avg_sq=int(r["exp_avg_sq"]),
-                              param_copy=int(r["param_copy"]), numel=int(r["numel"]),
+                              param_copy=int(r["param_copy"]),
+                              max_exp_avg_sq=int(r["max_exp_avg_sq"]), numel=int(r["numel"]),
                               hyper=0, flags=int(r["flags"]))
 
-    def _launch(self, entries, hyper_idx, hypers, device) -> None:
+    def _launch(self, entries, hyper_idx, hypers, hyper_ams, device) -> None:
         lib = _lib.load()
         stream = torch.cuda.current_stream(device).cuda_stream
         partials, coef = self._ws(device)
@@ -580,16 +608,22 @@ class FusedAdamW(Optimizer):
             flags |= _lib.F_BF16_COPY
         state_code = _lib.STATE_BF16 if self.state_dtype == torch.bfloat16 else _lib.STATE_F32
 
-        # Partition into launches of at most MAX_HYPER hyperparameter sets.
-        if len(hypers) > _lib.MAX_HYPER:
-            parts = []
-            for start in range(0, len(hypers), _lib.MAX_HYPER):
-                sel = [i for i, h in enumerate(hyper_idx) if start <= h < start + _lib.MAX_HYPER]
-                parts.append(([entries[i] for i in sel],
-                              [hyper_idx[i] - start for i in sel],
-                              hypers[start:start + _lib.MAX_HYPER]))
+        # Partition into launches of one amsgrad setting and at most MAX_HYPER
+        # hyperparameter sets each.
+        n_ams = sum(hyper_ams)
+        if len(hypers) <= _lib.MAX_HYPER and n_ams in (0, len(hypers)):
+            parts = [(entries, hyper_idx, hypers, n_ams > 0)]
         else:
-            parts = [(entries, hyper_idx, hypers)]
+            parts = []
+            for ams in (False, True):
+                hsel = [h for h in range(len(hypers)) if hyper_ams[h] == ams]
+                for start in range(0, len(hsel), _lib.MAX_HYPER):
+                    block = hsel[start:start + _lib.MAX_HYPER]
+                    remap = {h: j for j, h in enumerate(block)}
+                    sel = [i for i, h in enumerate(hyper_idx) if h in remap]
+                    parts.append(([entries[i] for i in sel],
+                                  [remap[hyper_idx[i]] for i in sel],
+                                  [hypers[h] for h in block], ams))
 
         # Tables: reused while pointers and hyperparameter assignment are unchanged.
         sig = self._signature(entries, hyper_idx)
@@ -601,11 +635,12 @@ class FusedAdamW(Optimizer):
                 self._check_param(rec.p, g)
                 if rec.p.device != device:
                     raise NotImplementedError("FusedAdamW: all parameters must be on one device")
-            launches = [_Launch(self._rows(e, hi), self.chunk_elems, device) for e, hi, _ in parts]
+            launches = [_Launch(self._rows(e, hi, a), self.chunk_elems, device)
+                        for e, hi, _, a in parts]
             if len(parts) == 1:
                 norm_launch = launches[0]
             else:
-                norm_launch = _Launch(self._rows(entries, [0] * len(entries)),
+                norm_launch = _Launch(self._rows(entries, [0] * len(entries), False),
                                       self.chunk_elems, device)
             self._launch_cache = (sig, device, launches, norm_launch)
 
@@ -635,20 +670,21 @@ class FusedAdamW(Optimizer):
                 flags |= _lib.F_WRITE_GRAD
         if ev is not None:
             ev[1].record()
-        for launch, (_, _, hs) in zip(launches, parts):
+        for launch, (_, _, hs, ams) in zip(launches, parts):
             if launch.n_chunks == 0:
                 continue
+            lflags = flags | (_lib.F_AMSGRAD if ams else 0)
             harr = (_lib.Hyper * len(hs))(*hs)
             if launch.n_rows == 1:
                 row = self._row_struct(launch)
                 row_h = hs[int(launch.host_rows[0]["hyper"])]
                 _lib.check(lib.mi_adamw_step_flat(
                     ctypes.byref(row), ctypes.byref(row_h), coef.data_ptr(), self.chunk_elems,
-                    state_code, flags, self.max_blocks, stream), "mi_adamw_step_flat")
+                    state_code, lflags, self.max_blocks, stream), "mi_adamw_step_flat")
                 continue
             _lib.check(lib.mi_adamw_step(
                 launch.rows.data_ptr(), launch.chunks.data_ptr(), launch.n_chunks,
-                self.chunk_elems, harr, len(hs), coef.data_ptr(), state_code, flags,
+                self.chunk_elems, harr, len(hs), coef.data_ptr(), state_code, lflags,
                 self.max_blocks, stream), "mi_adamw_step")
         if ev is not None:
             ev[2].record()

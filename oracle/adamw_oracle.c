@@ -14,6 +14,8 @@
  *       adam.py:457  m  = lerp(m, g, f32(1 - beta1))                 (lerp_)
  *       adam.py:476  v  = v * f32(beta2); v = v + f32(1-beta2)*g*g   (mul_, addcmul_)
  *       adam.py:545  d  = sqrt(v) / bc2_sqrt; d = d + f32(eps)       (sqrt, div, add_)
+ *       (amsgrad, adam.py:538-543: vmax = maximum(vmax, v), NaN-propagating,
+ *        and d is computed from vmax instead of v)
  *       adam.py:547  p  = p + f32(-step_size) * (m / d)              (addcdiv_)
  *   - torch/include/ATen/native/Lerp.h:21-35  the two-branch lerp formula.
  *   - torch/nn/utils/clip_grad.py:50-117,121-183  global L2 norm, then
@@ -97,8 +99,18 @@ static inline float addcmul_f32(float v, float s, float g, int mode)
     }
 }
 
-/* One element of the op chain above.  p, m, v are updated in place. */
-static inline void adamw_elem(float *p, float g, float *m, float *v,
+/* torch.maximum: NaN if either operand is NaN (a first), else the larger, a on
+ * ties. */
+static inline float maximum_nan(float a, float b)
+{
+    if (isnan(a)) return a;
+    if (isnan(b)) return b;
+    return a < b ? b : a;
+}
+
+/* One element of the op chain above.  p, m, v (and vmax with amsgrad, when
+ * non-NULL) are updated in place. */
+static inline void adamw_elem(float *p, float g, float *m, float *v, float *vmax,
                               const oracle_hyper *h, const oracle_opmodel *om,
                               float inv_bc2, float bc2f)
 {
@@ -106,7 +118,12 @@ static inline void adamw_elem(float *p, float g, float *m, float *v,
     float mm = lerp_f32(*m, g, h->lerp_w, om->lerp_fma);    /* adam.py:457 */
     float vv = *v * h->beta2;                               /* adam.py:476 */
     vv = addcmul_f32(vv, h->one_minus_beta2, g, om->addcmul_mode);
-    float d = sqrtf(vv);                                    /* adam.py:545 */
+    float dv = vv;
+    if (vmax) {                                             /* adam.py:538-540 */
+        *vmax = maximum_nan(*vmax, vv);
+        dv = *vmax;
+    }
+    float d = sqrtf(dv);                                    /* adam.py:543,545 */
     d = om->div_recip ? d * inv_bc2 : d / bc2f;
     d = d + h->eps;
                                                             /* adam.py:547 */
@@ -120,10 +137,10 @@ static inline void adamw_elem(float *p, float g, float *m, float *v,
     *p = pp; *m = mm; *v = vv;
 }
 
-/* fp32 state: p, g, m, v are n contiguous floats.  grad_scale multiplies the
- * gradient first (clip_grad.py:174, g *= coef), then grad_sign applies
- * `maximize` (adam.py:397).  Pass grad_scale = 1 for "no clip". */
-void oracle_adamw_f32(float *p, const float *g, float *m, float *v, int64_t n,
+/* fp32 state: p, g, m, v (and vmax, or NULL without amsgrad) are n contiguous
+ * floats.  grad_scale multiplies the gradient first (clip_grad.py:174,
+ * g *= coef), then grad_sign applies `maximize` (adam.py:397). */
+void oracle_adamw_f32(float *p, const float *g, float *m, float *v, float *vmax, int64_t n,
                       const oracle_hyper *h, const oracle_opmodel *om, float grad_scale,
                       int apply_scale)
 {
@@ -133,16 +150,15 @@ void oracle_adamw_f32(float *p, const float *g, float *m, float *v, int64_t n,
         float gi = g[i];
         if (apply_scale) gi = gi * grad_scale;
         gi = gi * h->grad_sign;
-        adamw_elem(&p[i], gi, &m[i], &v[i], h, om, inv_bc2, bc2f);
+        adamw_elem(&p[i], gi, &m[i], &v[i], vmax ? &vmax[i] : NULL, h, om, inv_bc2, bc2f);
     }
 }
 
-/* bf16 state variant: m and v are stored as bf16, widened to fp32, updated with
- * the same fp32 op chain, and stored back rounded to nearest even.  If copy is
- * non-NULL the updated fp32 parameter is also written as a bf16 model copy. */
-void oracle_adamw_bf16state(float *p, const float *g, uint16_t *m, uint16_t *v, int64_t n,
-                            const oracle_hyper *h, const oracle_opmodel *om, float grad_scale,
-                            int apply_scale)
+/* bf16 state variant: m, v (and vmax) are stored as bf16, widened to fp32,
+ * updated with the same fp32 op chain, and stored back rounded to nearest even. */
+void oracle_adamw_bf16state(float *p, const float *g, uint16_t *m, uint16_t *v,
+                            uint16_t *vmax, int64_t n, const oracle_hyper *h,
+                            const oracle_opmodel *om, float grad_scale, int apply_scale)
 {
     float bc2f = (float)h->bc2_sqrt;
     float inv_bc2 = (float)(1.0 / h->bc2_sqrt);
@@ -152,9 +168,11 @@ void oracle_adamw_bf16state(float *p, const float *g, uint16_t *m, uint16_t *v, 
         gi = gi * h->grad_sign;
         float mm = oracle_bf16_to_f32(m[i]);
         float vv = oracle_bf16_to_f32(v[i]);
-        adamw_elem(&p[i], gi, &mm, &vv, h, om, inv_bc2, bc2f);
+        float mx = vmax ? oracle_bf16_to_f32(vmax[i]) : 0.0f;
+        adamw_elem(&p[i], gi, &mm, &vv, vmax ? &mx : NULL, h, om, inv_bc2, bc2f);
         m[i] = oracle_f32_to_bf16(mm);
         v[i] = oracle_f32_to_bf16(vv);
+        if (vmax) vmax[i] = oracle_f32_to_bf16(mx);
     }
 }
 

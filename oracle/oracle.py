@@ -10,8 +10,9 @@ It restates, in NumPy plus the C kernels of ``adamw_oracle.c``:
   ``bc2 ** 0.5``) and ATen's cast of each Python scalar to the fp32 opmath
   type of the kernel that consumes it.
 * ``adamw_step`` / ``adamw_step_bf16state`` -- the per-element op chain of
-  ``_single_tensor_adam`` (``adam.py:419,457,476,545,547``) and
-  ``ATen/native/Lerp.h:21-35``, one fp32 rounding per ATen kernel.
+  ``_single_tensor_adam`` (``adam.py:419,457,476,545,547``; with amsgrad
+  ``:539-543``) and ``ATen/native/Lerp.h:21-35``, one fp32 rounding per ATen
+  kernel.
 * ``total_norm`` / ``clip_coef`` -- ``torch/nn/utils/clip_grad.py:50-117``
   (global L2 norm over all gradients) and ``:165-169`` (the clamped
   coefficient), the clip mini-megatron defines at ``config.py:16``
@@ -98,11 +99,12 @@ def _load(path: str = _LIB_PATH):
     f32p = ctypes.POINTER(ctypes.c_float)
     u16p = ctypes.POINTER(ctypes.c_uint16)
     i64 = ctypes.c_int64
-    lib.oracle_adamw_f32.argtypes = [f32p, f32p, f32p, f32p, i64, ctypes.POINTER(Hyper),
+    lib.oracle_adamw_f32.argtypes = [f32p, f32p, f32p, f32p, f32p, i64, ctypes.POINTER(Hyper),
                                      ctypes.POINTER(OpModel), ctypes.c_float, ctypes.c_int]
     lib.oracle_adamw_f32.restype = None
-    lib.oracle_adamw_bf16state.argtypes = [f32p, f32p, u16p, u16p, i64, ctypes.POINTER(Hyper),
-                                           ctypes.POINTER(OpModel), ctypes.c_float, ctypes.c_int]
+    lib.oracle_adamw_bf16state.argtypes = [f32p, f32p, u16p, u16p, u16p, i64,
+                                           ctypes.POINTER(Hyper), ctypes.POINTER(OpModel),
+                                           ctypes.c_float, ctypes.c_int]
     lib.oracle_adamw_bf16state.restype = None
     lib.oracle_to_bf16.argtypes = [f32p, u16p, i64]
     lib.oracle_to_bf16.restype = None
@@ -189,24 +191,27 @@ def hyper_from_group(lr, beta1, beta2, eps, weight_decay, step, maximize=False) 
 
 
 def adamw_step(p, g, m, v, *, lr, betas, eps, weight_decay, step, maximize=False,
-               grad_scale=None, opmodel=OPMODEL_TORCH_ROCM) -> None:
-    """One AdamW step on fp32 numpy arrays, in place (p, m, v)."""
+               grad_scale=None, vmax=None, opmodel=OPMODEL_TORCH_ROCM) -> None:
+    """One AdamW step on fp32 numpy arrays, in place (p, m, v; vmax with amsgrad)."""
     h = hyper_from_group(lr, betas[0], betas[1], eps, weight_decay, step, maximize)
     n = p.size
-    if not (g.size == m.size == v.size == n):
+    if not (g.size == m.size == v.size == n) or (vmax is not None and vmax.size != n):
         raise ValueError("p, g, m, v sizes differ")
     scale = 1.0 if grad_scale is None else float(np.float32(grad_scale))
-    lib().oracle_adamw_f32(_f32(p), _f32(g), _f32(m), _f32(v), n, ctypes.byref(h),
+    lib().oracle_adamw_f32(_f32(p), _f32(g), _f32(m), _f32(v),
+                           None if vmax is None else _f32(vmax), n, ctypes.byref(h),
                            ctypes.byref(opmodel), scale, 0 if grad_scale is None else 1)
 
 
 def adamw_step_bf16state(p, g, m_bits, v_bits, *, lr, betas, eps, weight_decay, step,
-                         maximize=False, grad_scale=None, opmodel=OPMODEL_TORCH_ROCM) -> None:
+                         maximize=False, grad_scale=None, vmax_bits=None,
+                         opmodel=OPMODEL_TORCH_ROCM) -> None:
     """AdamW step with bf16-stored moments (uint16 bit arrays), fp32 math."""
     h = hyper_from_group(lr, betas[0], betas[1], eps, weight_decay, step, maximize)
     n = p.size
     scale = 1.0 if grad_scale is None else float(np.float32(grad_scale))
-    lib().oracle_adamw_bf16state(_f32(p), _f32(g), _u16(m_bits), _u16(v_bits), n,
+    lib().oracle_adamw_bf16state(_f32(p), _f32(g), _u16(m_bits), _u16(v_bits),
+                                 None if vmax_bits is None else _u16(vmax_bits), n,
                                  ctypes.byref(h), ctypes.byref(opmodel), scale,
                                  0 if grad_scale is None else 1)
 

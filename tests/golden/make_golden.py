@@ -26,24 +26,31 @@ def _randn(shape, seed, std):
 
 
 def run_case(name, *, lr, betas, eps, wd, steps, gstd, maximize=False, clip=None,
-             start_step=0, store):
+             start_step=0, amsgrad=False, gdecay=1.0, store):
     params = [torch.nn.Parameter(_randn(s, 100 + i, 0.02)) for i, s in enumerate(SHAPES)]
     opt = torch.optim.AdamW(params, lr=lr, betas=betas, eps=eps, weight_decay=wd,
-                            maximize=maximize, foreach=False)
+                            maximize=maximize, amsgrad=amsgrad, foreach=False)
     if start_step:
         for i, p in enumerate(params):
             opt.state[p]["step"] = torch.tensor(float(start_step))
             opt.state[p]["exp_avg"] = _randn(p.shape, 200 + i, 1e-3)
             opt.state[p]["exp_avg_sq"] = _randn(p.shape, 300 + i, 1e-6).abs()
+            if amsgrad:
+                # a running maximum that sits above v for about half the elements
+                opt.state[p]["max_exp_avg_sq"] = torch.maximum(
+                    opt.state[p]["exp_avg_sq"], _randn(p.shape, 400 + i, 1e-6).abs())
     for i, p in enumerate(params):
         store[f"{name}/p0/{i}"] = p.detach().numpy().copy()
         if start_step:
             store[f"{name}/m0/{i}"] = opt.state[p]["exp_avg"].numpy().copy()
             store[f"{name}/v0/{i}"] = opt.state[p]["exp_avg_sq"].numpy().copy()
+            if amsgrad:
+                store[f"{name}/vmax0/{i}"] = opt.state[p]["max_exp_avg_sq"].numpy().copy()
     norms = []
     for t in range(steps):
         for i, p in enumerate(params):
-            p.grad = _randn(p.shape, 1000 * (t + 1) + i, gstd)
+            # gdecay < 1 shrinks the gradients step by step, so v falls below its maximum
+            p.grad = _randn(p.shape, 1000 * (t + 1) + i, gstd * gdecay ** t)
             store[f"{name}/g/{t}/{i}"] = p.grad.numpy().copy()
         if clip is not None:
             norms.append(float(torch.nn.utils.clip_grad_norm_(params, clip)))
@@ -53,8 +60,11 @@ def run_case(name, *, lr, betas, eps, wd, steps, gstd, maximize=False, clip=None
         store[f"{name}/m/{i}"] = opt.state[p]["exp_avg"].numpy().copy()
         store[f"{name}/v/{i}"] = opt.state[p]["exp_avg_sq"].numpy().copy()
         store[f"{name}/step/{i}"] = np.float32(opt.state[p]["step"].item())
+        if amsgrad:
+            store[f"{name}/vmax/{i}"] = opt.state[p]["max_exp_avg_sq"].numpy().copy()
     store[f"{name}/meta"] = np.array([lr, betas[0], betas[1], eps, wd, steps, float(maximize),
-                                      -1.0 if clip is None else clip, start_step], dtype=np.float64)
+                                      -1.0 if clip is None else clip, start_step,
+                                      float(amsgrad)], dtype=np.float64)
     if clip is not None:
         store[f"{name}/norms"] = np.array(norms, dtype=np.float32)
 
@@ -94,6 +104,13 @@ def main():
              maximize=True, store=store)
     run_case("wd0", lr=6e-4, betas=(0.9, 0.999), wd=0.0, eps=1e-8, steps=2, gstd=1e-3, store=store)
     run_case("lr0", lr=0.0, betas=(0.9, 0.999), wd=0.1, eps=1e-8, steps=1, gstd=1e-3, store=store)
+    # amsgrad from zero state with gradients shrinking 4x per step: after the first
+    # steps v decays below its running maximum and the maximum drives the update
+    run_case("amsgrad_decay", lr=6e-4, betas=(0.9, 0.95), wd=0.1, eps=1e-8, steps=5, gstd=1e-2,
+             gdecay=0.25, amsgrad=True, store=store)
+    # amsgrad mid-training with a stored maximum above v on about half the elements, clipped
+    run_case("amsgrad_mid_clip", lr=3e-4, betas=(0.9, 0.999), wd=0.1, eps=1e-8, steps=3,
+             gstd=1e-1, clip=1.0, start_step=1000, amsgrad=True, store=store)
     clip_cases(store)
     np.savez_compressed(OUT, **store)
     print(f"wrote {OUT}: {len(store)} arrays, torch {torch.__version__}")

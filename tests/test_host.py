@@ -54,8 +54,7 @@ def test_invalid_arguments_raise_like_torch(kwargs):
     assert str(ours.value) == str(ref.value)
 
 
-@pytest.mark.parametrize("kwargs", [dict(amsgrad=True), dict(capturable=True),
-                                    dict(differentiable=True),
+@pytest.mark.parametrize("kwargs", [dict(capturable=True), dict(differentiable=True),
                                     dict(betas=(torch.tensor(0.9), torch.tensor(0.999)))])
 def test_unsupported_flags_fail_loudly(kwargs):
     with pytest.raises(NotImplementedError):
@@ -179,7 +178,7 @@ def test_library_exports_every_header_symbol():
     assert set(names) == set(_lib.EXPORTS)
     for name in names:
         assert hasattr(lib, name), name
-    assert _lib.version().startswith("mi_adamw 1 gfx950")
+    assert _lib.version().startswith(f"mi_adamw {_lib.ABI_VERSION} gfx950")
 
 
 def test_header_structs_match_bindings():
@@ -188,8 +187,49 @@ def test_header_structs_match_bindings():
     assert f"#define MI_ADAMW_MAX_HYPER {_lib.MAX_HYPER}" in text
     assert f"#define MI_ADAMW_MAX_NORM_BLOCKS {_lib.MAX_NORM_BLOCKS}" in text
     assert f"#define MI_ADAMW_CHUNK_QUANTUM {_lib.CHUNK_QUANTUM}" in text
-    assert ctypes.sizeof(_lib.TensorRow) == 56
+    assert ctypes.sizeof(_lib.TensorRow) == 64
     assert ctypes.sizeof(_lib.Hyper) == 8 * 4
+    # Field order of mi_adamw_tensor, as declared in the header.
+    body = text[text.index("typedef struct mi_adamw_tensor {"):text.index("} mi_adamw_tensor;")]
+    fields = re.findall(r"\*?\s*(\w+);", body)
+    assert fields == [f for f, _ in _lib.TensorRow._fields_]
+    assert f"#define MI_ADAMW_F_AMSGRAD (1 << 3)" in text and _lib.F_AMSGRAD == 1 << 3
+
+
+def test_table_rows_are_built_field_by_field_on_cpu():
+    """The tensor tables the optimizer and the clip hand the kernels, built on
+    CPU tensors (no launch): every field lands where the row layout puts it."""
+    from mi_adamw import clip as C
+    from mi_adamw.optimizer import _ROW_DTYPE, _Rec
+    assert _ROW_DTYPE.names == tuple(f for f, _ in _lib.TensorRow._fields_)
+    assert _ROW_DTYPE.itemsize == ctypes.sizeof(_lib.TensorRow)
+    grads = [torch.zeros(10), torch.zeros(4097), torch.zeros(0)]
+    launch = C._tables(grads, torch.device("cpu"))
+    rows = launch.host_rows
+    assert len(rows) == 2
+    assert list(rows["grad"]) == [grads[0].data_ptr(), grads[1].data_ptr()]
+    assert list(rows["numel"]) == [10, 4097]
+    assert list(rows["max_exp_avg_sq"]) == [0, 0]
+    assert launch.n_chunks == 1 + 2
+
+    params = [torch.nn.Parameter(torch.zeros(6)), torch.nn.Parameter(torch.zeros(5))]
+    opt = mi_adamw.FusedAdamW([dict(params=params[:1], amsgrad=True),
+                               dict(params=params[1:])])
+    entries = []
+    for gi, p in enumerate(params):
+        rec = _Rec(gi, p, opt._slots[id(p)])
+        rec.st = opt.state[p]
+        opt._init_state(p, rec.st, gi == 0)
+        entries.append((rec, torch.zeros_like(p)))
+    ams_rows = opt._tensor_rows(entries[:1], [0], True)
+    plain_rows = opt._tensor_rows(entries[1:], [0], False)
+    st0, st1 = opt.state[params[0]], opt.state[params[1]]
+    assert ams_rows["max_exp_avg_sq"][0] == st0["max_exp_avg_sq"].data_ptr() != 0
+    assert ams_rows["exp_avg_sq"][0] == st0["exp_avg_sq"].data_ptr()
+    assert plain_rows["max_exp_avg_sq"][0] == 0 and "max_exp_avg_sq" not in st1
+    assert list(plain_rows["numel"]) == [5] and list(ams_rows["numel"]) == [6]
+    row = opt._row_struct(type("L", (), {"host_rows": ams_rows})())
+    assert row.max_exp_avg_sq == st0["max_exp_avg_sq"].data_ptr() and row.numel == 6
 
 
 def test_build_chunks_helper():
@@ -228,6 +268,13 @@ def test_abi_rejects_bad_arguments_without_launching():
     # Flat entry: a bf16 copy requested without a copy pointer, and a misaligned pointer.
     assert lib.mi_adamw_step_flat(ctypes.byref(row), h, None, 65536, 0, _lib.F_BF16_COPY, 0,
                                   None) == _lib.E_INVALID
+    # amsgrad without a max_exp_avg_sq pointer, then with a misaligned one.
+    assert lib.mi_adamw_step_flat(ctypes.byref(row), h, None, 65536, 0, _lib.F_AMSGRAD, 0,
+                                  None) == _lib.E_INVALID
+    row.max_exp_avg_sq = 84
+    assert lib.mi_adamw_step_flat(ctypes.byref(row), h, None, 65536, 0, _lib.F_AMSGRAD, 0,
+                                  None) == _lib.E_ALIGN
+    row.max_exp_avg_sq = 0
     row.grad = 36
     assert lib.mi_adamw_step_flat(ctypes.byref(row), h, None, 65536, 0, 0, 0, None) == _lib.E_ALIGN
     assert "invalid" in _lib.strerror(_lib.E_INVALID)

@@ -36,8 +36,8 @@ def gold():
 
 
 def _run_golden(gold, name, opmodel):
-    lr, b1, b2, eps, wd, steps, maximize, clip, start = gold[f"{name}/meta"]
-    steps, start = int(steps), int(start)
+    lr, b1, b2, eps, wd, steps, maximize, clip, start, amsgrad = gold[f"{name}/meta"]
+    steps, start, amsgrad = int(steps), int(start), bool(amsgrad)
     out = []
     for i in range(N_SHAPES):
         p = gold[f"{name}/p0/{i}"].reshape(-1).copy()
@@ -47,7 +47,10 @@ def _run_golden(gold, name, opmodel):
         else:
             m = np.zeros_like(p)
             v = np.zeros_like(p)
-        out.append([p, m, v])
+        vmax = None
+        if amsgrad:
+            vmax = gold[f"{name}/vmax0/{i}"].reshape(-1).copy() if start else np.zeros_like(p)
+        out.append([p, m, v, vmax])
     norms = []
     for t in range(steps):
         grads = [gold[f"{name}/g/{t}/{i}"].reshape(-1) for i in range(N_SHAPES)]
@@ -58,24 +61,26 @@ def _run_golden(gold, name, opmodel):
             norms.append(O.total_norm(grads))
             scale = O.clip_coef(gold[f"{name}/norms"][t], clip)
         for i in range(N_SHAPES):
-            p, m, v = out[i]
+            p, m, v, vmax = out[i]
             O.adamw_step(p, grads[i].copy(), m, v, lr=lr, betas=(b1, b2), eps=eps, weight_decay=wd,
                          step=float(start + t + 1), maximize=bool(maximize), grad_scale=scale,
-                         opmodel=opmodel)
+                         vmax=vmax, opmodel=opmodel)
     return out, norms
 
 
 GOLDEN_CASES = ["step1_zero", "chain10_refcfg", "midtrain_clip", "small_norm_clip", "lerp_big",
-                "maximize", "wd0", "lr0"]
+                "maximize", "wd0", "lr0", "amsgrad_decay", "amsgrad_mid_clip"]
 
 
 @pytest.mark.parametrize("name", GOLDEN_CASES)
 def test_oracle_matches_torch_cpu_golden(gold, name):
     out, norms = _run_golden(gold, name, O.OPMODEL_TORCH_CPU)
     steps = int(gold[f"{name}/meta"][5])
-    for i, (p, m, v) in enumerate(out):
+    for i, (p, m, v, vmax) in enumerate(out):
         assert O.max_ulp(m, gold[f"{name}/m/{i}"].reshape(-1))[0] == 0
         assert O.max_ulp(v, gold[f"{name}/v/{i}"].reshape(-1))[0] == 0
+        if vmax is not None:
+            assert O.max_ulp(vmax, gold[f"{name}/vmax/{i}"].reshape(-1))[0] == 0
         pr = gold[f"{name}/p/{i}"].reshape(-1).astype(np.float64)
         tol = steps * 2.0 ** -22 * (np.abs(pr) + np.sqrt(np.mean(pr ** 2)))
         assert np.all(np.abs(p - pr) <= tol)
@@ -90,7 +95,7 @@ def test_opmodels_differ_where_expected(gold):
     cpu, _ = _run_golden(gold, "chain10_refcfg", O.OPMODEL_TORCH_CPU)
     gpu, _ = _run_golden(gold, "chain10_refcfg", O.OPMODEL_TORCH_ROCM)
     differs = False
-    for (pc, mc, vc), (pg, mg, vg) in zip(cpu, gpu):
+    for (pc, mc, vc, _), (pg, mg, vg, _) in zip(cpu, gpu):
         for a, b in ((pc, pg), (mc, mg), (vc, vg)):
             a64, b64 = a.astype(np.float64), b.astype(np.float64)
             tol = 10 * 2.0 ** -21 * (np.abs(b64) + np.sqrt(np.mean(b64 ** 2)))

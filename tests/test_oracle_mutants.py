@@ -39,6 +39,8 @@ MUTANTS = {
     "bf16_truncates": ("u += 0x7fffu + lsb;", "u += 0u * lsb;"),
     "sumsq_off_by_one": ("for (int64_t i = b; i < e; ++i) { double x = (double)g[i]; s += x * x; }",
                          "for (int64_t i = b; i + 1 < e; ++i) { double x = (double)g[i]; s += x * x; }"),
+    "amsgrad_max_unused": ("        dv = *vmax;\n", "        (void)dv;\n"),
+    "amsgrad_min": ("return a < b ? b : a;", "return a < b ? a : b;"),
     "grad_scale_ignored": ("if (apply_scale) gi = gi * grad_scale;\n        gi = gi * h->grad_sign;\n        adamw_elem",
                            "gi = gi * h->grad_sign;\n        adamw_elem"),
 }
