@@ -25,6 +25,7 @@ from __future__ import annotations
 
 import argparse
 import json
+import math
 import os
 import statistics
 import sys
@@ -124,7 +125,29 @@ def time_fused(opt, steps: int, warmup: int):
     gpu = start.elapsed_time(end) / steps
     norm_ms = [e[0].elapsed_time(e[1]) for e in evs]
     upd_ms = [e[1].elapsed_time(e[2]) for e in evs]
-    return gpu, wall, norm_ms, upd_ms
+    step_ms = [e[0].elapsed_time(e[2]) for e in evs]
+    return gpu, wall, norm_ms, upd_ms, step_ms
+
+
+def _pct(xs, q):
+    """Nearest-rank percentile of a list (q in [0, 1])."""
+    ys = sorted(xs)
+    return ys[min(len(ys) - 1, max(0, math.ceil(q * len(ys)) - 1))]
+
+
+def host_cpu() -> dict:
+    """CPU model and counts of this host, for the baseline's context."""
+    model = None
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {"model": model, "logical_cpus": os.cpu_count(),
+            "affinity_cpus": len(os.sched_getaffinity(0)), "torch_threads": torch.get_num_threads()}
 
 
 def torch_gpu_rows(name: str, device, steps: int = 10, warmup: int = 3) -> dict:
@@ -218,6 +241,7 @@ def cpu_baseline(name: str, budget_s: float = 20.0) -> dict:
     return {
         "value": round(total_b * n / ms / 1e6, 2), "unit": "GB/s", "cores": threads,
         "kind": "reference", "ms_per_step": round(ms, 2), "params_per_s": round(n / ms * 1e3, 1),
+        "host": host_cpu(),
         "sample": f"torch.optim.AdamW(foreach=False){' after clip_grad_norm_' if clip else ''} "
                   f"on CPU, {len(params)} tensors / {n} params of {shape_name} (fp32 state), "
                   f"median of {len(times)} steps after 2 warm-up",
@@ -241,7 +265,7 @@ def run_config(name: str, steps: int, warmup: int, device, with_context: bool) -
     params, opt, n, n_tensors = build_set(name, device)
     total_b, upd_b = bytes_per_param(clip, state, copy)
     log(f"[bench] {name}: {n} params in {n_tensors} tensors; timing {steps} steps")
-    gpu_ms, wall_ms, norm_ms, upd_ms = time_fused(opt, steps, warmup)
+    gpu_ms, wall_ms, norm_ms, upd_ms, step_ms = time_fused(opt, steps, warmup)
     upd_avg = statistics.mean(upd_ms)
     norm_avg = statistics.mean(norm_ms) if clip else 0.0
     step_bytes = total_b * n
@@ -251,7 +275,8 @@ def run_config(name: str, steps: int, warmup: int, device, with_context: bool) -
         "wall_ms_per_step": wall_ms, "bytes_per_step": step_bytes,
         "gbs": step_bytes / gpu_ms / 1e6, "params_per_s": n / gpu_ms * 1e3,
         "norm_kernel_ms": norm_avg, "update_kernel_ms": upd_avg,
-        "update_kernel_ms_p90": sorted(upd_ms)[int(0.9 * (len(upd_ms) - 1))],
+        "update_kernel_ms_p90": _pct(upd_ms, 0.9),
+        "step_ms_median": statistics.median(step_ms), "step_ms_p90": _pct(step_ms, 0.9),
         "update_bytes_per_launch": upd_b * n, "update_gbs": achieved_upd,
         "dtype": "f32" if state == "fp32" else "f32 math, bf16 moments",
     }
@@ -331,6 +356,8 @@ def main() -> int:
         "wall_ms_per_step": round(head["wall_ms_per_step"], 5),
         "kernels_ms": {"grad_norm": round(head["norm_kernel_ms"], 5),
                        "update": round(head["update_kernel_ms"], 5)},
+        "step_ms_median": round(head["step_ms_median"], 5),
+        "step_ms_p90": round(head["step_ms_p90"], 5),
         "roofline": {
             "bound": "hbm",
             "achieved": round(head["update_gbs"], 2),
