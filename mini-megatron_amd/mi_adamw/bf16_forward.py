@@ -1,0 +1,116 @@
+"""The step's bf16 model copy as the forward pass's GEMM weights.
+
+Reference path.  With ``--amp`` mini-megatron runs its forward under
+``torch.autocast("cuda", dtype=torch.bfloat16)`` (main.py:93,190,205) over fp32
+parameters.  Every GEMM weight reaches ``F.linear`` in the tensor-parallel
+linear layers (parallel/tensor_parallel.py:55,79), and autocast casts it to
+bf16 there: one cast kernel per weight per forward (4 B read + 2 B written per
+parameter), whose backward widens the bf16 weight gradient to fp32 into
+``p.grad``.  ``FusedAdamW(bf16_copy=True)`` already writes that same bf16 value
+-- round-to-nearest-even of the updated fp32 master -- inside its step.
+
+``bf16_weights(optimizer, *modules)`` hands those copies to the linear layers
+for the duration of a forward, in place of the casts:
+
+* forward: ``module.weight`` (and ``bias``) is the bf16 copy; autocast leaves a
+  tensor that already has its target dtype alone, so the GEMM sees the same
+  operands as under the cast;
+* backward: the weight gradient, bf16, is widened to fp32 and accumulated into
+  the master's ``.grad`` -- the backward of autocast's own cast.  (Autocast
+  also caches one cast per weight per region, so a layer called twice inside
+  the context sums its two bf16 gradients before the widening, as here.)
+
+Loss, activations and master gradients are therefore bit-identical to plain
+autocast, without the per-forward weight casts.  Only layers whose weights
+autocast casts to bf16 may be swapped (``F.linear``-based layers); layer norms
+and embeddings keep their fp32 weights, as under autocast.  A copy is refreshed
+from its master when the master changed outside the optimizer (its version
+counter or storage moved, e.g. ``model.load_state_dict``); a change made
+through ``p.data`` is not visible that way: call
+``optimizer.refresh_bf16_copies()`` after one.
+"""
+from __future__ import annotations
+
+import torch
+
+
+class _MastersAsBf16(torch.autograd.Function):
+    """Forward: the bf16 copies of n masters.  Backward: each copy's gradient
+    widened to fp32 for its master (what ``Tensor.to``'s backward does for
+    autocast's cast).  One node for every swapped weight, so the host pays one
+    Python call per forward and one per backward, not one per weight."""
+
+    @staticmethod
+    def forward(ctx, n, *tensors):
+        ctx.set_materialize_grads(False)
+        return tuple(c.view_as(c) for c in tensors[n:])
+
+    @staticmethod
+    def backward(ctx, *grads):
+        widened = tuple(None if g is None else g.to(torch.float32) for g in grads)
+        return (None,) + widened + (None,) * len(grads)
+
+
+def linear_layers(module: torch.nn.Module) -> bool:
+    """Default selection: ``nn.Linear`` and any layer class named ``*Linear`` (the
+    reference's ColumnParallelLinear / RowParallelLinear), which call F.linear."""
+    return isinstance(module, torch.nn.Linear) or type(module).__name__.endswith("Linear")
+
+
+class bf16_weights:
+    """Context manager: selected layers of ``modules`` run on the optimizer's bf16 copies.
+
+    Enter it inside the bf16 autocast region, around the forward::
+
+        with torch.autocast("cuda", dtype=torch.bfloat16), mi_adamw.bf16_weights(opt, model):
+            loss = model(tokens, labels, mask)[1]
+        loss.backward()
+
+    ``select(module) -> bool`` chooses the layers (default ``linear_layers``);
+    only their directly owned fp32 parameters that the optimizer steps are
+    swapped.  While the context is open, ``layer.weight`` is the bf16 copy;
+    on exit the parameters are back in place.  Entering outside a bf16 autocast
+    region raises.
+    """
+
+    def __init__(self, optimizer, *modules: torch.nn.Module, select=linear_layers):
+        if not getattr(optimizer, "bf16_copy", False):
+            raise RuntimeError("bf16_weights needs an optimizer built with bf16_copy=True")
+        owned = {id(p) for g in optimizer.param_groups for p in g["params"]}
+        self.optimizer = optimizer
+        self.swaps: list[tuple[torch.nn.Module, str, torch.nn.Parameter]] = []
+        seen: set[int] = set()
+        for root in modules:
+            for mod in root.modules():
+                if id(mod) in seen or not select(mod):
+                    continue
+                seen.add(id(mod))
+                for n, p in mod.named_parameters(recurse=False):
+                    if id(p) in owned and p.dtype == torch.float32:
+                        self.swaps.append((mod, n, p))
+        self._active = False
+
+    def __enter__(self) -> "bf16_weights":
+        if not self.swaps:
+            return self
+        dev = self.swaps[0][2].device.type
+        if not (torch.is_autocast_enabled(dev) and torch.get_autocast_dtype(dev) == torch.bfloat16):
+            raise RuntimeError("bf16_weights: enter it inside a bf16 autocast region; outside "
+                               "one the swapped weights would not match autocast's casts")
+        opt = self.optimizer
+        opt._track_copies()
+        masters = [p for _, _, p in self.swaps]
+        copies = [opt._current_copy(p) for p in masters]
+        aliases = _MastersAsBf16.apply(len(masters), *masters, *copies)
+        for (mod, n, _), a in zip(self.swaps, aliases):
+            # Assigned into _parameters directly: a non-leaf bf16 tensor for the
+            # duration of the context, restored on exit.
+            mod._parameters[n] = a
+        self._active = True
+        return self
+
+    def __exit__(self, *exc) -> None:
+        if self._active:
+            for mod, n, p in self.swaps:
+                mod._parameters[n] = p
+            self._active = False

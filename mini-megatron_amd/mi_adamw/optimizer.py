@@ -241,6 +241,7 @@ class FusedAdamW(Optimizer):
         self._recs_key: tuple | None = None
         self._workspace: dict[torch.device, tuple] = {}
         self._flat: FlatLayout | None = None
+        self._copy_sync: dict[int, tuple[int, int]] | None = None
         self.timing_events = None
 
         defaults = dict(
@@ -251,12 +252,16 @@ class FusedAdamW(Optimizer):
         super().__init__(params, defaults)
         self.register_load_state_dict_post_hook(FusedAdamW._after_load_state_dict)
 
+        if self.bf16_copy:
+            for group in self.param_groups:
+                for p in group["params"]:
+                    self._check_copyable(p)
         if self.flat_buffer:
             self._flat = FlatLayout(self.param_groups, self.state_dtype, self.bf16_copy)
         elif self.bf16_copy:
             for group in self.param_groups:
                 for p in group["params"]:
-                    self._copies[id(p)] = p.detach().to(torch.bfloat16)
+                    self._copies[id(p)] = self._new_copy(p)
 
     # ------------------------------------------------------------------ torch API
 
@@ -277,6 +282,10 @@ class FusedAdamW(Optimizer):
         if getattr(self, "_flat", None) is not None:
             raise NotImplementedError("FusedAdamW(flat_buffer=True): add_param_group after "
                                       "construction is not supported")
+        if getattr(self, "bf16_copy", False):
+            ps = param_group["params"]
+            for p in ([ps] if isinstance(ps, torch.Tensor) else list(ps)):
+                self._check_copyable(p)
         super().add_param_group(param_group)
         if not hasattr(self, "_slots"):
             return
@@ -301,7 +310,7 @@ class FusedAdamW(Optimizer):
                     st["step"] = self._step_views[slot]
         if getattr(self, "bf16_copy", False) and getattr(self, "_flat", None) is None:
             for p in new:
-                self._copies[id(p)] = p.detach().to(torch.bfloat16)
+                self._copies[id(p)] = self._new_copy(p)
         self._launch_cache = None
         self._recs = None
 
@@ -327,6 +336,55 @@ class FusedAdamW(Optimizer):
         if self._flat is not None:
             return self._flat.copy_view(p)
         return self._copies[id(p)]
+
+    @torch.no_grad()
+    def refresh_bf16_copies(self) -> None:
+        """Rewrite every bf16 copy from its fp32 master (after the masters were
+        changed outside the optimizer, e.g. through ``p.data``)."""
+        if not self.bf16_copy:
+            raise RuntimeError("FusedAdamW was built without bf16_copy=True")
+        for g in self.param_groups:
+            for p in g["params"]:
+                self._refresh_copy(p)
+
+    @staticmethod
+    def _check_copyable(p: torch.Tensor) -> None:
+        if torch.is_complex(p):
+            raise NotImplementedError("FusedAdamW: bf16_copy=True needs real fp32 parameters "
+                                      "(a complex parameter has no bf16 copy)")
+
+    @staticmethod
+    def _new_copy(p: torch.Tensor) -> torch.Tensor:
+        return p.detach().to(torch.bfloat16, memory_format=torch.contiguous_format)
+
+    def _refresh_copy(self, p: torch.Tensor) -> torch.Tensor:
+        if self._flat is not None:
+            c = self._flat.copy_view(p)
+            c.copy_(p.detach())
+        else:
+            c = self._copies.get(id(p))
+            if c is None or c.shape != p.shape or c.device != p.device:
+                c = self._copies[id(p)] = self._new_copy(p)
+                self._launch_cache = None
+            else:
+                c.copy_(p.detach())
+        if self._copy_sync is not None:
+            self._copy_sync[id(p)] = (p._version, p.data_ptr())
+        return c
+
+    def _track_copies(self) -> None:
+        """Start tracking which copies are current (first use of bf16_weights):
+        every copy is rewritten once, then each step records the masters it wrote."""
+        if self._copy_sync is None:
+            self._copy_sync = {}
+            self.refresh_bf16_copies()
+
+    @torch.no_grad()
+    def _current_copy(self, p: torch.Tensor) -> torch.Tensor:
+        """p's bf16 copy, rewritten first if p changed since the copy was written."""
+        if self._copy_sync.get(id(p)) != (p._version, p.data_ptr()):
+            return self._refresh_copy(p)
+        return self._copy_for(p)
 
     @torch.no_grad()
     def set_state(self, p: torch.Tensor, step: float, exp_avg: torch.Tensor,
@@ -434,6 +492,8 @@ class FusedAdamW(Optimizer):
                                       "(fp32 master parameters only)")
         if torch.is_complex(p) and self.state_dtype != torch.float32:
             raise NotImplementedError("FusedAdamW: complex parameters need fp32 state")
+        if self.bf16_copy:
+            self._check_copyable(p)
         if g.dtype != p.dtype or g.shape != p.shape or g.device != p.device:
             raise RuntimeError("FusedAdamW: gradient dtype/shape/device differs from its parameter")
         if not (p.is_contiguous() and g.is_contiguous()):
@@ -512,6 +572,10 @@ class FusedAdamW(Optimizer):
         device = entries[0][0].p.device
         with torch.cuda.device(device):
             self._launch(entries, hyper_idx, hypers, hyper_ams, device)
+        if self._copy_sync is not None:
+            # the launch wrote these masters' copies
+            for rec, _ in entries:
+                self._copy_sync[id(rec.p)] = (rec.p._version, rec.p.data_ptr())
         return loss
 
     def _adopt_step(self, p, st, slot):
@@ -554,15 +618,34 @@ class FusedAdamW(Optimizer):
                                               [hyper_idx[i] for i in idx], ams))
         return np.concatenate(rows) if rows else np.zeros(0, dtype=_ROW_DTYPE)
 
+    def _state_tensor(self, p: torch.Tensor, st: dict, key: str) -> torch.Tensor:
+        """st[key] as the kernel reads it: p's element count, state dtype, p's
+        device, contiguous (converted in place in the state if it is not)."""
+        t = st[key]
+        want = self._state_dtype_for(p)
+        if t.numel() != p.numel():
+            raise RuntimeError(f"FusedAdamW: state[{key!r}] has {t.numel()} elements but its "
+                               f"parameter has {p.numel()}")
+        if t.dtype != want or t.device != p.device or not t.is_contiguous():
+            with torch.no_grad():
+                t = st[key] = t.to(device=p.device, dtype=want,
+                                   memory_format=torch.contiguous_format)
+        return t
+
     def _tensor_rows(self, entries, hyper_idx, ams) -> np.ndarray:
         rows = np.zeros(len(entries), dtype=_ROW_DTYPE)
         bf16_state = self.state_dtype == torch.bfloat16
         for i, ((rec, g), h) in enumerate(zip(entries, hyper_idx)):
             p, st = rec.p, rec.st
-            m, v = st["exp_avg"], st["exp_avg_sq"]
-            c = self._copy_for(p) if self.bf16_copy else None
+            m = self._state_tensor(p, st, "exp_avg")
+            v = self._state_tensor(p, st, "exp_avg_sq")
+            c = None
+            if self.bf16_copy:
+                c = self._copy_for(p)
+                if c.numel() != p.numel() or c.device != p.device or not c.is_contiguous():
+                    c = self._refresh_copy(p)   # p.data was replaced: a new copy of its size
             pp, gp, mp, vp, cp = p.data_ptr(), g.data_ptr(), m.data_ptr(), v.data_ptr(), _ptr(c)
-            xp = st["max_exp_avg_sq"].data_ptr() if ams else 0
+            xp = self._state_tensor(p, st, "max_exp_avg_sq").data_ptr() if ams else 0
             n = p.numel() * (2 if torch.is_complex(p) else 1)
             sa = 8 if bf16_state else 16
             vec = (pp % 16 == 0 and gp % 16 == 0 and mp % sa == 0 and vp % sa == 0

@@ -1,0 +1,68 @@
+"""GPU: training with the step's bf16 copies as the forward's GEMM weights.
+
+Reference loop: zero_grad, forward under bf16 autocast, backward, step
+(main.py:202-209 with --amp).  Two identical models train side by side, one
+with plain autocast (every F.linear casts its fp32 weight), one inside
+mi_adamw.bf16_weights (the step's bf16 copies, no casts).  Loss, master
+gradients, parameters and copies must agree bit for bit at every iteration:
+the copy is round-to-nearest-even of the updated master, which is the value
+autocast's cast produces, and the copy's backward widens the gradient exactly
+as the cast's does.
+"""
+from __future__ import annotations
+
+import pytest
+import torch
+
+import mi_adamw
+import refgpt
+from test_bf16_forward import _bits_equal, weight_casts
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def dev():
+    if not torch.cuda.is_available():
+        pytest.fail("GPU test run without a ROCm GPU")
+    print("mi_adamw", mi_adamw.version(), flush=True)
+    return torch.device("cuda", 0)
+
+
+@pytest.mark.parametrize("flat", [False, True])
+def test_training_on_bf16_copies_is_bit_identical(dev, flat):
+    a = refgpt.tiny(dev, seed=11)
+    b = refgpt.tiny(dev, seed=11)
+    hp = dict(lr=1e-3, betas=(0.9, 0.95), weight_decay=0.1, bf16_copy=True, max_grad_norm=1.0,
+              flat_buffer=flat)
+    oa = mi_adamw.FusedAdamW(a.parameters(), **hp)
+    ob = mi_adamw.FusedAdamW(b.parameters(), **hp)
+    for it in range(5):
+        ids, labels, mask = refgpt.batch(dev, seed=100 + it)
+        oa.zero_grad()
+        ob.zero_grad()
+        with torch.autocast("cuda", dtype=torch.bfloat16):
+            _, la = a(ids, labels, mask)
+        la.backward()
+        with torch.autocast("cuda", dtype=torch.bfloat16), mi_adamw.bf16_weights(ob, b):
+            _, lb = b(ids, labels, mask)
+        lb.backward()
+        assert _bits_equal(la.detach(), lb.detach()), it
+        for p, q in zip(a.parameters(), b.parameters()):
+            assert _bits_equal(p.grad, q.grad), it
+        oa.step()
+        ob.step()
+        torch.cuda.synchronize()
+        for p, q in zip(a.parameters(), b.parameters()):
+            assert _bits_equal(p.detach(), q.detach()), it
+            assert _bits_equal(ob.bf16_param(q), q.detach().bfloat16()), it
+        print(f"iteration {it}: loss {la.item():.6f} identical", flush=True)
+
+
+def test_weight_casts_disappear_on_the_gpu(dev):
+    model = refgpt.tiny(dev)
+    opt = mi_adamw.FusedAdamW(model.parameters(), bf16_copy=True)
+    plain, swapped = weight_casts(model, opt, *refgpt.batch(dev), device_type="cuda")
+    n_linear = sum(1 for m in model.modules() if isinstance(m, refgpt.ColumnLinear))
+    print("aten::_to_copy per forward", plain, swapped, flush=True)
+    assert plain - swapped == n_linear

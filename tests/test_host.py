@@ -230,6 +230,15 @@ def test_table_rows_are_built_field_by_field_on_cpu():
     assert list(plain_rows["numel"]) == [5] and list(ams_rows["numel"]) == [6]
     row = opt._row_struct(type("L", (), {"host_rows": ams_rows})())
     assert row.max_exp_avg_sq == st0["max_exp_avg_sq"].data_ptr() and row.numel == 6
+    # A state tensor of the wrong size is refused before any pointer reaches a kernel;
+    # one of the wrong dtype or layout is converted in place.
+    st1["exp_avg"] = torch.zeros(4)
+    with pytest.raises(RuntimeError, match="elements"):
+        opt._tensor_rows(entries[1:], [0], False)
+    st1["exp_avg"] = torch.zeros(10, dtype=torch.float64)[::2]
+    rows = opt._tensor_rows(entries[1:], [0], False)
+    assert st1["exp_avg"].dtype == torch.float32 and st1["exp_avg"].is_contiguous()
+    assert rows["exp_avg"][0] == st1["exp_avg"].data_ptr()
 
 
 def test_build_chunks_helper():
