@@ -345,3 +345,64 @@ def test_misaligned_views_take_scalar_path(dev):
     torch.cuda.synchronize()
     assert ours[0].data_ptr() % 16 != 0
     _assert_same(ref_views, ours, topt, oopt)
+
+
+@pytest.mark.parametrize("state_dtype", [torch.float32, torch.bfloat16])
+def test_chunk_size_and_grid_shape_do_not_change_results(dev, state_dtype):
+    """The update is elementwise: chunk size (one 4096-element tile per workgroup, or
+    pipelined multi-tile chunks) and grid shape (one chunk per workgroup, or a capped
+    grid striding over chunks) must give the same bits.  The clip norm's float64
+    partial sums do depend on the chunk assignment; its fp32 result is compared to
+    1 ulp, with max_norm so large that the coefficient is exactly 1."""
+    import mi_adamw
+    results, norms = [], []
+    for chunk, max_blocks in ((4096, 0), (8192, 0), (65536, 0), (1 << 20, 0), (4096, 64),
+                              (65536, 7)):
+        params = make_params(MINI_SHAPES, dev)
+        # max_grad_norm 1e9: the norm pass runs under this chunking, the coefficient is 1
+        opt = mi_adamw.FusedAdamW(params, lr=3e-4, betas=(0.9, 0.95), weight_decay=0.1,
+                                  chunk_elems=chunk, state_dtype=state_dtype, bf16_copy=True,
+                                  max_grad_norm=1e9)
+        opt.max_blocks = max_blocks
+        load_states(opt, params, midtrain_state(params, 10.0))
+        for step in (1, 2):
+            set_grads(params, step, 1e-3)
+            opt.step()
+        copies = [c.clone() for c in opt.bf16_params()]
+        normed = opt.last_grad_norm
+        torch.cuda.synchronize()
+        results.append(([p.detach().clone() for p in params],
+                        [opt.state[p]["exp_avg"].clone() for p in params],
+                        [opt.state[p]["exp_avg_sq"].clone() for p in params], copies))
+        norms.append(normed.clone())
+        print(f"chunk {chunk} max_blocks {max_blocks} done", flush=True)
+    base = results[0]
+    for other in results[1:]:
+        for xs, ys in zip(base, other):
+            for x, y in zip(xs, ys):
+                assert torch.equal(x.view(torch.int16) if x.dtype == torch.bfloat16 else x.view(torch.int32),
+                                   y.view(torch.int16) if y.dtype == torch.bfloat16 else y.view(torch.int32))
+    for n in norms[1:]:
+        assert max_ulp(n, norms[0]) <= 1
+
+
+def test_clip_step_is_deterministic(dev):
+    """Two runs on the same inputs give the same bits, norm included (fixed reduction order)."""
+    import mi_adamw
+    runs = []
+    for _ in range(2):
+        params = make_params(MINI_SHAPES, dev)
+        opt = mi_adamw.FusedAdamW(params, lr=3e-4, betas=(0.9, 0.95), weight_decay=0.1,
+                                  max_grad_norm=1.0)
+        load_states(opt, params, midtrain_state(params, 1000.0))
+        norms = []
+        for step in range(3):
+            set_grads(params, step, 1e-2)
+            opt.step()
+            norms.append(opt.last_grad_norm.clone())
+        torch.cuda.synchronize()
+        runs.append(([p.detach().clone() for p in params], norms))
+    for a, b in zip(runs[0][0], runs[1][0]):
+        assert torch.equal(a.view(torch.int32), b.view(torch.int32))
+    for a, b in zip(runs[0][1], runs[1][1]):
+        assert torch.equal(a.view(torch.int32), b.view(torch.int32))
