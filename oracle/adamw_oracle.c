@@ -31,36 +31,13 @@
  *
  * Build: gcc -O2 -ffp-contract=off (Makefile beside this file).  Contraction
  * must stay off so that every fused multiply-add here is an explicit fmaf().
+ * Declarations: adamw_oracle.h.
  */
 #include <math.h>
 #include <stdint.h>
 #include <string.h>
 
-typedef struct oracle_opmodel {
-    int lerp_fma;     /* 1: self + w*(end-self) evaluated as fmaf(w, end-self, self)    */
-    int addcmul_mode; /* v + s*g*g:  0 = v + (s*(g*g)) rounded per op,
-                                      1 = fmaf(s, g*g, v),
-                                      2 = fmaf(s*g, g, v),
-                                      3 = v + ((s*g)*g) rounded per op               */
-    int addcdiv_mode; /* p + s*m/d:  0 = p + (s*(m/d)) rounded per op,
-                                      1 = fmaf(s, m/d, p),
-                                      2 = p + ((s*m)/d) rounded per op               */
-    int div_recip;    /* 1: x / c evaluated as x * f32(1.0 / c), the reciprocal taken
-                            in float64 on the host (host scalar c); 0: x / f32(c)      */
-} oracle_opmodel;
-
-/* Host scalars of one AdamW step, already reduced the way adam.py:414-536 and
- * ATen's scalar handling reduce them (float64 on the host, then cast to fp32). */
-typedef struct oracle_hyper {
-    float wd_factor;       /* f32(1 - lr*wd); 1.0f when weight_decay == 0 (adam.py:417-419) */
-    float lerp_w;          /* f32(1 - beta1)                         (adam.py:457)          */
-    float beta2;           /* f32(beta2)                             (adam.py:476)          */
-    float one_minus_beta2; /* f32(1 - beta2)                         (adam.py:476)          */
-    double bc2_sqrt;       /* (1 - beta2**step) ** 0.5 in float64    (adam.py:532,536)      */
-    float eps;             /* f32(eps)                               (adam.py:545)          */
-    float neg_step_size;   /* f32(-(lr / (1 - beta1**step)))         (adam.py:534,547)      */
-    float grad_sign;       /* -1.0f when maximize (adam.py:397), else 1.0f                  */
-} oracle_hyper;
+#include "adamw_oracle.h"
 
 static inline uint32_t f2u(float x) { uint32_t u; memcpy(&u, &x, 4); return u; }
 static inline float u2f(uint32_t u) { float x; memcpy(&x, &u, 4); return x; }

@@ -1,0 +1,71 @@
+/*
+ * adamw_oracle.h -- declarations of the CPU oracle (adamw_oracle.c), test
+ * infrastructure only: the Python tests bind it through oracle.py, the C ABI
+ * test (tests/c/abi_check.c) links it directly.  Nothing in the product
+ * includes this header.
+ */
+#ifndef ADAMW_ORACLE_H
+#define ADAMW_ORACLE_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct oracle_opmodel {
+    int lerp_fma;     /* 1: self + w*(end-self) evaluated as fmaf(w, end-self, self)    */
+    int addcmul_mode; /* v + s*g*g:  0 = v + (s*(g*g)) rounded per op,
+                                      1 = fmaf(s, g*g, v),
+                                      2 = fmaf(s*g, g, v),
+                                      3 = v + ((s*g)*g) rounded per op               */
+    int addcdiv_mode; /* p + s*m/d:  0 = p + (s*(m/d)) rounded per op,
+                                      1 = fmaf(s, m/d, p),
+                                      2 = p + ((s*m)/d) rounded per op               */
+    int div_recip;    /* 1: x / c evaluated as x * f32(1.0 / c), the reciprocal taken
+                            in float64 on the host (host scalar c); 0: x / f32(c)      */
+} oracle_opmodel;
+
+/* Host scalars of one AdamW step, already reduced the way adam.py:414-536 and
+ * ATen's scalar handling reduce them (float64 on the host, then cast to fp32). */
+typedef struct oracle_hyper {
+    float wd_factor;       /* f32(1 - lr*wd); 1.0f when weight_decay == 0 (adam.py:417-419) */
+    float lerp_w;          /* f32(1 - beta1)                         (adam.py:457)          */
+    float beta2;           /* f32(beta2)                             (adam.py:476)          */
+    float one_minus_beta2; /* f32(1 - beta2)                         (adam.py:476)          */
+    double bc2_sqrt;       /* (1 - beta2**step) ** 0.5 in float64    (adam.py:532,536)      */
+    float eps;             /* f32(eps)                               (adam.py:545)          */
+    float neg_step_size;   /* f32(-(lr / (1 - beta1**step)))         (adam.py:534,547)      */
+    float grad_sign;       /* -1.0f when maximize (adam.py:397), else 1.0f                  */
+} oracle_hyper;
+
+uint16_t oracle_f32_to_bf16(float x);
+float oracle_bf16_to_f32(uint16_t h);
+
+/* fp32 state: p, g, m, v (and vmax, or NULL without amsgrad) are n contiguous
+ * floats, updated in place; grad_scale multiplies g first when apply_scale. */
+void oracle_adamw_f32(float *p, const float *g, float *m, float *v, float *vmax, int64_t n,
+                      const oracle_hyper *h, const oracle_opmodel *om, float grad_scale,
+                      int apply_scale);
+
+/* bf16-stored moments (bit patterns), fp32 math, stores rounded to nearest even. */
+void oracle_adamw_bf16state(float *p, const float *g, uint16_t *m, uint16_t *v,
+                            uint16_t *vmax, int64_t n, const oracle_hyper *h,
+                            const oracle_opmodel *om, float grad_scale, int apply_scale);
+
+void oracle_to_bf16(const float *x, uint16_t *out, int64_t n);
+
+/* Sum of squares in float64 (per 4096-element block, then across blocks). */
+double oracle_sumsq_f64(const float *g, int64_t n);
+
+/* clip_grad.py:165-169: min(max_norm * (1 / (norm + 1e-6)), 1) in fp32, NaN kept. */
+float oracle_clip_coef(float total_norm, double max_norm);
+
+/* Largest ulp distance between two fp32 arrays (NaN vs NaN counts 0). */
+int64_t oracle_max_ulp(const float *a, const float *b, int64_t n, int64_t *argmax);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* ADAMW_ORACLE_H */

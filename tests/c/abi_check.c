@@ -1,0 +1,341 @@
+/*
+ * abi_check.c -- libmi_adamw's C ABI (include/mi_adamw.h) driven from plain C:
+ * no Python, no torch, only the HIP runtime API for device memory.  It shows
+ * that the boundary works for any host that can call C, the way a cgo / JNI /
+ * N-API binding would call it.
+ *
+ *   abi_check cpu   host-side checks only, no device needed: version, error
+ *                   text, the chunk-table helper, and argument rejections that
+ *                   return before any launch.
+ *   abi_check gpu   parity on the device against the CPU oracle
+ *                   (oracle/adamw_oracle.h, test infrastructure):
+ *                   - flat range, fp32 state, fused clip: norm within 1e-6,
+ *                     coefficient and p, m, v bit-exact;
+ *                   - tensor/chunk tables, three tensors, two hyperparameter
+ *                     sets, bf16 moments and bf16 model copy: bit-exact;
+ *                   - flat range with amsgrad: p, m, v, max_exp_avg_sq bit-exact.
+ *
+ * The per-step scalars are computed here as the header documents (float64 on
+ * the host, as torch/optim/adam.py:529-536 does, then cast to fp32), with
+ * floating-point contraction off so that no step fuses.
+ * Exit status 0 on success; the first failed check prints and exits 1.
+ */
+#include <hip/hip_runtime_api.h>
+#include <math.h>
+#include <stdint.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include "adamw_oracle.h"
+#include "mi_adamw.h"
+
+#define CHECK(cond, ...)                                                      \
+    do {                                                                      \
+        if (!(cond)) {                                                        \
+            fprintf(stderr, "abi_check: FAILED %s:%d: ", __FILE__, __LINE__); \
+            fprintf(stderr, __VA_ARGS__);                                     \
+            fprintf(stderr, "\n");                                            \
+            exit(1);                                                          \
+        }                                                                     \
+    } while (0)
+#define HIP(x) CHECK((x) == hipSuccess, "%s", #x)
+
+static uint64_t rng_state = 0x9e3779b97f4a7c15ull;
+static float urand(void) /* uniform in [-1, 1) */
+{
+    rng_state ^= rng_state << 13;
+    rng_state ^= rng_state >> 7;
+    rng_state ^= rng_state << 17;
+    return (float)((double)(rng_state >> 11) * (2.0 / 9007199254740992.0) - 1.0);
+}
+
+static const oracle_opmodel ROCM_OPS = {1, 1, 1, 1};
+
+/* One (group, step) of AdamW, for the library and for the oracle. */
+static void scalars(double lr, double b1, double b2, double eps, double wd, double step,
+                    int maximize, mi_adamw_hyper *h, oracle_hyper *o)
+{
+    const double bc1 = 1.0 - pow(b1, step);
+    const double bc2 = 1.0 - pow(b2, step);
+    const double bc2_sqrt = pow(bc2, 0.5);
+    h->wd_factor = wd != 0.0 ? (float)(1.0 - lr * wd) : 1.0f;
+    h->lerp_w = (float)(1.0 - b1);
+    h->beta2 = (float)b2;
+    h->one_minus_beta2 = (float)(1.0 - b2);
+    h->inv_bc2_sqrt = (float)(1.0 / bc2_sqrt);
+    h->eps = (float)eps;
+    h->neg_step_size = (float)(-(lr / bc1));
+    h->grad_sign = maximize ? -1.0f : 1.0f;
+    o->wd_factor = h->wd_factor;
+    o->lerp_w = h->lerp_w;
+    o->beta2 = h->beta2;
+    o->one_minus_beta2 = h->one_minus_beta2;
+    o->bc2_sqrt = bc2_sqrt;
+    o->eps = h->eps;
+    o->neg_step_size = h->neg_step_size;
+    o->grad_sign = h->grad_sign;
+}
+
+static void fill(float *x, int64_t n, float scale, int absolute)
+{
+    for (int64_t i = 0; i < n; ++i) {
+        float u = urand() * scale;
+        x[i] = absolute ? fabsf(u) : u;
+    }
+}
+
+static void *dev_copy(const void *host, size_t bytes)
+{
+    void *d = NULL;
+    HIP(hipMalloc(&d, bytes));
+    HIP(hipMemcpy(d, host, bytes, hipMemcpyHostToDevice));
+    return d;
+}
+
+static void back(void *host, const void *dev, size_t bytes)
+{
+    HIP(hipMemcpy(host, dev, bytes, hipMemcpyDeviceToHost));
+}
+
+static void same_f32(const float *a, const float *b, int64_t n, const char *what)
+{
+    int64_t where = -1;
+    const int64_t ulp = oracle_max_ulp(a, b, n, &where);
+    CHECK(ulp == 0, "%s differs from the oracle by %lld ulp at %lld", what, (long long)ulp,
+          (long long)where);
+}
+
+static void same_u16(const uint16_t *a, const uint16_t *b, int64_t n, const char *what)
+{
+    for (int64_t i = 0; i < n; ++i)
+        CHECK(a[i] == b[i], "%s differs from the oracle at %lld: %04x vs %04x", what,
+              (long long)i, a[i], b[i]);
+}
+
+/* ------------------------------------------------------------------ CPU */
+
+static int cpu_checks(void)
+{
+    char want[32];
+    snprintf(want, sizeof want, "mi_adamw %d gfx950", MI_ADAMW_ABI_VERSION);
+    CHECK(strncmp(mi_adamw_version(), want, strlen(want)) == 0, "version %s", mi_adamw_version());
+    CHECK(strstr(mi_adamw_strerror(MI_ADAMW_E_INVALID), "invalid") != NULL, "strerror");
+
+    const int64_t numels[5] = {0, 1, 4096, 4097, 3 * 4096 - 5};
+    const int64_t n = mi_adamw_build_chunks(numels, 5, 4096, NULL, 0);
+    CHECK(n == 7, "chunk count %lld", (long long)n);
+    mi_adamw_chunk chunks[7];
+    CHECK(mi_adamw_build_chunks(numels, 5, 4096, chunks, 7) == 7, "chunk fill");
+    const int32_t want_rows[7][2] = {{1, 0}, {2, 0}, {3, 0}, {3, 1}, {4, 0}, {4, 1}, {4, 2}};
+    for (int i = 0; i < 7; ++i)
+        CHECK(chunks[i].tensor == want_rows[i][0] && chunks[i].index == want_rows[i][1],
+              "chunk %d", i);
+    CHECK(mi_adamw_build_chunks(numels, 5, 1000, NULL, 0) == MI_ADAMW_E_INVALID, "chunk size");
+    CHECK(mi_adamw_build_chunks(numels, 5, 4096, chunks, 6) == MI_ADAMW_E_INVALID, "capacity");
+
+    /* Every call below is refused on the host before anything is launched. */
+    mi_adamw_hyper h[1];
+    memset(h, 0, sizeof h);
+    const void *fake = (const void *)(uintptr_t)4096;
+    CHECK(mi_adamw_step(NULL, NULL, 1, 4096, h, 1, NULL, 0, 0, 0, NULL) == MI_ADAMW_E_INVALID,
+          "null tables");
+    CHECK(mi_adamw_step(fake, fake, 1, 4096, h, MI_ADAMW_MAX_HYPER + 1, NULL, 0, 0, 0, NULL) ==
+              MI_ADAMW_E_INVALID, "too many hyper sets");
+    CHECK(mi_adamw_step(fake, fake, 1, 1000, h, 1, NULL, 0, 0, 0, NULL) == MI_ADAMW_E_INVALID,
+          "chunk size");
+    CHECK(mi_adamw_step(fake, fake, 1, 4096, h, 1, NULL, 0, MI_ADAMW_F_CLIP, 0, NULL) ==
+              MI_ADAMW_E_INVALID, "clip without a scale");
+    mi_adamw_tensor t;
+    memset(&t, 0, sizeof t);
+    t.param = (float *)(uintptr_t)4096;
+    t.grad = (float *)(uintptr_t)(8192 + 4); /* flagged aligned, but not 16-byte aligned */
+    t.exp_avg = (void *)(uintptr_t)12288;
+    t.exp_avg_sq = (void *)(uintptr_t)16384;
+    t.numel = 10;
+    t.flags = MI_ADAMW_T_VEC;
+    CHECK(mi_adamw_step_flat(&t, h, NULL, 4096, MI_ADAMW_STATE_F32, 0, 0, NULL) ==
+              MI_ADAMW_E_ALIGN, "misaligned flat range");
+    t.grad = (float *)(uintptr_t)8192;
+    CHECK(mi_adamw_step_flat(&t, h, NULL, 4096, MI_ADAMW_STATE_F32, MI_ADAMW_F_AMSGRAD, 0,
+                             NULL) == MI_ADAMW_E_INVALID, "amsgrad without max_exp_avg_sq");
+    CHECK(mi_adamw_grad_norm_flat(NULL, 10, 4096, 1.0f, NULL, NULL, NULL, NULL) ==
+              MI_ADAMW_E_INVALID, "null gradient");
+    printf("abi_check cpu: ok (%s)\n", mi_adamw_version());
+    return 0;
+}
+
+/* ------------------------------------------------------------------ GPU */
+
+/* Flat range, fp32 state, fused clip (optionally amsgrad). */
+static void flat_case(int64_t n, int amsgrad)
+{
+    const size_t fb = (size_t)n * sizeof(float);
+    float *p = malloc(fb), *g = malloc(fb), *m = malloc(fb), *v = malloc(fb), *x = malloc(fb);
+    float *pr = malloc(fb), *mr = malloc(fb), *vr = malloc(fb), *xr = malloc(fb);
+    CHECK(p && g && m && v && x && pr && mr && vr && xr, "host allocation");
+    fill(p, n, 0.02f, 0);
+    fill(g, n, 1e-2f, 0); /* norm ~ 1e-2 sqrt(n/3) >> 1: the clip scales */
+    fill(m, n, 1e-3f, 0);
+    fill(v, n, 1e-6f, 1);
+    fill(x, n, 2e-6f, 1); /* running maximum above v on part of the elements */
+    memcpy(pr, p, fb);
+    memcpy(mr, m, fb);
+    memcpy(vr, v, fb);
+    memcpy(xr, x, fb);
+
+    float *dp = dev_copy(p, fb), *dg = dev_copy(g, fb), *dm = dev_copy(m, fb);
+    float *dv = dev_copy(v, fb), *dx = amsgrad ? dev_copy(x, fb) : NULL;
+    double *dpart = NULL;
+    float *dnorm = NULL, *dcoef = NULL;
+    HIP(hipMalloc((void **)&dpart, MI_ADAMW_MAX_NORM_BLOCKS * sizeof(double)));
+    HIP(hipMalloc((void **)&dnorm, sizeof(float)));
+    HIP(hipMalloc((void **)&dcoef, sizeof(float)));
+
+    mi_adamw_hyper h;
+    oracle_hyper oh;
+    scalars(3e-4, 0.9, 0.95, 1e-8, 0.1, 1001.0, 0, &h, &oh);
+    int rc = mi_adamw_grad_norm_flat(dg, n, 4096, 1.0f, dpart, dnorm, dcoef, NULL);
+    CHECK(rc == 0, "mi_adamw_grad_norm_flat: %s", mi_adamw_strerror(rc));
+    mi_adamw_tensor t;
+    memset(&t, 0, sizeof t);
+    t.param = dp;
+    t.grad = dg;
+    t.exp_avg = dm;
+    t.exp_avg_sq = dv;
+    t.max_exp_avg_sq = dx;
+    t.numel = n;
+    t.flags = MI_ADAMW_T_VEC; /* hipMalloc pointers are 256-byte aligned */
+    const int32_t flags = MI_ADAMW_F_CLIP | (amsgrad ? MI_ADAMW_F_AMSGRAD : 0);
+    rc = mi_adamw_step_flat(&t, &h, dcoef, 4096, MI_ADAMW_STATE_F32, flags, 0, NULL);
+    CHECK(rc == 0, "mi_adamw_step_flat: %s", mi_adamw_strerror(rc));
+    HIP(hipDeviceSynchronize());
+
+    float norm, coef;
+    back(&norm, dnorm, sizeof norm);
+    back(&coef, dcoef, sizeof coef);
+    const double ref = sqrt(oracle_sumsq_f64(g, n));
+    CHECK(fabs((double)norm - ref) <= 1e-6 * ref, "norm %.9g vs %.9g", norm, ref);
+    const float coef_ref = oracle_clip_coef(norm, 1.0);
+    CHECK(memcmp(&coef, &coef_ref, sizeof coef) == 0 && coef < 1.0f, "coef %.9g vs %.9g", coef,
+          coef_ref);
+    oracle_adamw_f32(pr, g, mr, vr, amsgrad ? xr : NULL, n, &oh, &ROCM_OPS, coef, 1);
+    back(p, dp, fb);
+    back(m, dm, fb);
+    back(v, dv, fb);
+    same_f32(p, pr, n, "param");
+    same_f32(m, mr, n, "exp_avg");
+    same_f32(v, vr, n, "exp_avg_sq");
+    if (amsgrad) {
+        back(x, dx, fb);
+        same_f32(x, xr, n, "max_exp_avg_sq");
+    }
+    printf("abi_check gpu: flat fp32 %s n=%lld: norm %.7g coef %.7g, bit-exact\n",
+           amsgrad ? "amsgrad + clip" : "clip", (long long)n, norm, coef);
+    HIP(hipFree(dp)); HIP(hipFree(dg)); HIP(hipFree(dm)); HIP(hipFree(dv));
+    if (dx) HIP(hipFree(dx));
+    HIP(hipFree(dpart)); HIP(hipFree(dnorm)); HIP(hipFree(dcoef));
+    free(p); free(g); free(m); free(v); free(x); free(pr); free(mr); free(vr); free(xr);
+}
+
+/* Tensor and chunk tables: three tensors, two hyper sets, bf16 moments, bf16 copy. */
+static void table_case(void)
+{
+    enum { NT = 3 };
+    const int64_t numel[NT] = {5, 3 * 4096 + 7, 70001};
+    mi_adamw_hyper h[2];
+    oracle_hyper oh[2];
+    scalars(3e-4, 0.9, 0.95, 1e-8, 0.1, 11.0, 0, &h[0], &oh[0]);
+    scalars(1e-3, 0.9, 0.999, 1e-8, 0.0, 3.0, 1, &h[1], &oh[1]); /* no decay, maximize */
+    const int32_t hyper_of[NT] = {1, 0, 0};
+
+    mi_adamw_tensor rows[NT];
+    float *p[NT], *g[NT], *pr[NT];
+    uint16_t *m[NT], *v[NT], *mr[NT], *vr[NT], *c[NT];
+    void *dp[NT], *dg[NT], *dm[NT], *dv[NT], *dc[NT];
+    for (int k = 0; k < NT; ++k) {
+        const int64_t n = numel[k];
+        p[k] = malloc(n * 4); g[k] = malloc(n * 4); pr[k] = malloc(n * 4);
+        m[k] = malloc(n * 2); v[k] = malloc(n * 2); mr[k] = malloc(n * 2); vr[k] = malloc(n * 2);
+        c[k] = malloc(n * 2);
+        CHECK(p[k] && g[k] && pr[k] && m[k] && v[k] && mr[k] && vr[k] && c[k], "host allocation");
+        fill(p[k], n, 0.02f, 0);
+        fill(g[k], n, 1e-3f, 0);
+        for (int64_t i = 0; i < n; ++i) {
+            m[k][i] = oracle_f32_to_bf16(urand() * 1e-3f);
+            v[k][i] = oracle_f32_to_bf16(fabsf(urand()) * 1e-6f);
+        }
+        memcpy(pr[k], p[k], n * 4);
+        memcpy(mr[k], m[k], n * 2);
+        memcpy(vr[k], v[k], n * 2);
+        dp[k] = dev_copy(p[k], n * 4);
+        dg[k] = dev_copy(g[k], n * 4);
+        dm[k] = dev_copy(m[k], n * 2);
+        dv[k] = dev_copy(v[k], n * 2);
+        HIP(hipMalloc(&dc[k], n * 2));
+        memset(&rows[k], 0, sizeof rows[k]);
+        rows[k].param = dp[k];
+        rows[k].grad = dg[k];
+        rows[k].exp_avg = dm[k];
+        rows[k].exp_avg_sq = dv[k];
+        rows[k].param_copy = dc[k];
+        rows[k].numel = n;
+        rows[k].hyper = hyper_of[k];
+        rows[k].flags = MI_ADAMW_T_VEC;
+    }
+    const int64_t n_chunks = mi_adamw_build_chunks(numel, NT, 4096, NULL, 0);
+    CHECK(n_chunks == 1 + 4 + 18, "chunk count %lld", (long long)n_chunks);
+    mi_adamw_chunk *chunks = malloc(n_chunks * sizeof *chunks);
+    CHECK(chunks && mi_adamw_build_chunks(numel, NT, 4096, chunks, n_chunks) == n_chunks,
+          "chunk table");
+    void *d_rows = dev_copy(rows, sizeof rows);
+    void *d_chunks = dev_copy(chunks, n_chunks * sizeof *chunks);
+    const int rc = mi_adamw_step(d_rows, d_chunks, n_chunks, 4096, h, 2, NULL,
+                                 MI_ADAMW_STATE_BF16, MI_ADAMW_F_BF16_COPY, 0, NULL);
+    CHECK(rc == 0, "mi_adamw_step: %s", mi_adamw_strerror(rc));
+    HIP(hipDeviceSynchronize());
+    for (int k = 0; k < NT; ++k) {
+        const int64_t n = numel[k];
+        oracle_adamw_bf16state(pr[k], g[k], mr[k], vr[k], NULL, n, &oh[hyper_of[k]], &ROCM_OPS,
+                               1.0f, 0);
+        back(p[k], dp[k], n * 4);
+        back(m[k], dm[k], n * 2);
+        back(v[k], dv[k], n * 2);
+        back(c[k], dc[k], n * 2);
+        same_f32(p[k], pr[k], n, "param (tables)");
+        same_u16(m[k], mr[k], n, "bf16 exp_avg");
+        same_u16(v[k], vr[k], n, "bf16 exp_avg_sq");
+        for (int64_t i = 0; i < n; ++i)
+            CHECK(c[k][i] == oracle_f32_to_bf16(pr[k][i]), "bf16 copy at %lld", (long long)i);
+        HIP(hipFree(dp[k])); HIP(hipFree(dg[k])); HIP(hipFree(dm[k])); HIP(hipFree(dv[k]));
+        HIP(hipFree(dc[k]));
+        free(p[k]); free(g[k]); free(pr[k]); free(m[k]); free(v[k]); free(mr[k]); free(vr[k]);
+        free(c[k]);
+    }
+    HIP(hipFree(d_rows));
+    HIP(hipFree(d_chunks));
+    free(chunks);
+    printf("abi_check gpu: tables, %d tensors, %lld chunks, bf16 state + copy: bit-exact\n", NT,
+           (long long)n_chunks);
+}
+
+static int gpu_checks(void)
+{
+    int count = 0;
+    HIP(hipGetDeviceCount(&count));
+    CHECK(count > 0, "no GPU");
+    HIP(hipSetDevice(0));
+    flat_case(1000003, 0);
+    table_case();
+    flat_case(262147, 1);
+    printf("abi_check gpu: ok (%s)\n", mi_adamw_version());
+    return 0;
+}
+
+int main(int argc, char **argv)
+{
+    if (argc == 2 && strcmp(argv[1], "cpu") == 0) return cpu_checks();
+    if (argc == 2 && strcmp(argv[1], "gpu") == 0) return gpu_checks();
+    fprintf(stderr, "usage: abi_check cpu|gpu\n");
+    return 2;
+}

@@ -72,7 +72,8 @@ def _build(src_text: str, out_dir: str, name: str) -> str:
     with open(c_path, "w") as f:
         f.write(src_text)
     subprocess.run(["gcc", "-O2", "-fPIC", "-ffp-contract=off", "-fno-fast-math", "-std=c11",
-                    "-shared", "-o", so_path, c_path, "-lm"], check=True)
+                    "-I", os.path.dirname(SOURCE), "-shared", "-o", so_path, c_path, "-lm"],
+                   check=True)
     return so_path
 
 
