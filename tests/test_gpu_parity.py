@@ -406,3 +406,36 @@ def test_clip_step_is_deterministic(dev):
         assert torch.equal(a.view(torch.int32), b.view(torch.int32))
     for a, b in zip(runs[0][1], runs[1][1]):
         assert torch.equal(a.view(torch.int32), b.view(torch.int32))
+
+
+def test_step_on_a_side_stream(dev):
+    """step() enqueues on the current stream, tables and clip included: a side stream
+    gives the same bits as the default one (ordering against the grads' producer is the
+    caller's, as for any torch op)."""
+    import mi_adamw
+    runs = []
+    for use_side in (False, True):
+        params = make_params(MINI_SHAPES, dev)
+        opt = mi_adamw.FusedAdamW(params, lr=3e-4, betas=(0.9, 0.95), weight_decay=0.1,
+                                  max_grad_norm=1.0, bf16_copy=True)
+        load_states(opt, params, midtrain_state(params, 100.0))
+        side = torch.cuda.Stream(device=dev)
+        for step in range(3):
+            set_grads(params, step, 1e-2)
+            if use_side:
+                side.wait_stream(torch.cuda.current_stream(dev))
+                with torch.cuda.stream(side):
+                    opt.step()
+                    norm = opt.last_grad_norm.clone()
+                torch.cuda.current_stream(dev).wait_stream(side)
+            else:
+                opt.step()
+                norm = opt.last_grad_norm.clone()
+        torch.cuda.synchronize()
+        runs.append(([p.detach().clone() for p in params], [c.clone() for c in opt.bf16_params()],
+                     norm))
+    for a, b in zip(runs[0][0], runs[1][0]):
+        assert torch.equal(a.view(torch.int32), b.view(torch.int32))
+    for a, b in zip(runs[0][1], runs[1][1]):
+        assert torch.equal(a.view(torch.int16), b.view(torch.int16))
+    assert torch.equal(runs[0][2], runs[1][2])
