@@ -439,3 +439,42 @@ def test_step_on_a_side_stream(dev):
     for a, b in zip(runs[0][1], runs[1][1]):
         assert torch.equal(a.view(torch.int16), b.view(torch.int16))
     assert torch.equal(runs[0][2], runs[1][2])
+
+
+def test_special_values_match_torch(dev):
+    """Denormals, signed zeros, tiny and huge magnitudes, inf and NaN in p, g, m and v:
+    the kernel keeps fp32 denormals and follows torch's per-op chain through all of them."""
+    import mi_adamw
+    specials = torch.tensor([0.0, -0.0, 1e-45, -1e-45, 1e-40, -3e-39, 1.17e-38, 1e-30, -1e-20,
+                             1e-8, 1.0, -1.0, 3e4, -1e15, 1e30, 3.4e38, float("inf"),
+                             float("-inf"), float("nan")], dtype=torch.float32)
+    k = specials.numel()
+    # every combination of a special p, g, m and |v| (v >= 0 as in real state)
+    idx = torch.cartesian_prod(*(torch.arange(k) for _ in range(4)))
+    pv, gv, mv, vv = (specials[idx[:, j]] for j in range(4))
+    vv = vv.abs()
+    n = idx.shape[0]
+    for betas, step, maximize in (((0.9, 0.95), 1.0, False), ((0.3, 0.999), 7.0, True)):
+        ref = [torch.nn.Parameter(pv.clone().to(dev))]
+        ours = [torch.nn.Parameter(pv.clone().to(dev))]
+        ref[0].grad = gv.clone().to(dev)
+        ours[0].grad = gv.clone().to(dev)
+        hp = dict(lr=1e-3, betas=betas, eps=1e-8, weight_decay=0.1, maximize=maximize)
+        topt = torch.optim.AdamW(ref, foreach=False, **hp)
+        oopt = mi_adamw.FusedAdamW(ours, **hp)
+        st = [{"step": torch.tensor(step - 1), "exp_avg": mv.clone().to(dev),
+               "exp_avg_sq": vv.clone().to(dev)}]
+        load_states(topt, ref, st)
+        load_states(oopt, ours, st)
+        topt.step()
+        oopt.step()
+        torch.cuda.synchronize()
+        for a, b, what in ((ref[0], ours[0], "p"),
+                           (topt.state[ref[0]]["exp_avg"], oopt.state[ours[0]]["exp_avg"], "m"),
+                           (topt.state[ref[0]]["exp_avg_sq"], oopt.state[ours[0]]["exp_avg_sq"], "v")):
+            a, b = a.detach(), b.detach()
+            nan_a, nan_b = torch.isnan(a), torch.isnan(b)
+            assert torch.equal(nan_a, nan_b), what
+            same = torch.equal(a[~nan_a].view(torch.int32), b[~nan_b].view(torch.int32))
+            assert same, (what, betas, int((a[~nan_a] != b[~nan_b]).sum()))
+        print(f"{n} special combinations, betas {betas}: identical", flush=True)
