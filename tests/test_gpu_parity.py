@@ -478,3 +478,36 @@ def test_special_values_match_torch(dev):
             same = torch.equal(a[~nan_a].view(torch.int32), b[~nan_b].view(torch.int32))
             assert same, (what, betas, int((a[~nan_a] != b[~nan_b]).sum()))
         print(f"{n} special combinations, betas {betas}: identical", flush=True)
+
+
+def test_special_values_bf16_state_match_oracle(dev):
+    """The special-value grid with bf16 moments (and a bf16 copy), against the oracle's
+    bf16-state model: bf16 rounding of inf, NaN (0x7FC0), denormals and overflow to inf."""
+    import mi_adamw
+    specials = torch.tensor([0.0, -0.0, 1e-45, -1e-40, 9.2e-41, 1.17e-38, 1e-30, -1e-20, 1e-8,
+                             1.0, -1.0, 3e4, 3.3961e38, 3.4e38, float("inf"), float("-inf"),
+                             float("nan")], dtype=torch.float32)
+    k = specials.numel()
+    idx = torch.cartesian_prod(*(torch.arange(k) for _ in range(4)))
+    pv, gv, mv, vv = (specials[idx[:, j]] for j in range(4))
+    vv = vv.abs()
+    p = torch.nn.Parameter(pv.clone().to(dev))
+    p.grad = gv.clone().to(dev)
+    opt = mi_adamw.FusedAdamW([p], lr=1e-3, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.1,
+                              state_dtype=torch.bfloat16, bf16_copy=True)
+    load_states(opt, [p], [{"step": torch.tensor(4.0), "exp_avg": mv.clone(),
+                            "exp_avg_sq": vv.clone()}])
+    opt.step()
+    torch.cuda.synchronize()
+    pn = pv.numpy().copy()
+    mb = O.to_bf16_bits(mv.numpy())
+    vb = O.to_bf16_bits(vv.numpy())
+    O.adamw_step_bf16state(pn, gv.numpy().copy(), mb, vb, lr=1e-3, betas=(0.9, 0.95), eps=1e-8,
+                           weight_decay=0.1, step=5.0)
+    assert O.max_ulp(pn, to_np(p))[0] == 0
+    got_m = to_np(opt.state[p]["exp_avg"].view(torch.int16)).view(np.uint16)
+    got_v = to_np(opt.state[p]["exp_avg_sq"].view(torch.int16)).view(np.uint16)
+    assert np.array_equal(got_m, mb) and np.array_equal(got_v, vb)
+    copy = to_np(opt.bf16_param(p).view(torch.int16)).view(np.uint16)
+    assert np.array_equal(copy, O.to_bf16_bits(pn))
+    print(f"{idx.shape[0]} special combinations with bf16 state: identical to the oracle", flush=True)
