@@ -248,54 +248,69 @@ def cpu_baseline(name: str, budget_s: float = 20.0) -> dict:
     }
 
 
-def bf16_forward_rows(device, batch: int = 4, iters: int = 20, warmup: int = 5,
-                      rounds: int = 3) -> dict:
-    """One training iteration of the reference GPT-125M (12 x 768, 12 heads, FFN 3072,
-    vocab 50304, batch x 512 tokens; main.py:202-209 with --amp), timed with plain bf16
-    autocast and with mi_adamw.bf16_weights, alternating on the same model."""
+def training_rows(device, batch: int, variants, iters: int = 20, warmup: int = 5,
+                  rounds: int = 3) -> dict:
+    """Training iterations of the reference GPT-125M (12 x 768, 12 heads, FFN 3072, vocab
+    50304, batch x 512 tokens) as main.py:202-209 runs them with --amp: zero_grad, forward
+    under bf16 autocast, backward, optimizer step.  Each variant is an optimizer choice on
+    its own copy of the model (same initialisation); variants alternate round by round."""
     import contextlib
     sys.path.insert(0, os.path.join(ROOT, "tests"))
     import refgpt
     from mi_adamw import FusedAdamW, bf16_weights
-    torch.manual_seed(0)
-    model = refgpt.GPT(vocab=50304, h=768, heads=12, ffn=3072, layers=12, seq=512).to(device)
-    opt = FusedAdamW(model.parameters(), **HP, bf16_copy=True, max_grad_norm=1.0)
+    ref_hp = dict(lr=6e-4, weight_decay=0.1)          # config.py:11,13; default betas and eps
+    makers = {
+        "torch_single_tensor": lambda ps: torch.optim.AdamW(ps, **ref_hp, fused=False),
+        "torch_fused": lambda ps: torch.optim.AdamW(ps, **ref_hp, fused=True),
+        "mi_adamw": lambda ps: FusedAdamW(ps, **ref_hp, fused=False),
+        "mi_adamw_bf16_weights": lambda ps: FusedAdamW(ps, **ref_hp, fused=False, bf16_copy=True),
+    }
     ids, labels, mask = refgpt.batch(device, b=batch, s=512, vocab=50304)
-    n_linear = sum(1 for m in model.modules() if isinstance(m, refgpt.ColumnLinear))
+    runs = {}
+    for name in variants:
+        torch.manual_seed(0)
+        model = refgpt.GPT(vocab=50304, h=768, heads=12, ffn=3072, layers=12, seq=512).to(device)
+        runs[name] = (model, makers[name](model.parameters()))
+    n_linear = sum(1 for m in runs[variants[0]][0].modules() if isinstance(m, refgpt.ColumnLinear))
 
-    def iteration(use):
+    def iteration(name):
+        model, opt = runs[name]
         opt.zero_grad()
-        ctx = bf16_weights(opt, model) if use else contextlib.nullcontext()
+        ctx = (bf16_weights(opt, model) if name == "mi_adamw_bf16_weights"
+               else contextlib.nullcontext())
         with torch.autocast("cuda", dtype=torch.bfloat16), ctx:
             _, loss = model(ids, labels, mask)
         loss.backward()
         opt.step()
 
-    times = {False: [], True: []}
-    for use in (False, True):
+    times = {name: [] for name in variants}
+    for name in variants:
         for _ in range(warmup):
-            iteration(use)
+            iteration(name)
     torch.cuda.synchronize()
     for _ in range(rounds):
-        for use in (False, True):
+        for name in variants:
             evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
                    for _ in range(iters)]
             for e0, e1 in evs:
                 e0.record()
-                iteration(use)
+                iteration(name)
                 e1.record()
             torch.cuda.synchronize()
-            times[use] += [e0.elapsed_time(e1) for e0, e1 in evs]
-    plain, ours = statistics.median(times[False]), statistics.median(times[True])
-    del model, opt
+            times[name] += [e0.elapsed_time(e1) for e0, e1 in evs]
+    del runs
     torch.cuda.empty_cache()
+    rows = {}
+    for name in variants:
+        ms = statistics.median(times[name])
+        rows[name] = {"ms_per_iteration": round(ms, 4),
+                      "tokens_per_s": round(batch * 512 / ms * 1e3, 1)}
     return {
-        "workload": "gpt-125m training iteration (fwd + bwd + fused clip/AdamW step, "
-                    f"bf16 autocast, {batch} x 512 tokens)",
-        "iterations": rounds * iters,
-        "plain_autocast_ms": round(plain, 4), "bf16_weights_ms": round(ours, 4),
-        "saved_ms": round(plain - ours, 4), "saved_pct": round(100 * (plain - ours) / plain, 2),
-        "weight_casts_removed_per_forward": n_linear,
+        "workload": f"gpt-125m training iteration, bf16 autocast, {batch} x 512 tokens "
+                    "(zero_grad, forward, backward, AdamW step)",
+        "iterations_per_variant": rounds * iters,
+        "weight_casts_removed_per_forward_by_bf16_weights": n_linear,
+        "variants": rows,
     }
 
 
@@ -351,9 +366,9 @@ def main() -> int:
                     help="one of %s, or 'all'" % ", ".join(CONFIGS))
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-context", action="store_true", help="skip torch's GPU rows")
-    ap.add_argument("--bf16-forward", action="store_true",
-                    help="also time a gpt-125m training iteration with plain bf16 autocast "
-                         "against mi_adamw.bf16_weights (the step's bf16 copies as GEMM weights)")
+    ap.add_argument("--training", action="store_true",
+                    help="also time gpt-125m training iterations (bf16 autocast) with torch's "
+                         "per-tensor and fused AdamW, FusedAdamW, and FusedAdamW + bf16_weights")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="after the timed steps, run 3 plain 1 GiB device copies (torch copy_) "
                          "so a counter run (rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE) sees a "
@@ -428,11 +443,16 @@ def main() -> int:
     if len(results) > 1:
         line["sweep"] = [{k: (round(v, 5) if isinstance(v, float) else v) for k, v in r.items()
                           if k != "torch_gpu"} for r in results]
-    if args.bf16_forward:
-        log("[bench] gpt-125m training iteration: plain autocast vs bf16_weights")
-        # the reference's micro-batch (config.py:9), then a GPU-bound one
-        line["bf16_forward"] = [bf16_forward_rows(device, batch=b) for b in (4, 16)]
-        for row in line["bf16_forward"]:
+    if args.training:
+        log("[bench] gpt-125m training iterations by optimizer")
+        # the reference's micro-batch (config.py:9) with every optimizer, then a GPU-bound
+        # batch for the bf16 copies against autocast's casts
+        line["training"] = [
+            training_rows(device, 4, ["torch_single_tensor", "torch_fused", "mi_adamw",
+                                      "mi_adamw_bf16_weights"]),
+            training_rows(device, 16, ["mi_adamw", "mi_adamw_bf16_weights"]),
+        ]
+        for row in line["training"]:
             log(f"[bench] {row}")
     if not args.no_cpu:
         log("[bench] CPU baseline (torch.optim.AdamW foreach=False on host cores)")

@@ -33,10 +33,9 @@ def _ws(device):
 
 
 def _tables(grads, device):
-    key = tuple(g.data_ptr() for g in grads) + tuple(g.numel() for g in grads)
-    hit = _cache.get(key)
-    if hit is not None:
-        return hit
+    """The tables of one gradient list.  The chunk table depends on the sizes only and is
+    cached by them; when the gradients moved (zero_grad freed them and backward allocated
+    them elsewhere) only the rows are rewritten."""
     from .optimizer import _ROW_DTYPE, _Launch
     rows = np.zeros(len(grads), dtype=_ROW_DTYPE)
     ptrs = np.array([g.data_ptr() for g in grads], dtype=np.uint64)
@@ -46,6 +45,12 @@ def _tables(grads, device):
     rows["numel"] = [g.numel() * (2 if torch.is_complex(g) else 1) for g in grads]
     rows["flags"] = np.where(ptrs % 16 == 0, _lib.T_VEC, 0)
     rows = rows[rows["numel"] > 0]
+    key = (device, tuple(int(n) for n in rows["numel"]))
+    launch = _cache.get(key)
+    if launch is not None:
+        if not np.array_equal(launch.host_rows["grad"], rows["grad"]):
+            launch.set_rows(rows, device)
+        return launch
     launch = _Launch(rows, _CHUNK, device, tables=True)
     if len(_cache) > 8:
         _cache.clear()

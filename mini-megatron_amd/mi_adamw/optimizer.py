@@ -102,17 +102,34 @@ class _Rec:
         self.st = None
 
 
+def _upload(arr: np.ndarray, device: torch.device) -> torch.Tensor:
+    """A host array as a new device tensor, copied from pinned memory without blocking
+    the host: the copy is ordered on the current stream, before the launches that
+    read it, and torch keeps the pinned block until the copy has run.  (A CPU device,
+    where only the host-side table logic runs, gets a plain copy.)"""
+    host = torch.from_numpy(arr.view(np.uint8))
+    if device.type != "cuda":
+        return host.clone()
+    return host.pin_memory().to(device, non_blocking=True)
+
+
 class _Launch:
     """Device-resident tensor and chunk tables for one kernel launch."""
 
-    __slots__ = ("rows", "chunks", "n_chunks", "n_rows", "host_rows")
+    __slots__ = ("rows", "chunks", "n_chunks", "n_rows", "host_rows", "tables", "src", "rest")
 
     def __init__(self, rows: np.ndarray, chunk_elems: int, device: torch.device,
-                 tables: bool = False):
+                 tables: bool = False, src: np.ndarray | None = None,
+                 rest: np.ndarray | None = None):
         lib = _lib.load()
         self.n_rows = len(rows)
         self.host_rows = rows.copy()
-        if len(rows) == 1 and not tables:
+        self.tables = tables or len(rows) != 1
+        # src[i]: the entry whose gradient row i points at (-1: a flat group row, whose
+        # gradient buffer never moves); rest[i]: row i's other pointers are aligned
+        self.src = src
+        self.rest = rest
+        if not self.tables:
             # One contiguous range: launched through the flat entry points,
             # which derive chunk bounds arithmetically and need no tables.
             self.n_chunks = -(-int(rows["numel"][0]) // chunk_elems)
@@ -127,8 +144,31 @@ class _Launch:
         if n2 != n:
             raise _lib.MiAdamwError("mi_adamw_build_chunks: inconsistent chunk count")
         self.n_chunks = int(n)
-        self.rows = torch.from_numpy(rows.view(np.uint8).copy()).to(device)
-        self.chunks = torch.from_numpy(chunks.view(np.uint8)).to(device)
+        self.rows = _upload(self.host_rows, device)
+        self.chunks = _upload(chunks, device)
+
+    def set_rows(self, rows: np.ndarray, device: torch.device) -> bool:
+        """New pointers for the same tensors (the gradients moved): replace the rows,
+        keep the chunk table.  False if the tensor sizes differ (rebuild instead)."""
+        if len(rows) != self.n_rows or not np.array_equal(rows["numel"], self.host_rows["numel"]):
+            return False
+        self.host_rows = rows.copy()
+        if self.tables:
+            # a new buffer: a launch still queued on another stream keeps reading the old one
+            self.rows = _upload(self.host_rows, device)
+        return True
+
+    def patch_grads(self, grads: np.ndarray, device: torch.device) -> None:
+        """The gradients moved: write their addresses (grads[src[i]] for row i) into
+        the rows and recompute the alignment flag; everything else stays."""
+        rows = self.host_rows.copy()
+        m = self.src >= 0
+        g = grads[self.src[m]]
+        rows["grad"][m] = g
+        rows["flags"][m] = np.where(self.rest[m] & (g % 16 == 0), _lib.T_VEC, 0)
+        self.host_rows = rows
+        if self.tables:
+            self.rows = _upload(rows, device)
 
 
 class FusedAdamW(Optimizer):
@@ -595,17 +635,23 @@ class FusedAdamW(Optimizer):
             ws = self._workspace[device] = (partials, coef)
         return ws
 
-    def _rows(self, entries, hyper_idx, ams) -> np.ndarray:
+    def _rows(self, entries, hyper_idx, ams):
+        """(rows, src, rest): the table rows of `entries`, the entry each row's gradient
+        belongs to (-1 for a flat group row) and whether its other pointers are aligned."""
         if self._flat is not None:
             return self._flat_rows(entries, hyper_idx, ams)
         return self._tensor_rows(entries, hyper_idx, ams)
 
-    def _flat_rows(self, entries, hyper_idx, ams) -> np.ndarray:
+    def _new_launch(self, entries, hyper_idx, ams, device) -> _Launch:
+        rows, src, rest = self._rows(entries, hyper_idx, ams)
+        return _Launch(rows, self.chunk_elems, device, src=src, rest=rest)
+
+    def _flat_rows(self, entries, hyper_idx, ams):
         """One row per param group whose every param steps with one hyper set."""
         by_group: dict[int, list[int]] = {}
         for i, (rec, _) in enumerate(entries):
             by_group.setdefault(rec.gi, []).append(i)
-        rows = []
+        rows, srcs, rests = [], [], []
         for gi, idx in by_group.items():
             hs = {hyper_idx[i] for i in idx}
             if len(idx) == len(self.param_groups[gi]["params"]) and len(hs) == 1:
@@ -613,10 +659,17 @@ class FusedAdamW(Optimizer):
                 r = np.zeros(1, dtype=_ROW_DTYPE)
                 r[0] = (pp, gp, mp, vp, cp, xp, n, hs.pop(), _lib.T_VEC)
                 rows.append(r)
+                srcs.append(np.full(1, -1, dtype=np.int64))
+                rests.append(np.ones(1, dtype=bool))
             else:
-                rows.append(self._tensor_rows([entries[i] for i in idx],
-                                              [hyper_idx[i] for i in idx], ams))
-        return np.concatenate(rows) if rows else np.zeros(0, dtype=_ROW_DTYPE)
+                r, src, rest = self._tensor_rows([entries[i] for i in idx],
+                                                 [hyper_idx[i] for i in idx], ams)
+                rows.append(r)
+                srcs.append(np.asarray(idx, dtype=np.int64)[src])
+                rests.append(rest)
+        if not rows:
+            return np.zeros(0, dtype=_ROW_DTYPE), np.zeros(0, np.int64), np.zeros(0, bool)
+        return np.concatenate(rows), np.concatenate(srcs), np.concatenate(rests)
 
     def _state_tensor(self, p: torch.Tensor, st: dict, key: str) -> torch.Tensor:
         """st[key] as the kernel reads it: p's element count, state dtype, p's
@@ -632,8 +685,9 @@ class FusedAdamW(Optimizer):
                                    memory_format=torch.contiguous_format)
         return t
 
-    def _tensor_rows(self, entries, hyper_idx, ams) -> np.ndarray:
+    def _tensor_rows(self, entries, hyper_idx, ams):
         rows = np.zeros(len(entries), dtype=_ROW_DTYPE)
+        rest = np.zeros(len(entries), dtype=bool)
         bf16_state = self.state_dtype == torch.bfloat16
         for i, ((rec, g), h) in enumerate(zip(entries, hyper_idx)):
             p, st = rec.p, rec.st
@@ -648,10 +702,12 @@ class FusedAdamW(Optimizer):
             xp = self._state_tensor(p, st, "max_exp_avg_sq").data_ptr() if ams else 0
             n = p.numel() * (2 if torch.is_complex(p) else 1)
             sa = 8 if bf16_state else 16
-            vec = (pp % 16 == 0 and gp % 16 == 0 and mp % sa == 0 and vp % sa == 0
-                   and cp % 8 == 0 and xp % sa == 0)
+            rest[i] = (pp % 16 == 0 and mp % sa == 0 and vp % sa == 0 and cp % 8 == 0
+                       and xp % sa == 0)
+            vec = rest[i] and gp % 16 == 0
             rows[i] = (pp, gp, mp, vp, cp, xp, n, h, _lib.T_VEC if vec else 0)
-        return rows[rows["numel"] > 0]
+        keep = rows["numel"] > 0
+        return rows[keep], np.flatnonzero(keep).astype(np.int64), rest[keep]
 
     def _copy_for(self, p):
         if self._flat is not None:
@@ -659,19 +715,18 @@ class FusedAdamW(Optimizer):
         return self._copies[id(p)]
 
     @staticmethod
-    def _signature(entries, hyper_idx) -> list:
-        """Everything a launch's tables encode: the pointers of each entry.
-
-        The grads are usually new tensors every step (zero_grad sets them to
-        None), so they are compared by address, as are params and moments.
-        """
+    def _signature(entries, hyper_idx) -> tuple[list, list]:
+        """What a launch's tables encode, in two parts: the hyperparameter assignment
+        and the parameter and state pointers, which rarely change; and the gradient
+        pointers, which change whenever zero_grad() frees the gradients and backward
+        allocates them elsewhere."""
         sig = list(hyper_idx)
-        for rec, g in entries:
+        for rec, _ in entries:
             st = rec.st
             x = st.get("max_exp_avg_sq")
-            sig += (rec.p.data_ptr(), g.data_ptr(), st["exp_avg"].data_ptr(),
-                    st["exp_avg_sq"].data_ptr(), 0 if x is None else x.data_ptr())
-        return sig
+            sig += (rec.p.data_ptr(), st["exp_avg"].data_ptr(), st["exp_avg_sq"].data_ptr(),
+                    0 if x is None else x.data_ptr())
+        return sig, [g.data_ptr() for _, g in entries]
 
     @staticmethod
     def _row_struct(launch: _Launch) -> _lib.TensorRow:
@@ -695,7 +750,7 @@ class FusedAdamW(Optimizer):
         # hyperparameter sets each.
         n_ams = sum(hyper_ams)
         if len(hypers) <= _lib.MAX_HYPER and n_ams in (0, len(hypers)):
-            parts = [(entries, hyper_idx, hypers, n_ams > 0)]
+            parts = [(entries, hyper_idx, hypers, n_ams > 0, None)]
         else:
             parts = []
             for ams in (False, True):
@@ -706,26 +761,39 @@ class FusedAdamW(Optimizer):
                     sel = [i for i, h in enumerate(hyper_idx) if h in remap]
                     parts.append(([entries[i] for i in sel],
                                   [remap[hyper_idx[i]] for i in sel],
-                                  [hypers[h] for h in block], ams))
+                                  [hypers[h] for h in block], ams,
+                                  np.asarray(sel, dtype=np.int64)))
 
-        # Tables: reused while pointers and hyperparameter assignment are unchanged.
-        sig = self._signature(entries, hyper_idx)
+        # Tables: reused while the pointers and the hyperparameter assignment are
+        # unchanged; when only the gradients moved, the rows are rewritten and the
+        # chunk tables kept.
+        sig, grads = self._signature(entries, hyper_idx)
         cache = self._launch_cache
         if cache is not None and cache[0] == sig and cache[1] == device:
             launches, norm_launch = cache[2], cache[3]
+            if cache[4] != grads:
+                # torch checks shape, dtype and device when .grad is assigned; the
+                # kernels also need dense storage
+                for rec, g in entries:
+                    if not g.is_contiguous():
+                        self._check_param(rec.p, g)
+                garr = np.asarray(grads, dtype=np.uint64)
+                for launch, part in zip(launches, parts):
+                    launch.patch_grads(garr if part[4] is None else garr[part[4]], device)
+                if norm_launch is not launches[0]:
+                    norm_launch.patch_grads(garr, device)
+                self._launch_cache = (sig, device, launches, norm_launch, grads)
         else:
             for rec, g in entries:
                 self._check_param(rec.p, g)
                 if rec.p.device != device:
                     raise NotImplementedError("FusedAdamW: all parameters must be on one device")
-            launches = [_Launch(self._rows(e, hi, a), self.chunk_elems, device)
-                        for e, hi, _, a in parts]
+            launches = [self._new_launch(e, hi, a, device) for e, hi, _, a, _ in parts]
             if len(parts) == 1:
                 norm_launch = launches[0]
             else:
-                norm_launch = _Launch(self._rows(entries, [0] * len(entries), False),
-                                      self.chunk_elems, device)
-            self._launch_cache = (sig, device, launches, norm_launch)
+                norm_launch = self._new_launch(entries, [0] * len(entries), False, device)
+            self._launch_cache = (sig, device, launches, norm_launch, grads)
 
         ev = self.timing_events
         if ev is not None:
@@ -753,7 +821,7 @@ class FusedAdamW(Optimizer):
                 flags |= _lib.F_WRITE_GRAD
         if ev is not None:
             ev[1].record()
-        for launch, (_, _, hs, ams) in zip(launches, parts):
+        for launch, (_, _, hs, ams, _) in zip(launches, parts):
             if launch.n_chunks == 0:
                 continue
             lflags = flags | (_lib.F_AMSGRAD if ams else 0)

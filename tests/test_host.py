@@ -221,8 +221,8 @@ def test_table_rows_are_built_field_by_field_on_cpu():
         rec.st = opt.state[p]
         opt._init_state(p, rec.st, gi == 0)
         entries.append((rec, torch.zeros_like(p)))
-    ams_rows = opt._tensor_rows(entries[:1], [0], True)
-    plain_rows = opt._tensor_rows(entries[1:], [0], False)
+    ams_rows = opt._tensor_rows(entries[:1], [0], True)[0]
+    plain_rows = opt._tensor_rows(entries[1:], [0], False)[0]
     st0, st1 = opt.state[params[0]], opt.state[params[1]]
     assert ams_rows["max_exp_avg_sq"][0] == st0["max_exp_avg_sq"].data_ptr() != 0
     assert ams_rows["exp_avg_sq"][0] == st0["exp_avg_sq"].data_ptr()
@@ -236,9 +236,56 @@ def test_table_rows_are_built_field_by_field_on_cpu():
     with pytest.raises(RuntimeError, match="elements"):
         opt._tensor_rows(entries[1:], [0], False)
     st1["exp_avg"] = torch.zeros(10, dtype=torch.float64)[::2]
-    rows = opt._tensor_rows(entries[1:], [0], False)
+    rows = opt._tensor_rows(entries[1:], [0], False)[0]
     assert st1["exp_avg"].dtype == torch.float32 and st1["exp_avg"].is_contiguous()
     assert rows["exp_avg"][0] == st1["exp_avg"].data_ptr()
+
+
+def test_launch_rows_refresh_keeps_the_chunk_table():
+    """When only pointers move, a launch takes new rows and keeps its chunk table; a
+    change of tensor sizes is refused, so the caller rebuilds."""
+    from mi_adamw.optimizer import _ROW_DTYPE, _Launch
+    rows = np.zeros(3, dtype=_ROW_DTYPE)
+    rows["grad"] = [4096, 8192, 12288]
+    rows["numel"] = [5, 4097, 9000]
+    launch = _Launch(rows, 4096, torch.device("cpu"))
+    chunks = launch.chunks
+    assert launch.n_chunks == 1 + 2 + 3
+    moved = rows.copy()
+    moved["grad"] = [65536, 131072, 196608]
+    assert launch.set_rows(moved, torch.device("cpu"))
+    assert launch.chunks is chunks
+    assert list(launch.host_rows["grad"]) == [65536, 131072, 196608]
+    assert bytes(launch.rows.numpy()) == moved.tobytes()
+    resized = moved.copy()
+    resized["numel"][1] = 4096
+    assert not launch.set_rows(resized, torch.device("cpu"))
+
+
+def test_moved_gradients_are_patched_into_the_rows():
+    """Only the gradient column (and its alignment flag) changes when gradients move;
+    empty tensors have no row, so rows map back to their entries."""
+    from mi_adamw.optimizer import _Rec
+    params = [torch.nn.Parameter(torch.zeros(n)) for n in (6, 0, 4097)]
+    opt = mi_adamw.FusedAdamW(params)
+    entries = []
+    for p in params:
+        rec = _Rec(0, p, opt._slots[id(p)])
+        rec.st = opt.state[p]
+        opt._init_state(p, rec.st, False)
+        entries.append((rec, torch.zeros_like(p)))
+    launch = opt._new_launch(entries, [0, 0, 0], False, torch.device("cpu"))
+    assert list(launch.src) == [0, 2] and launch.n_rows == 2
+    before = launch.host_rows.copy()
+    chunks = launch.chunks
+    new = np.array([1 << 20, 2 << 20, (3 << 20) + 4], dtype=np.uint64)   # the last misaligned
+    launch.patch_grads(new, torch.device("cpu"))
+    rows = launch.host_rows
+    assert list(rows["grad"]) == [1 << 20, (3 << 20) + 4]
+    assert list(rows["flags"]) == [_lib.T_VEC, 0]
+    for f in ("param", "exp_avg", "exp_avg_sq", "numel", "hyper"):
+        assert np.array_equal(rows[f], before[f])
+    assert launch.chunks is chunks and bytes(launch.rows.numpy()) == rows.tobytes()
 
 
 def test_build_chunks_helper():
