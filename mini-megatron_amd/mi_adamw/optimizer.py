@@ -559,15 +559,12 @@ class FusedAdamW(Optimizer):
                 loss = closure()
 
         # Gather params with grads (adam.py:148-153) and initialise their state.
-        entries = []   # (record, grad)
-        for rec in self._records():
-            g = rec.p.grad
-            if g is not None:
-                entries.append((rec, g))
+        entries = [(rec, g) for rec in self._records() if (g := rec.p.grad) is not None]
         if not entries:
             return loss
         flat = self._flat
         ams_g = [bool(g["amsgrad"]) for g in self.param_groups]
+        views = self._step_views
         for i, (rec, g) in enumerate(entries):
             if flat is not None and not flat.is_grad_view(rec.p, g):
                 self._check_param(rec.p, g)
@@ -583,7 +580,7 @@ class FusedAdamW(Optimizer):
             if len(st) == 0:
                 self._check_param(rec.p, g)
                 self._init_state(rec.p, st, ams_g[rec.gi])
-            elif st["step"] is not self._step_views[rec.slot]:
+            elif st["step"] is not views[rec.slot]:
                 self._adopt_step(rec.p, st, rec.slot)
             if ams_g[rec.gi] and "max_exp_avg_sq" not in st:
                 # amsgrad switched on for a group after its state was created
@@ -599,13 +596,18 @@ class FusedAdamW(Optimizer):
 
         # One hyperparameter set per distinct (group, step value).
         keys: dict[tuple[int, float], int] = {}
-        hyper_idx = []
-        for rec, _ in entries:
-            k = (rec.gi, float(steps_np[rec.slot]))
-            h = keys.get(k)
-            if h is None:
-                h = keys[k] = len(keys)
-            hyper_idx.append(h)
+        sel = steps_np[[rec.slot for rec, _ in entries]]
+        if len(self.param_groups) == 1 and sel.min() == sel.max():
+            keys[(0, float(sel[0]))] = 0          # the usual case: one set for everything
+            hyper_idx = [0] * len(entries)
+        else:
+            hyper_idx = []
+            for (rec, _), step in zip(entries, sel.tolist()):
+                k = (rec.gi, step)
+                h = keys.get(k)
+                if h is None:
+                    h = keys[k] = len(keys)
+                hyper_idx.append(h)
         hypers = [_hyper(self.param_groups[gi], step) for (gi, step) in keys]
         hyper_ams = [ams_g[gi] for (gi, _) in keys]
 
@@ -720,12 +722,9 @@ class FusedAdamW(Optimizer):
         and the parameter and state pointers, which rarely change; and the gradient
         pointers, which change whenever zero_grad() frees the gradients and backward
         allocates them elsewhere."""
-        sig = list(hyper_idx)
-        for rec, _ in entries:
-            st = rec.st
-            x = st.get("max_exp_avg_sq")
-            sig += (rec.p.data_ptr(), st["exp_avg"].data_ptr(), st["exp_avg_sq"].data_ptr(),
-                    0 if x is None else x.data_ptr())
+        sig = [(rec.p.data_ptr(), rec.st["exp_avg"].data_ptr(), rec.st["exp_avg_sq"].data_ptr(),
+                _ptr(rec.st.get("max_exp_avg_sq"))) for rec, _ in entries]
+        sig.append(tuple(hyper_idx))
         return sig, [g.data_ptr() for _, g in entries]
 
     @staticmethod
