@@ -119,6 +119,14 @@ __device__ __forceinline__ void adamw_elem(float& p, float g, float& m, float& v
 __device__ __forceinline__ f32x4 ld4(const float* p) {
     return __builtin_nontemporal_load((const GLOBAL f32x4*)(p));
 }
+// Norm-pass loads.  kKeep: an ordinary load, which allocates the line in the
+// memory-side cache (MI355X Infinity Cache), so that the update pass right after
+// finds it there; otherwise a streaming (nontemporal) load.
+template <bool kKeep>
+__device__ __forceinline__ f32x4 ld4_norm(const float* p) {
+    if (kKeep) return *(const GLOBAL f32x4*)(p);
+    return __builtin_nontemporal_load((const GLOBAL f32x4*)(p));
+}
 __device__ __forceinline__ void st4(float* p, f32x4 v) {
     __builtin_nontemporal_store(v, (GLOBAL f32x4*)(p));
 }
@@ -280,15 +288,17 @@ __device__ __forceinline__ void sumsq4(f32x4 a, double& acc0, double& acc1) {
     acc1 += (double)a.z * a.z + (double)a.w * a.w;
 }
 
-template <class Src>
-__global__ __launch_bounds__(kNormThreads) void mi_adamw_sumsq_kernel(
-    Src src, int64_t n_chunks, int64_t chunk_elems, double* __restrict__ partials) {
-    double acc0 = 0.0, acc1 = 0.0;
-    int64_t c = blockIdx.x;
+// Sum of squares over chunks c, c + stride, ... below c_end.  The next chunk's
+// table entry is fetched while the current chunk's loads are in flight.  Returns
+// the first chunk of the sequence at or past c_end.
+template <bool kKeep, class Src>
+__device__ __forceinline__ int64_t sumsq_chunks(const Src& src, int64_t c, int64_t c_end,
+                                                int64_t stride, int64_t chunk_elems,
+                                                double& acc0, double& acc1) {
     mi_adamw_tensor t;
     int64_t begin = 0, end = 0;
-    if (c < n_chunks) src.get(c, chunk_elems, t, begin, end);
-    for (; c < n_chunks; c += gridDim.x) {
+    if (c < c_end) src.get(c, chunk_elems, t, begin, end);
+    for (; c < c_end; c += stride) {
         const float* __restrict__ g = t.grad;
         const bool vec = t.flags & MI_ADAMW_T_VEC;
         const int64_t vend = vec ? begin + ((end - begin) & ~static_cast<int64_t>(kVec - 1)) : begin;
@@ -297,10 +307,10 @@ __global__ __launch_bounds__(kNormThreads) void mi_adamw_sumsq_kernel(
         f32x4 a{}, b{}, d{}, e{};
         const bool full = i + 3 * kNormTile < vend;
         if (full) {
-            a = ld4(g + i);
-            b = ld4(g + i + kNormTile);
-            d = ld4(g + i + 2 * kNormTile);
-            e = ld4(g + i + 3 * kNormTile);
+            a = ld4_norm<kKeep>(g + i);
+            b = ld4_norm<kKeep>(g + i + kNormTile);
+            d = ld4_norm<kKeep>(g + i + 2 * kNormTile);
+            e = ld4_norm<kKeep>(g + i + 3 * kNormTile);
         }
         // ...then look up the next chunk while those loads are in flight; the
         // barrier keeps the scheduler from hoisting the lookup (and its waits)
@@ -308,8 +318,8 @@ __global__ __launch_bounds__(kNormThreads) void mi_adamw_sumsq_kernel(
         __builtin_amdgcn_sched_barrier(0);
         mi_adamw_tensor tn;
         int64_t bn = 0, en = 0;
-        const bool more = c + gridDim.x < n_chunks;
-        if (more) src.get(c + gridDim.x, chunk_elems, tn, bn, en);
+        const bool more = c + stride < c_end;
+        if (more) src.get(c + stride, chunk_elems, tn, bn, en);
         __builtin_amdgcn_sched_barrier(0);
         if (full) {
             sumsq4(a, acc0, acc1);
@@ -318,17 +328,17 @@ __global__ __launch_bounds__(kNormThreads) void mi_adamw_sumsq_kernel(
             sumsq4(e, acc0, acc1);
             i += 4 * kNormTile;
             for (; i + 3 * kNormTile < vend; i += 4 * kNormTile) {
-                a = ld4(g + i);
-                b = ld4(g + i + kNormTile);
-                d = ld4(g + i + 2 * kNormTile);
-                e = ld4(g + i + 3 * kNormTile);
+                a = ld4_norm<kKeep>(g + i);
+                b = ld4_norm<kKeep>(g + i + kNormTile);
+                d = ld4_norm<kKeep>(g + i + 2 * kNormTile);
+                e = ld4_norm<kKeep>(g + i + 3 * kNormTile);
                 sumsq4(a, acc0, acc1);
                 sumsq4(b, acc0, acc1);
                 sumsq4(d, acc0, acc1);
                 sumsq4(e, acc0, acc1);
             }
         }
-        for (; i < vend; i += kNormTile) sumsq4(ld4(g + i), acc0, acc1);
+        for (; i < vend; i += kNormTile) sumsq4(ld4_norm<kKeep>(g + i), acc0, acc1);
         for (int64_t j = vend + threadIdx.x; j < end; j += kNormThreads) {
             double x = ld1(g + j);
             acc0 += x * x;
@@ -339,6 +349,21 @@ __global__ __launch_bounds__(kNormThreads) void mi_adamw_sumsq_kernel(
             end = en;
         }
     }
+    return c;
+}
+
+// Workgroup b sums chunks b, b + grid, b + 2*grid, ...: streaming loads below
+// keep_from, ordinary loads from keep_from on (the last chunks the pass reads, the
+// ones still in the memory-side cache when the update reaches them).  Two loops,
+// not one with a per-chunk choice: the compiler would fold the two loads into one.
+template <class Src>
+__global__ __launch_bounds__(kNormThreads) void mi_adamw_sumsq_kernel(
+    Src src, int64_t n_chunks, int64_t chunk_elems, double* __restrict__ partials,
+    int64_t keep_from) {
+    double acc0 = 0.0, acc1 = 0.0;
+    int64_t c = blockIdx.x;
+    c = sumsq_chunks<false>(src, c, keep_from, gridDim.x, chunk_elems, acc0, acc1);
+    sumsq_chunks<true>(src, c, n_chunks, gridDim.x, chunk_elems, acc0, acc1);
     const double total = block_sum<kNormThreads>(acc0 + acc1);
     if (threadIdx.x == 0) partials[blockIdx.x] = total;
 }
@@ -482,6 +507,13 @@ __global__ __launch_bounds__(kUpdThreads) void mi_adamw_scale_kernel(
 // Measured on MI355X over 163M-2G gradients: 512 reads at 6.9-7.3 TB/s, 1024 at
 // 6.6-7.0, 2048-4096 and non-multiples of the CU count lower.
 constexpr int kNormBlocks = 512;
+// Gradient bytes the norm pass reads with cache-allocating loads (its last chunks):
+// the update pass, whose own streaming accesses do not displace them, then reads
+// them from the 256 MB Infinity Cache instead of HBM.
+#ifndef MI_ADAMW_NORM_KEEP_MB
+#define MI_ADAMW_NORM_KEEP_MB 256
+#endif
+constexpr int64_t kNormKeepBytes = int64_t(MI_ADAMW_NORM_KEEP_MB) << 20;
 
 bool chunk_elems_ok(int64_t chunk_elems) {
     return chunk_elems > 0 && (chunk_elems % kChunkQuantum) == 0 &&
@@ -508,8 +540,10 @@ int launch_norm(const Src& src, int64_t n_chunks, int64_t chunk_elems, float max
     if (n_chunks <= 0 || !chunk_elems_ok(chunk_elems) || !partials || !norm || !coef)
         return MI_ADAMW_E_INVALID;
     const unsigned grid = grid_for(n_chunks, kNormBlocks, kNormThreads);
+    const int64_t keep_chunks = kNormKeepBytes / (chunk_elems * static_cast<int64_t>(sizeof(float)));
+    const int64_t keep_from = n_chunks > keep_chunks ? n_chunks - keep_chunks : 0;
     hipLaunchKernelGGL(mi_adamw_sumsq_kernel<Src>, dim3(grid), dim3(kNormThreads), 0, s, src,
-                       n_chunks, chunk_elems, partials);
+                       n_chunks, chunk_elems, partials, keep_from);
     int rc = launch_status();
     if (rc != MI_ADAMW_OK) return rc;
     hipLaunchKernelGGL(mi_adamw_norm_finalize_kernel, dim3(1), dim3(kNormThreads), 0, s, partials,
