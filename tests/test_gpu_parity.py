@@ -511,3 +511,31 @@ def test_special_values_bf16_state_match_oracle(dev):
     copy = to_np(opt.bf16_param(p).view(torch.int16)).view(np.uint16)
     assert np.array_equal(copy, O.to_bf16_bits(pn))
     print(f"{idx.shape[0]} special combinations with bf16 state: identical to the oracle", flush=True)
+
+
+def test_mismatched_checkpoint_state_raises_before_any_launch(dev):
+    """A state dict from another model (moments of the wrong size) makes step() raise, as
+    torch's own AdamW does, and nothing is written: no pointer of a too-small buffer ever
+    reaches a kernel."""
+    import mi_adamw
+    params = make_params([(64, 48), (4099,)], dev)
+    other = make_params([(64, 48), (4000,)], dev)
+    for p in other:
+        p.grad = torch.ones_like(p)
+    donor = torch.optim.AdamW(other, lr=1e-3, fused=False)
+    donor.step()
+    ref_opt = torch.optim.AdamW(clone_params(params), lr=1e-3, fused=False)
+    ref_opt.load_state_dict(donor.state_dict())
+    for p in ref_opt.param_groups[0]["params"]:
+        p.grad = torch.ones_like(p)
+    with pytest.raises(RuntimeError):
+        ref_opt.step()                                   # torch refuses too
+    opt = mi_adamw.FusedAdamW(params, lr=1e-3, fused=False)
+    opt.load_state_dict(donor.state_dict())
+    for p in params:
+        p.grad = torch.ones_like(p)
+    before = [p.detach().clone() for p in params]
+    with pytest.raises(RuntimeError, match="elements"):
+        opt.step()
+    torch.cuda.synchronize()
+    assert all(torch.equal(a, b.detach()) for a, b in zip(before, params))
