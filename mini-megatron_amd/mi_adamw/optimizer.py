@@ -271,6 +271,27 @@ class FusedAdamW(Optimizer):
         self.flat_buffer = bool(flat_buffer)
         self.chunk_elems = int(chunk_elems)
         self.max_blocks = 0
+        self._reset_bookkeeping()
+
+        defaults = dict(
+            lr=lr, betas=betas, eps=eps, weight_decay=weight_decay, amsgrad=amsgrad,
+            maximize=maximize, foreach=foreach, capturable=capturable,
+            differentiable=differentiable, fused=fused, decoupled_weight_decay=True,
+        )
+        # add_param_group (called by the base constructor) checks and registers every
+        # parameter, and makes the per-parameter bf16 copies unless the flat layout
+        # holds them
+        super().__init__(params, defaults)
+        self.register_load_state_dict_post_hook(FusedAdamW._after_load_state_dict)
+        if self.flat_buffer:
+            self._flat = FlatLayout(self.param_groups, self.state_dtype, self.bf16_copy)
+
+    _OPTIONS = ("max_grad_norm", "clip_write_grads", "state_dtype", "bf16_copy", "flat_buffer",
+                "chunk_elems", "max_blocks")
+
+    def _reset_bookkeeping(self) -> None:
+        """The state this class keeps beside torch's: step slots, the packed step buffer,
+        bf16 copies, launch tables, workspaces."""
         self.last_grad_norm: torch.Tensor | None = None
         self._slots: dict[int, int] = {}
         self._steps = torch.zeros(0, dtype=torch.float32)
@@ -284,28 +305,21 @@ class FusedAdamW(Optimizer):
         self._copy_sync: dict[int, tuple[int, int]] | None = None
         self.timing_events = None
 
-        defaults = dict(
-            lr=lr, betas=betas, eps=eps, weight_decay=weight_decay, amsgrad=amsgrad,
-            maximize=maximize, foreach=foreach, capturable=capturable,
-            differentiable=differentiable, fused=fused, decoupled_weight_decay=True,
-        )
-        super().__init__(params, defaults)
-        self.register_load_state_dict_post_hook(FusedAdamW._after_load_state_dict)
-
-        if self.bf16_copy:
-            for group in self.param_groups:
-                for p in group["params"]:
-                    self._check_copyable(p)
-        if self.flat_buffer:
-            self._flat = FlatLayout(self.param_groups, self.state_dtype, self.bf16_copy)
-        elif self.bf16_copy:
-            for group in self.param_groups:
-                for p in group["params"]:
-                    self._copies[id(p)] = self._new_copy(p)
-
     # ------------------------------------------------------------------ torch API
 
+    def __getstate__(self) -> dict[str, Any]:
+        """torch's optimizer state (defaults, state, param_groups) plus this class's
+        options, so that pickling and copy.deepcopy give a working optimizer."""
+        if getattr(self, "_flat", None) is not None:
+            raise NotImplementedError("FusedAdamW(flat_buffer=True) cannot be pickled or copied: "
+                                      "its parameters are views of its own buffers; save "
+                                      "state_dict() instead")
+        state = super().__getstate__()
+        state["mi_adamw_options"] = {k: getattr(self, k) for k in self._OPTIONS if hasattr(self, k)}
+        return state
+
     def __setstate__(self, state: dict[str, Any]) -> None:
+        options = state.pop("mi_adamw_options", None)
         super().__setstate__(state)
         for group in self.param_groups:
             group.setdefault("amsgrad", False)
@@ -315,8 +329,18 @@ class FusedAdamW(Optimizer):
             group.setdefault("differentiable", False)
             group.setdefault("fused", None)
             group["decoupled_weight_decay"] = True
-        self._recs = None
-        self._launch_cache = None
+        if options is None:
+            self._recs = None
+            self._launch_cache = None
+            return
+        # Unpickled or copied: rebuild the bookkeeping from the groups and the state.
+        for k, v in options.items():
+            setattr(self, k, v)
+        self._reset_bookkeeping()
+        self.register_load_state_dict_post_hook(FusedAdamW._after_load_state_dict)
+        for group in self.param_groups:
+            self._register_params(group["params"])
+        FusedAdamW._after_load_state_dict(self)
 
     def add_param_group(self, param_group: dict[str, Any]) -> None:
         if getattr(self, "_flat", None) is not None:
@@ -329,7 +353,11 @@ class FusedAdamW(Optimizer):
         super().add_param_group(param_group)
         if not hasattr(self, "_slots"):
             return
-        new = [p for p in self.param_groups[-1]["params"] if id(p) not in self._slots]
+        self._register_params(self.param_groups[-1]["params"])
+
+    def _register_params(self, params) -> None:
+        """Step slots (and bf16 copies) for parameters this optimizer has not seen."""
+        new = [p for p in params if id(p) not in self._slots]
         if not new:
             return
         old_n = len(self._step_views)
@@ -348,7 +376,7 @@ class FusedAdamW(Optimizer):
                 slot = self._slots[id(p)]
                 if self._step_views[slot] is not None:
                     st["step"] = self._step_views[slot]
-        if getattr(self, "bf16_copy", False) and getattr(self, "_flat", None) is None:
+        if getattr(self, "bf16_copy", False) and not getattr(self, "flat_buffer", False):
             for p in new:
                 self._copies[id(p)] = self._new_copy(p)
         self._launch_cache = None

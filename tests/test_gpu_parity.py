@@ -231,6 +231,7 @@ def test_flat_buffer_matches_per_tensor(dev):
         _assert_same(ref, ours, topt, oopt, max_allowed=0)
     for p in ours:
         assert torch.equal(oopt.bf16_param(p), p.detach().to(torch.bfloat16))
+    assert oopt._copies == {}          # the copies live in the flat buffer only
 
 
 def test_state_dict_roundtrip_with_torch(dev):

@@ -342,3 +342,29 @@ def test_moving_gradients_refresh_rows_only(dev):
     assert max_ulp_all(ref, ours) == 0
     assert max_ulp_all([topt.state[p]["exp_avg"] for p in ref],
                        [oopt.state[q]["exp_avg"] for q in ours]) == 0
+
+
+def test_deepcopy_mid_training_continues_identically(dev):
+    """copy.deepcopy of a FusedAdamW mid-training (as torch optimizers allow) gives an
+    optimizer over copied parameters that continues bit for bit like the original."""
+    import copy
+    import mi_adamw
+    params = make_params([(64, 48), (4099,), (3,)], dev)
+    opt = mi_adamw.FusedAdamW(params, lr=3e-4, betas=(0.9, 0.95), weight_decay=0.1,
+                              max_grad_norm=1.0, bf16_copy=True)
+    for step in range(1, 4):
+        set_grads(params, step, 1e-2)
+        opt.step()
+    clone = copy.deepcopy(opt)
+    cparams = clone.param_groups[0]["params"]
+    for step in range(4, 7):
+        set_grads(params, step, 1e-2)
+        set_grads(cparams, step, 1e-2)
+        opt.step()
+        clone.step()
+    torch.cuda.synchronize()
+    assert max_ulp_all(params, cparams) == 0
+    assert torch.equal(opt.last_grad_norm, clone.last_grad_norm)
+    for p, q in zip(params, cparams):
+        assert float(opt.state[p]["step"]) == float(clone.state[q]["step"]) == 6.0
+        assert torch.equal(opt.bf16_param(p), clone.bf16_param(q))

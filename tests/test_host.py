@@ -334,3 +334,41 @@ def test_abi_rejects_bad_arguments_without_launching():
     row.grad = 36
     assert lib.mi_adamw_step_flat(ctypes.byref(row), h, None, 65536, 0, 0, 0, None) == _lib.E_ALIGN
     assert "invalid" in _lib.strerror(_lib.E_INVALID)
+
+
+def test_deepcopy_and_pickle_give_a_working_optimizer():
+    """torch optimizers survive copy.deepcopy and pickling (Optimizer.__getstate__);
+    FusedAdamW's own options and bookkeeping come back with them."""
+    import copy
+    import pickle
+    params = [torch.nn.Parameter(torch.randn(4, 3)), torch.nn.Parameter(torch.randn(5))]
+    ref = torch.optim.AdamW(params, lr=1e-3, fused=False)
+    for p in params:
+        p.grad = torch.randn_like(p)
+    ref.step()
+    opt = mi_adamw.FusedAdamW(params, lr=1e-3, fused=False, max_grad_norm=0.5, bf16_copy=True,
+                              state_dtype=torch.bfloat16, chunk_elems=8192)
+    opt.load_state_dict(ref.state_dict())
+    for clone in (copy.deepcopy(opt), pickle.loads(pickle.dumps(opt))):
+        assert (clone.max_grad_norm, clone.bf16_copy, clone.state_dtype, clone.chunk_elems) == \
+            (0.5, True, torch.bfloat16, 8192)
+        cps = clone.param_groups[0]["params"]
+        assert all(q is not p for q, p in zip(cps, params))
+        for q, p in zip(cps, params):
+            st = clone.state[q]
+            assert float(st["step"]) == 1.0
+            assert st["step"] is clone._step_views[clone._slots[id(q)]]   # re-homed
+            assert st["exp_avg"].dtype == torch.bfloat16
+            assert torch.equal(st["exp_avg"], opt.state[p]["exp_avg"])
+            assert torch.equal(clone.bf16_param(q), q.detach().bfloat16())
+        assert clone.state_dict()["param_groups"] == opt.state_dict()["param_groups"]
+
+
+def test_flat_layout_makes_no_per_parameter_copies():
+    """With flat_buffer=True the bf16 copies live in the flat copy buffer only."""
+    if not torch.cuda.is_available():
+        opt = mi_adamw.FusedAdamW([torch.nn.Parameter(torch.zeros(3))], bf16_copy=True)
+        assert len(opt._copies) == 1
+        with pytest.raises(RuntimeError, match="ROCm GPU"):
+            mi_adamw.FusedAdamW([torch.nn.Parameter(torch.zeros(3))], bf16_copy=True,
+                                flat_buffer=True)
