@@ -145,7 +145,8 @@ def weight_casts(model, opt, ids, labels, mask, device_type="cpu"):
     """aten::_to_copy calls in one bf16-autocast forward, plain and with bf16_weights."""
     out = []
     for use in (False, True):
-        with torch.profiler.profile(activities=[torch.profiler.ProfilerActivity.CPU]) as prof:
+        with torch.profiler.profile(activities=[torch.profiler.ProfilerActivity.CPU],
+                                    acc_events=True) as prof:
             with torch.autocast(device_type, dtype=torch.bfloat16):
                 if use:
                     with mi_adamw.bf16_weights(opt, model):
