@@ -511,6 +511,10 @@ class FusedAdamW(Optimizer):
                             st[key] = self._flat.adopt_state(p, key, t)
                         elif t.dtype != self._state_dtype_for(p):
                             st[key] = t.to(self._state_dtype_for(p)).contiguous()
+        if self.bf16_copy:
+            # checkpoint.py:18-19 loads the model, then the optimizer: the masters may
+            # have just changed, so the copies are rewritten from them
+            self.refresh_bf16_copies()
         self._launch_cache = None
         self._recs = None
 

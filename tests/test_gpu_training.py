@@ -368,3 +368,56 @@ def test_deepcopy_mid_training_continues_identically(dev):
     for p, q in zip(params, cparams):
         assert float(opt.state[p]["step"]) == float(clone.state[q]["step"]) == 6.0
         assert torch.equal(opt.bf16_param(p), clone.bf16_param(q))
+
+
+def _batch(dev, seed):
+    return torch.randint(0, 512, (4, 32), device=dev, generator=gen(dev, seed))
+
+
+def _train_step(model, opt, sch, tokens):
+    """zero_grad, forward, backward, step, scheduler step (main.py:202-210)."""
+    opt.zero_grad()
+    logits = model(tokens)
+    loss = F.cross_entropy(logits.view(-1, logits.shape[-1]), tokens.view(-1))
+    loss.backward()
+    opt.step()
+    sch.step()
+    return loss.detach()
+
+
+def test_checkpoint_file_round_trip_as_the_reference_does(dev):
+    """checkpoint.py:5-21: torch.save of model, optimizer and scheduler state, then
+    torch.load(map_location=device, weights_only=True) and the three load_state_dict
+    calls.  Training continues bit for bit, and the bf16 copies match the loaded masters."""
+    import io
+    import mi_adamw
+    hp = dict(lr=6e-4, weight_decay=0.1, fused=False)
+
+    def build(seed):
+        torch.manual_seed(seed)
+        m = TinyGPT().to(dev)
+        o = mi_adamw.FusedAdamW(m.parameters(), **hp, bf16_copy=True, max_grad_norm=1.0)
+        s = torch.optim.lr_scheduler.LambdaLR(o, _lr_lambda(2, 10))
+        return m, o, s
+
+    model, opt, sch = build(0)
+    batches = [_batch(dev, 100 + i) for i in range(6)]
+    for ids in batches[:3]:
+        _train_step(model, opt, sch, ids)
+    buf = io.BytesIO()
+    torch.save({"model_state": model.state_dict(), "optimizer_state": opt.state_dict(),
+                "scheduler_state": sch.state_dict(), "step": 3}, buf)
+    buf.seek(0)
+    model2, opt2, sch2 = build(1)                      # different initial weights
+    state = torch.load(buf, map_location=dev, weights_only=True)
+    model2.load_state_dict(state["model_state"])
+    opt2.load_state_dict(state["optimizer_state"])
+    sch2.load_state_dict(state["scheduler_state"])
+    for p in model2.parameters():
+        assert torch.equal(opt2.bf16_param(p), p.detach().bfloat16())
+    for ids in batches[3:]:
+        la = _train_step(model, opt, sch, ids)
+        lb = _train_step(model2, opt2, sch2, ids)
+        assert torch.equal(la, lb)
+    torch.cuda.synchronize()
+    assert max_ulp_all(list(model.parameters()), list(model2.parameters())) == 0
