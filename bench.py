@@ -232,7 +232,7 @@ def cpu_baseline(name: str, budget_s: float = 20.0) -> dict:
         one()
     times = []
     t_start = time.perf_counter()
-    while len(times) < 5 or (time.perf_counter() - t_start < budget_s and len(times) < 50):
+    while len(times) < 5 or (time.perf_counter() - t_start < budget_s and len(times) < 200):
         t0 = time.perf_counter()
         one()
         times.append(time.perf_counter() - t0)
