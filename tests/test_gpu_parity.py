@@ -176,6 +176,29 @@ def test_clip_grad_norm_dropin(dev):
     assert max_ulp_all([p.grad for p in ref], [q.grad for q in ours]) <= 1
 
 
+def test_clip_grad_norm_with_moving_gradients(dev):
+    """clip_grad_norm_ in a training loop: new gradient tensors every call (their tables
+    are refreshed, the chunk table kept), each result against torch's on the same grads."""
+    import mi_adamw
+    from mi_adamw import clip as C
+    ref = make_params(MINI_SHAPES, dev)
+    ours = clone_params(ref)
+    held = []
+    for step in range(1, 5):
+        set_grads(ref, step, 1e-2)
+        held.append([q.grad for q in ours if q.grad is not None])   # force new addresses
+        for p, q in zip(ref, ours):
+            q.grad = p.grad.clone()
+        tn = torch.nn.utils.clip_grad_norm_(ref, 1.0)
+        on = mi_adamw.clip_grad_norm_(ours, 1.0)
+        assert rel_err(on, tn) <= 1e-6
+        for p, q in zip(ref, ours):
+            # each scaled by its own coefficient (the two norms may differ by an ulp)
+            assert close_rel(q.grad, p.grad, 1e-6, 1e-12) <= 1.0
+    keys = [k for k in C._cache if k[0] == dev]
+    assert len(keys) == 1, "one chunk table for one set of sizes"
+
+
 def test_bf16_copy_and_state(dev):
     import mi_adamw
     params = make_params(MINI_SHAPES, dev)
