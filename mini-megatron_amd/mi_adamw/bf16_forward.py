@@ -28,6 +28,10 @@ from its master when the master changed outside the optimizer (its version
 counter or storage moved, e.g. ``model.load_state_dict``); a change made
 through ``p.data`` is not visible that way: call
 ``optimizer.refresh_bf16_copies()`` after one.
+
+Meant for eager-mode models, the reference's default; it is not tested with a
+``torch.compile``'d model (``--compile``, main.py), whose graphs guard on the
+parameters this context replaces.
 """
 from __future__ import annotations
 
