@@ -831,21 +831,22 @@ class FusedAdamW(Optimizer):
             ev[0].record()
         if self.max_grad_norm is not None:
             norm = torch.empty((), dtype=torch.float32, device=device)
-            if norm_launch.n_rows == 1:
+            if norm_launch.n_chunks == 0:
+                # nothing but empty tensors: torch's norm of no elements is 0
+                norm.zero_()
+                coef.fill_(1.0)
+            elif norm_launch.n_rows == 1:
                 row = self._row_struct(norm_launch)
                 _lib.check(lib.mi_adamw_grad_norm_flat(
                     row.grad, row.numel, self.chunk_elems, float(self.max_grad_norm),
                     partials.data_ptr(), norm.data_ptr(), coef.data_ptr(),
                     stream), "mi_adamw_grad_norm_flat")
-            elif norm_launch.n_chunks > 0:
+            else:
                 _lib.check(lib.mi_adamw_grad_norm(
                     norm_launch.rows.data_ptr(), norm_launch.chunks.data_ptr(),
                     norm_launch.n_chunks, self.chunk_elems, float(self.max_grad_norm),
                     partials.data_ptr(), norm.data_ptr(), coef.data_ptr(),
                     stream), "mi_adamw_grad_norm")
-            else:
-                norm.zero_()
-                coef.fill_(1.0)
             self.last_grad_norm = norm
             flags |= _lib.F_CLIP
             if self.clip_write_grads:

@@ -421,3 +421,40 @@ def test_checkpoint_file_round_trip_as_the_reference_does(dev):
         assert torch.equal(la, lb)
     torch.cuda.synchronize()
     assert max_ulp_all(list(model.parameters()), list(model2.parameters())) == 0
+
+
+@pytest.mark.parametrize("flat", [False, True])
+def test_empty_tensors_and_empty_groups_with_clip(dev, flat):
+    """Zero-element parameters, a param group holding nothing else, and a model with
+    nothing but empty tensors: the step runs, as torch's does, and the norm of no
+    elements is 0."""
+    import mi_adamw
+    shapes_a = [(0,), (0, 5)]
+    shapes_b = [(64, 48), (4099,)]
+    ref_a, ref_b = make_params(shapes_a, dev), make_params(shapes_b, dev, seed=2000)
+    ours_a, ours_b = clone_params(ref_a), clone_params(ref_b)
+    hp = dict(lr=3e-4, betas=(0.9, 0.95), weight_decay=0.1)
+    topt = torch.optim.AdamW([dict(params=ref_a), dict(params=ref_b)], foreach=False, **hp)
+    oopt = mi_adamw.FusedAdamW([dict(params=ours_a), dict(params=ours_b)], **hp,
+                               max_grad_norm=1.0, flat_buffer=flat)
+    for step in range(1, 4):
+        set_grads(ref_a + ref_b, step, 1e-2)
+        for p, q in zip(ref_a + ref_b, ours_a + ours_b):
+            if flat:
+                q.grad.copy_(p.grad)
+            else:
+                q.grad = p.grad.clone()
+        oopt.step()
+        torch.nn.utils.clip_grads_with_norm_(ref_a + ref_b, 1.0, oopt.last_grad_norm.clone())
+        topt.step()
+    torch.cuda.synchronize()
+    assert max_ulp_all(ref_b, ours_b) == 0
+    # nothing but empty tensors
+    empties = make_params(shapes_a, dev)
+    opt = mi_adamw.FusedAdamW(empties, max_grad_norm=1.0, flat_buffer=flat)
+    for p in empties:
+        if not flat:
+            p.grad = torch.zeros_like(p)
+    opt.step()
+    torch.cuda.synchronize()
+    assert opt.last_grad_norm.item() == 0.0
