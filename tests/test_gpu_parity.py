@@ -61,6 +61,8 @@ def _assert_same(ref, ours, topt, oopt, max_allowed=0):
     ((0.3, 0.95), 1e-3, 0.01, False),    # lerp weight 0.7: the other Lerp.h branch
     ((0.9, 0.95), 3e-4, 0.1, True),      # maximize
     ((0.9, 0.95), 0.0, 0.1, False),      # lr = 0, the reference's first step (main.py:39-40)
+    ((0.0, 0.0), 1e-3, 0.1, False),      # lerp weight 1 and beta2 0: bias corrections exactly 1
+    ((0.0, 0.999), 1e-3, 0.0, True),
 ])
 def test_chained_steps_match_torch_bitwise(dev, betas, lr, wd, maximize):
     """Steps 1..10 from zero state: bias corrections change every step."""
@@ -74,6 +76,22 @@ def test_chained_steps_match_torch_bitwise(dev, betas, lr, wd, maximize):
         torch.cuda.synchronize()
         print(f"step {step}", flush=True)
         _assert_same(ref, ours, topt, oopt, max_allowed=0)
+
+
+def test_eps_zero_matches_torch_including_its_nans(dev):
+    """eps = 0: where v is 0 the denominator is 0 and torch produces inf/NaN; so must we."""
+    ref, ours, topt, oopt = _pair(dev, eps=0.0)
+    for step in range(1, 4):
+        set_grads(ref, step, 1e-3)
+        for p in ref:
+            p.grad.view(-1)[::7] = 0.0          # v stays 0 there on the first step
+        for p, q in zip(ref, ours):
+            q.grad = p.grad.clone()
+        topt.step()
+        oopt.step()
+    torch.cuda.synchronize()
+    assert any(bool(torch.isnan(p).any()) for p in ref)
+    _assert_same(ref, ours, topt, oopt, max_allowed=0)
 
 
 def test_kernel_matches_oracle_bitwise(dev):
