@@ -45,14 +45,14 @@ class _MastersAsBf16(torch.autograd.Function):
     Python call per forward and one per backward, not one per weight."""
 
     @staticmethod
-    def forward(ctx, n, *tensors):
+    def forward(ctx, copies, *masters):
+        # the copies come in as one list: only the masters are autograd inputs
         ctx.set_materialize_grads(False)
-        return tuple(c.view_as(c) for c in tensors[n:])
+        return tuple(c.view_as(c) for c in copies)
 
     @staticmethod
     def backward(ctx, *grads):
-        widened = tuple(None if g is None else g.to(torch.float32) for g in grads)
-        return (None,) + widened + (None,) * len(grads)
+        return (None,) + tuple(None if g is None else g.to(torch.float32) for g in grads)
 
 
 def linear_layers(module: torch.nn.Module) -> bool:
@@ -104,8 +104,8 @@ class bf16_weights:
         opt = self.optimizer
         opt._track_copies()
         masters = [p for _, _, p in self.swaps]
-        copies = [opt._current_copy(p) for p in masters]
-        aliases = _MastersAsBf16.apply(len(masters), *masters, *copies)
+        copies = opt._current_copies(masters)
+        aliases = _MastersAsBf16.apply(copies, *masters)
         for (mod, n, _), a in zip(self.swaps, aliases):
             # Assigned into _parameters directly: a non-leaf bf16 tensor for the
             # duration of the context, restored on exit.

@@ -58,6 +58,7 @@ class FlatLayout:
         self.exp_avg_sq = torch.zeros(off, dtype=state_dtype, device=device)
         self.copy = torch.zeros(off, dtype=torch.bfloat16, device=device) if bf16_copy else None
         self.max_exp_avg_sq: torch.Tensor | None = None   # allocated on first amsgrad use
+        self._copy_views: dict[int, torch.Tensor] = {}
         with torch.no_grad():
             for p in params:
                 view = self._view(self.param, p)
@@ -106,7 +107,11 @@ class FlatLayout:
         return view
 
     def copy_view(self, p: torch.Tensor) -> torch.Tensor:
-        return self._view(self.copy, p)
+        """p's slice of the bf16 copy buffer (made once: the buffer never moves)."""
+        v = self._copy_views.get(id(p))
+        if v is None:
+            v = self._copy_views[id(p)] = self._view(self.copy, p)
+        return v
 
     def zero_grads(self, param_groups) -> None:
         self.grad.zero_()

@@ -447,12 +447,17 @@ class FusedAdamW(Optimizer):
             self._copy_sync = {}
             self.refresh_bf16_copies()
 
-    @torch.no_grad()
-    def _current_copy(self, p: torch.Tensor) -> torch.Tensor:
-        """p's bf16 copy, rewritten first if p changed since the copy was written."""
-        if self._copy_sync.get(id(p)) != (p._version, p.data_ptr()):
-            return self._refresh_copy(p)
-        return self._copy_for(p)
+    def _current_copies(self, masters: list) -> list:
+        """The masters' bf16 copies, each rewritten first if its master changed since
+        the copy was written (one pass of cheap checks; grad mode is touched only when
+        a copy must be refreshed)."""
+        sync = self._copy_sync
+        stale = [p for p in masters if sync.get(id(p)) != (p._version, p.data_ptr())]
+        if stale:
+            with torch.no_grad():
+                for p in stale:
+                    self._refresh_copy(p)
+        return [self._copy_for(p) for p in masters]
 
     @torch.no_grad()
     def set_state(self, p: torch.Tensor, step: float, exp_avg: torch.Tensor,
