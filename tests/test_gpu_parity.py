@@ -581,3 +581,31 @@ def test_mismatched_checkpoint_state_raises_before_any_launch(dev):
         opt.step()
     torch.cuda.synchronize()
     assert all(torch.equal(a, b.detach()) for a, b in zip(before, params))
+
+
+def test_thousands_of_ragged_tensors_with_clip(dev):
+    """3,000 parameters of random sizes (most with a scalar tail, many smaller than one
+    lane's vector) and two large ones: one table launch of thousands of rows, bit-identical
+    to torch given the same clip norm."""
+    import mi_adamw
+    rng = np.random.default_rng(11)
+    shapes = [(int(n),) for n in rng.integers(1, 5000, 3000)] + [(70001,), (262147,)]
+    ref = make_params(shapes, dev)
+    ours = clone_params(ref)
+    hp = dict(lr=3e-4, betas=(0.9, 0.95), weight_decay=0.1)
+    topt = torch.optim.AdamW(ref, foreach=False, **hp)
+    oopt = mi_adamw.FusedAdamW(ours, **hp, max_grad_norm=1.0)
+    for step in range(1, 3):
+        set_grads(ref, step, 1e-2)
+        for p, q in zip(ref, ours):
+            q.grad = p.grad.clone()
+        oopt.step()
+        torch.nn.utils.clip_grads_with_norm_(ref, 1.0, oopt.last_grad_norm.clone())
+        topt.step()
+    torch.cuda.synchronize()
+    launch = oopt._launch_cache[2][0]
+    assert launch.n_rows == len(shapes) and launch.tables
+    exact = O.total_norm([to_np(p.grad) for p in ours])
+    print("rows", launch.n_rows, "chunks", launch.n_chunks, "norm", oopt.last_grad_norm.item(),
+          float(exact), flush=True)
+    _assert_same(ref, ours, topt, oopt, max_allowed=0)
