@@ -172,10 +172,12 @@ class _Launch:
 
 
 class FusedAdamW(Optimizer):
-    """AdamW with the whole step fused into one MI355X kernel launch.
+    """AdamW with the whole step fused into one MI355X kernel launch (three with the
+    global-norm clip: sum of squares, finalize, update).
 
     The constructor takes torch.optim.AdamW's arguments, with its defaults and
-    its ValueError checks, plus keyword-only options:
+    its ValueError checks (amsgrad and maximize work as in torch), plus
+    keyword-only options:
 
     max_grad_norm:    if set, clip the global gradient L2 norm to this value
                       before the update, as ``torch.nn.utils.clip_grad_norm_``
