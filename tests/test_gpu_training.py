@@ -458,3 +458,49 @@ def test_empty_tensors_and_empty_groups_with_clip(dev, flat):
     opt.step()
     torch.cuda.synchronize()
     assert opt.last_grad_norm.item() == 0.0
+
+
+def test_flat_buffer_under_distributed_optimizer_usage(dev):
+    """The reference's DistributedOptimizer builds ``optimizer_cls([{"params": owned}],
+    **kwargs)`` and its zero_grad sets every gradient to None
+    (parallel/distributed_optimizer.py:26-35), so backward hands a flat-buffer optimizer
+    freshly allocated gradients, and on some steps a parameter has none.  Fresh
+    gradients are copied into the buffer; a group with a missing gradient is stepped
+    tensor by tensor, its clip norm over the gradients present; parameters, moments,
+    step counts and bf16 copies stay bit-identical to torch."""
+    import mi_adamw
+    shapes = [(64, 48), (48,), (128, 64), (64,), (7, 5)]
+    ref = make_params(shapes, dev)
+    ours = clone_params(ref)
+    hp = dict(lr=6e-4, weight_decay=0.1, fused=False)
+    topt = torch.optim.AdamW([{"params": ref}], **hp)
+    oopt = mi_adamw.AdamW([{"params": ours}], **hp, flat_buffer=True, max_grad_norm=1.0,
+                          bf16_copy=True)
+    g = gen(dev, 21)
+    for step in range(6):
+        for p, q in zip(ref, ours):
+            p.grad = None
+            q.grad = None
+        skip = {1, 4} if step in (2, 3) else set()
+        for i, (p, q) in enumerate(zip(ref, ours)):
+            if i not in skip:
+                p.grad = torch.randn(p.shape, device=dev, generator=g) * 1e-2
+                q.grad = p.grad.clone()          # allocated outside the flat buffer
+        oopt.step()
+        present = [p for p in ref if p.grad is not None]
+        want = torch.nn.utils.get_total_norm([p.grad for p in present])
+        assert abs(oopt.last_grad_norm.item() - want.item()) <= 1e-6 * want.item()
+        torch.nn.utils.clip_grads_with_norm_(present, 1.0, oopt.last_grad_norm.clone())
+        topt.step()
+        torch.cuda.synchronize()
+        assert max_ulp_all(ref, ours) == 0
+        for i, q in enumerate(ours):
+            if i not in skip:
+                assert oopt._flat.is_grad_view(q, q.grad)
+    for p, q in zip(ref, ours):
+        ts, os_ = topt.state[p], oopt.state[q]
+        assert float(ts["step"]) == float(os_["step"])
+        assert max_ulp(ts["exp_avg"], os_["exp_avg"]) == 0
+        assert max_ulp(ts["exp_avg_sq"], os_["exp_avg_sq"]) == 0
+        assert torch.equal(oopt.bf16_param(q), q.detach().to(torch.bfloat16))
+    assert float(oopt.state[ours[1]]["step"]) == 4.0
