@@ -40,7 +40,7 @@
 extern "C" {
 #endif
 
-#define MI_ADAMW_ABI_VERSION 2
+#define MI_ADAMW_ABI_VERSION 3
 #define MI_ADAMW_MAX_HYPER 16      /* hyperparameter sets per launch */
 #define MI_ADAMW_MAX_NORM_BLOCKS 4096 /* partial sums per grad-norm launch */
 
@@ -97,6 +97,39 @@ typedef struct mi_adamw_hyper {
     float neg_step_size;   /* -(lr / (1 - beta1**step))                      (adam.py:534,547) */
     float grad_sign;       /* -1 with maximize=True, else 1                  (adam.py:397) */
 } mi_adamw_hyper;
+
+/* How a capturable launch gets the learning rate (mi_adamw_capt_hyper.lr_mode). */
+#define MI_ADAMW_LR_FLOAT 0   /* lr is a Python float: step_size = (1/bc1) * lr, the way
+                                 torch evaluates `float / tensor` (Tensor.__rtruediv__)      */
+#define MI_ADAMW_LR_VALUE 1   /* lr is a tensor whose value the host passes in `lr`:
+                                 step_size = lr / bc1, a true division                       */
+#define MI_ADAMW_LR_DEVICE 2  /* lr is a device fp32 scalar at lr_ptr, read by the kernel:
+                                 step_size = lr / bc1, and the weight-decay factor
+                                 1 - lr*weight_decay is formed on the device                 */
+
+/* One parameter group of a capturable step (torch.optim.AdamW(capturable=True):
+ * adam.py:396-527, the per-step scalars at adam.py:480-522).  Nothing here
+ * depends on the step count: the kernel reads each tensor's step from device
+ * memory and forms
+ *   bc1 = 1 - beta1**step, bc2 = 1 - beta2**step, step_size (see lr_mode),
+ *   a = sqrt(bc2) * -step_size, e = eps * (1 / -step_size)
+ * in fp32, op for op, so that a launch recorded into a HIP graph stays right as
+ * the steps advance.  The element chain is then
+ *   p = p*wd_factor; m = lerp(m, g, lerp_w); v = v*beta2 + (1-beta2)*g*g;
+ *   p = p + m / (sqrt(v) / a + e). */
+typedef struct mi_adamw_capt_hyper {
+    float beta1;           /* base of beta1**step                              (adam.py:488) */
+    float beta2;           /* v *= beta2, and the base of beta2**step          (adam.py:476,497) */
+    float lerp_w;          /* 1 - beta1                                        (adam.py:457) */
+    float one_minus_beta2; /* 1 - beta2                                        (adam.py:476) */
+    float eps;             /* eps                                              (adam.py:522) */
+    float grad_sign;       /* -1 with maximize=True, else 1                    (adam.py:397) */
+    float lr;              /* LR_FLOAT, LR_VALUE: the learning rate                          */
+    float wd_factor;       /* LR_FLOAT, LR_VALUE: 1 - lr*weight_decay, 1 when wd == 0 (:419) */
+    float weight_decay;    /* LR_DEVICE: the weight decay, 0 for none                        */
+    int32_t lr_mode;       /* MI_ADAMW_LR_*                                                  */
+    const float *lr_ptr;   /* LR_DEVICE: device fp32 learning rate                           */
+} mi_adamw_capt_hyper;
 
 /* Library identification: "mi_adamw <abi> gfx950 ...". */
 const char *mi_adamw_version(void);
@@ -155,6 +188,21 @@ int mi_adamw_step(const mi_adamw_tensor *d_tensors, const mi_adamw_chunk *d_chun
 int mi_adamw_step_flat(const mi_adamw_tensor *t, const mi_adamw_hyper *hyper,
                        const float *d_grad_scale, int64_t chunk_elems, int32_t state_dtype,
                        int32_t flags, int32_t max_blocks, void *stream);
+
+/* The fused AdamW update of torch's capturable chain (adam.py:480-527) over
+ * every chunk of the tables, for a step that may be recorded into a HIP graph:
+ * no argument depends on the step count.  hypers: host array of n_hyper
+ * (<= MI_ADAMW_MAX_HYPER) groups, indexed by mi_adamw_tensor.hyper.
+ * d_steps: device fp32 step counts, already incremented for this step
+ * (adam.py:414); d_step_index: device int32 array, one entry per row of the
+ * tensor table, giving the row's index into d_steps.  The other arguments are
+ * those of mi_adamw_step. */
+int mi_adamw_step_capturable(const mi_adamw_tensor *d_tensors, const mi_adamw_chunk *d_chunks,
+                             int64_t n_chunks, int64_t chunk_elems,
+                             const mi_adamw_capt_hyper *hypers, int32_t n_hyper,
+                             const float *d_steps, const int32_t *d_step_index,
+                             const float *d_grad_scale, int32_t state_dtype, int32_t flags,
+                             int32_t max_blocks, void *stream);
 
 #ifdef __cplusplus
 }

@@ -16,7 +16,7 @@ import torch
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libmi_adamw.so")
 
-ABI_VERSION = 2
+ABI_VERSION = 3
 MAX_HYPER = 16
 MAX_NORM_BLOCKS = 4096
 CHUNK_QUANTUM = 4096
@@ -35,6 +35,10 @@ F_AMSGRAD = 1 << 3
 
 T_VEC = 1 << 0
 
+LR_FLOAT = 0
+LR_VALUE = 1
+LR_DEVICE = 2
+
 # Every symbol include/mi_adamw.h declares.
 EXPORTS = (
     "mi_adamw_version",
@@ -45,6 +49,7 @@ EXPORTS = (
     "mi_adamw_scale_grads",
     "mi_adamw_step",
     "mi_adamw_step_flat",
+    "mi_adamw_step_capturable",
 )
 
 
@@ -85,9 +90,28 @@ class Hyper(ctypes.Structure):
     ]
 
 
+class CaptHyper(ctypes.Structure):
+    """mi_adamw_capt_hyper: one param group of a capturable step (no per-step values)."""
+
+    _fields_ = [
+        ("beta1", ctypes.c_float),
+        ("beta2", ctypes.c_float),
+        ("lerp_w", ctypes.c_float),
+        ("one_minus_beta2", ctypes.c_float),
+        ("eps", ctypes.c_float),
+        ("grad_sign", ctypes.c_float),
+        ("lr", ctypes.c_float),
+        ("wd_factor", ctypes.c_float),
+        ("weight_decay", ctypes.c_float),
+        ("lr_mode", ctypes.c_int32),
+        ("lr_ptr", ctypes.c_void_p),
+    ]
+
+
 assert ctypes.sizeof(TensorRow) == 64
 assert ctypes.sizeof(ChunkRow) == 8
 assert ctypes.sizeof(Hyper) == 32
+assert ctypes.sizeof(CaptHyper) == 48 and CaptHyper.lr_ptr.offset == 40
 
 _vp = ctypes.c_void_p
 _i64 = ctypes.c_int64
@@ -103,6 +127,8 @@ _SIGNATURES = {
     "mi_adamw_scale_grads": ([_vp, _vp, _i64, _i64, _vp, _vp], ctypes.c_int),
     "mi_adamw_step": ([_vp, _vp, _i64, _i64, _vp, _i32, _vp, _i32, _i32, _i32, _vp], ctypes.c_int),
     "mi_adamw_step_flat": ([_vp, _vp, _vp, _i64, _i32, _i32, _i32, _vp], ctypes.c_int),
+    "mi_adamw_step_capturable": ([_vp, _vp, _i64, _i64, _vp, _i32, _vp, _vp, _vp, _i32, _i32,
+                                  _i32, _vp], ctypes.c_int),
 }
 
 _lib = None

@@ -11,7 +11,10 @@
 //   mi_adamw_update_kernel pass 2: p, g, m, v streamed with dwordx4 loads and
 //                          stores, the AdamW op chain in fp32 registers, optional
 //                          bf16 moments, bf16 model copy, gradient write-back and
-//                          amsgrad's running maximum of v.
+//                          amsgrad's running maximum of v.  Two chains: torch's
+//                          default one (per-step scalars from the host) and its
+//                          capturable one (per-step scalars formed per workgroup
+//                          from a device step count, for HIP graph capture).
 //   mi_adamw_scale_kernel  g *= coef in place (clip_grad_norm_'s write-back).
 //
 // Every launch walks a chunk table (one entry per `chunk_elems` slice of a
@@ -59,6 +62,8 @@ static_assert(offsetof(mi_adamw_tensor, max_exp_avg_sq) == 40 &&
 static_assert(offsetof(mi_adamw_tensor, hyper) == 56 && offsetof(mi_adamw_tensor, flags) == 60,
               "hyper and flags share the last word");
 static_assert(sizeof(mi_adamw_chunk) == 8, "mi_adamw_chunk is two int32");
+static_assert(sizeof(mi_adamw_capt_hyper) == 48 && offsetof(mi_adamw_capt_hyper, lr_ptr) == 40,
+              "mi_adamw_capt_hyper: ten 4-byte fields, then the lr pointer");
 
 // ---------------------------------------------------------------------------
 // Element math
@@ -88,24 +93,44 @@ __device__ __forceinline__ float maximum_nan(float a, float b) {
     return a < b ? b : a;
 }
 
+// The scalars one workgroup's element chain uses.  Default chain: the host's
+// per-step values (mi_adamw_hyper).  Capturable chain (kCapt): den_scale is
+// sqrt(bc2) * -step_size, divided by, and den_add is eps / -step_size.
+struct ElemScalars {
+    float wd_factor;
+    float lerp_w;
+    float beta2;
+    float one_minus_beta2;
+    float den_scale;       // 1 / bc2_sqrt (multiplied), or sqrt(bc2) * -step_size (divided by)
+    float den_add;         // eps, or eps / -step_size
+    float neg_step_size;   // default chain only
+    float grad_sign;
+};
+
 // One element of adam.py:419-547.  g already carries the clip scale and sign.
 // With kAms, x is amsgrad's running maximum of v and the denominator uses it.
-template <bool kAms>
+template <bool kAms, bool kCapt>
 __device__ __forceinline__ void adamw_elem(float& p, float g, float& m, float& v, float& x,
-                                           const mi_adamw_hyper& h) {
+                                           const ElemScalars& h) {
     p = p * h.wd_factor;                                   // adam.py:419 mul_
     m = lerp_fused(m, g, h.lerp_w);                        // adam.py:457 lerp_
     v = v * h.beta2;                                       // adam.py:476 mul_
     v = __builtin_fmaf(h.one_minus_beta2, g * g, v);       // adam.py:476 addcmul_
     float dv = v;
     if (kAms) {
-        x = maximum_nan(x, v);                             // adam.py:540 maximum(out=)
+        x = maximum_nan(x, v);                             // adam.py:512/540 maximum
         dv = x;
     }
-    float d = __builtin_sqrtf(dv);                         // adam.py:543/545 sqrt
-    d = d * h.inv_bc2_sqrt;                                //   / bc2_sqrt (reciprocal mul)
-    d = d + h.eps;                                         //   add_(eps)
-    p = __builtin_fmaf(h.neg_step_size, m / d, p);         // adam.py:547 addcdiv_
+    float d = __builtin_sqrtf(dv);                         // adam.py:520/545 sqrt
+    if (kCapt) {
+        d = d / h.den_scale;                               // adam.py:520-521 / (bc2_sqrt * -step_size)
+        d = d + h.den_add;                                 // adam.py:522 add_(eps / -step_size)
+        p = p + m / d;                                     // adam.py:527 addcdiv_, value 1
+    } else {
+        d = d * h.den_scale;                               //   / bc2_sqrt (reciprocal mul)
+        d = d + h.den_add;                                 //   add_(eps)
+        p = __builtin_fmaf(h.neg_step_size, m / d, p);     // adam.py:547 addcdiv_
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -158,17 +183,17 @@ __device__ __forceinline__ void st4_bf16(uint16_t* p, f32x4 v) {
 }
 
 // adamw_elem on the four lanes of a dwordx4 group.
-template <bool kAms>
+template <bool kAms, bool kCapt>
 __device__ __forceinline__ void adamw_vec(f32x4& p, f32x4 g, f32x4& m, f32x4& v, f32x4& x,
-                                          const mi_adamw_hyper& h) {
+                                          const ElemScalars& h) {
     float p0 = p.x, p1 = p.y, p2 = p.z, p3 = p.w;
     float m0 = m.x, m1 = m.y, m2 = m.z, m3 = m.w;
     float v0 = v.x, v1 = v.y, v2 = v.z, v3 = v.w;
     float x0 = x.x, x1 = x.y, x2 = x.z, x3 = x.w;
-    adamw_elem<kAms>(p0, g.x, m0, v0, x0, h);
-    adamw_elem<kAms>(p1, g.y, m1, v1, x1, h);
-    adamw_elem<kAms>(p2, g.z, m2, v2, x2, h);
-    adamw_elem<kAms>(p3, g.w, m3, v3, x3, h);
+    adamw_elem<kAms, kCapt>(p0, g.x, m0, v0, x0, h);
+    adamw_elem<kAms, kCapt>(p1, g.y, m1, v1, x1, h);
+    adamw_elem<kAms, kCapt>(p2, g.z, m2, v2, x2, h);
+    adamw_elem<kAms, kCapt>(p3, g.w, m3, v3, x3, h);
     p = f32x4{p0, p1, p2, p3};
     m = f32x4{m0, m1, m2, m3};
     v = f32x4{v0, v1, v2, v3};
@@ -218,9 +243,9 @@ struct TableSource {
     const mi_adamw_tensor* tensors;
     const mi_adamw_chunk* chunks;
     __device__ __forceinline__ void get(int64_t c, int64_t chunk_elems, mi_adamw_tensor& t,
-                                        int64_t& begin, int64_t& end) const {
+                                        int64_t& begin, int64_t& end, int32_t& row) const {
         const CONSTANT int32_t* ck = (const CONSTANT int32_t*)(chunks + c);
-        const int32_t row = ck[0];
+        row = ck[0];
         const int32_t index = ck[1];
         // mi_adamw_tensor is 8 eight-byte words: 6 pointers, numel, (hyper, flags).
         const CONSTANT uint64_t* w = (const CONSTANT uint64_t*)(tensors + row);
@@ -241,10 +266,70 @@ struct TableSource {
 struct FlatSource {
     mi_adamw_tensor t;
     __device__ __forceinline__ void get(int64_t c, int64_t chunk_elems, mi_adamw_tensor& out,
-                                        int64_t& begin, int64_t& end) const {
+                                        int64_t& begin, int64_t& end, int32_t& row) const {
         out = t;
+        row = 0;
         begin = c * chunk_elems;
         end = begin + chunk_elems < t.numel ? begin + chunk_elems : t.numel;
+    }
+};
+
+// ---------------------------------------------------------------------------
+// Per-step scalars: where a workgroup's ElemScalars come from.
+
+// Default chain: the host formed every per-step value (adam.py:529-536).
+struct StaticHyper {
+    static constexpr bool kCapt = false;
+    HyperPack hp;
+    __device__ __forceinline__ ElemScalars get(const mi_adamw_tensor& t, int32_t) const {
+        const mi_adamw_hyper& x = hp.h[t.hyper];
+        return ElemScalars{x.wd_factor, x.lerp_w, x.beta2, x.one_minus_beta2,
+                           x.inv_bc2_sqrt, x.eps, x.neg_step_size, x.grad_sign};
+    }
+};
+
+struct CaptPack {
+    mi_adamw_capt_hyper h[MI_ADAMW_MAX_HYPER];
+};
+
+// Capturable chain: adam.py:480-522 from the tensor's device step count, in
+// fp32 with one rounding per ATen op (powf is the device pow torch-ROCm's pow
+// kernel calls; `float / tensor` is a reciprocal times the float).  The step
+// counts and a device lr were written by earlier work on the stream and do not
+// change during the launch, so they are read through the constant address
+// space (scalar loads).
+struct CaptHyper {
+    static constexpr bool kCapt = true;
+    CaptPack cp;
+    const float* steps;
+    const int32_t* step_index;
+    __device__ __forceinline__ ElemScalars get(const mi_adamw_tensor& t, int32_t row) const {
+        const mi_adamw_capt_hyper& c = cp.h[t.hyper];
+        const int32_t slot = *((const CONSTANT int32_t*)(step_index) + row);
+        const float step = *((const CONSTANT float*)(steps) + slot);
+        const float bc1 = 1.0f - powf(c.beta1, step);                 // adam.py:488
+        const float bc2 = 1.0f - powf(c.beta2, step);                 // adam.py:497
+        float lr = c.lr;
+        float wd_factor = c.wd_factor;
+        if (c.lr_mode == MI_ADAMW_LR_DEVICE) {
+            lr = *(const CONSTANT float*)(c.lr_ptr);
+            // adam.py:419 with a tensor lr: 1 - lr * weight_decay, two fp32 ops
+            wd_factor = c.weight_decay != 0.0f ? 1.0f - lr * c.weight_decay : 1.0f;
+        }
+        // adam.py:499: lr / bc1; a float lr divides as (1 / bc1) * lr
+        const float step_size = c.lr_mode == MI_ADAMW_LR_FLOAT ? (1.0f / bc1) * lr : lr / bc1;
+        const float neg = -step_size;                                 // adam.py:500
+        const float bc2_sqrt = __builtin_sqrtf(bc2);                  // adam.py:502
+        ElemScalars h;
+        h.wd_factor = wd_factor;
+        h.lerp_w = c.lerp_w;
+        h.beta2 = c.beta2;
+        h.one_minus_beta2 = c.one_minus_beta2;
+        h.den_scale = bc2_sqrt * neg;                                 // adam.py:521
+        h.den_add = (1.0f / neg) * c.eps;                             // adam.py:522 eps / neg
+        h.neg_step_size = 0.0f;
+        h.grad_sign = c.grad_sign;
+        return h;
     }
 };
 
@@ -300,7 +385,8 @@ __device__ __forceinline__ int64_t sumsq_chunks(const Src& src, int64_t c, int64
                                                 double& acc0, double& acc1) {
     mi_adamw_tensor t;
     int64_t begin = 0, end = 0;
-    if (c < c_end) src.get(c, chunk_elems, t, begin, end);
+    int32_t row;
+    if (c < c_end) src.get(c, chunk_elems, t, begin, end, row);
     for (; c < c_end; c += stride) {
         const float* __restrict__ g = t.grad;
         const bool vec = t.flags & MI_ADAMW_T_VEC;
@@ -322,7 +408,7 @@ __device__ __forceinline__ int64_t sumsq_chunks(const Src& src, int64_t c, int64
         mi_adamw_tensor tn;
         int64_t bn = 0, en = 0;
         const bool more = c + stride < c_end;
-        if (more) src.get(c + stride, chunk_elems, tn, bn, en);
+        if (more) src.get(c + stride, chunk_elems, tn, bn, en, row);
         __builtin_amdgcn_sched_barrier(0);
         if (full) {
             sumsq4(a, acc0, acc1);
@@ -413,19 +499,24 @@ struct Tile {
     }
 };
 
-template <class Src, typename StateT, bool kClip, bool kCopy, bool kWriteGrad, bool kAms>
+template <class Src, class HS, typename StateT, bool kClip, bool kCopy, bool kWriteGrad, bool kAms>
 __global__ __launch_bounds__(kUpdThreads) void mi_adamw_update_kernel(
-    Src src, int64_t n_chunks, int64_t chunk_elems, HyperPack hp,
+    Src src, int64_t n_chunks, int64_t chunk_elems, HS hs,
     const float* __restrict__ grad_scale) {
     using IO = StateIO<StateT>;
     using T = Tile<StateT, kAms>;
+    constexpr bool kCapt = HS::kCapt;
     const float scale = kClip ? *grad_scale : 1.0f;
     for (int64_t c = blockIdx.x; c < n_chunks; c += gridDim.x) {
         mi_adamw_tensor t;
         int64_t begin, end;
-        src.get(c, chunk_elems, t, begin, end);
-        const mi_adamw_hyper h = hp.h[t.hyper];
-        const float gmul = h.grad_sign;
+        int32_t row;
+        src.get(c, chunk_elems, t, begin, end, row);
+        // Default chain: the scalars are kernel arguments.  Capturable chain: they
+        // take a few hundred instructions (two powf, three divisions), formed once
+        // the first tile's loads are in flight.
+        ElemScalars h;
+        if (!kCapt) h = hs.get(t, row);
         float* __restrict__ P = t.param;
         float* __restrict__ G = t.grad;
         void* __restrict__ M = t.exp_avg;
@@ -440,6 +531,11 @@ __global__ __launch_bounds__(kUpdThreads) void mi_adamw_update_kernel(
             if (i < vend) {
                 T cur;
                 cur.load(P, G, M, V, X, i);
+                if (kCapt) {
+                    __builtin_amdgcn_sched_barrier(0);
+                    h = hs.get(t, row);
+                }
+                const float gmul = h.grad_sign;
                 while (true) {
                     const int64_t j = i + kUpdTile;
                     const bool more = j < vend;
@@ -449,7 +545,7 @@ __global__ __launch_bounds__(kUpdThreads) void mi_adamw_update_kernel(
                     if (kClip) gs = f32x4{gs.x * scale, gs.y * scale, gs.z * scale, gs.w * scale};
                     if (kWriteGrad) st4(G + i, gs);
                     gs = f32x4{gs.x * gmul, gs.y * gmul, gs.z * gmul, gs.w * gmul};
-                    adamw_vec<kAms>(cur.p, gs, cur.m, cur.v, cur.x, h);
+                    adamw_vec<kAms, kCapt>(cur.p, gs, cur.m, cur.v, cur.x, h);
                     st4(P + i, cur.p);
                     IO::st(M, i, cur.m);
                     IO::st(V, i, cur.v);
@@ -463,6 +559,8 @@ __global__ __launch_bounds__(kUpdThreads) void mi_adamw_update_kernel(
         }
         // Scalar path: the ragged tail of a vector tensor, or a whole tensor
         // whose pointers are not aligned for dwordx4.
+        if (kCapt && vend < end) h = hs.get(t, row);
+        const float gmul = h.grad_sign;
         for (int64_t j = vend + threadIdx.x; j < end; j += kUpdThreads) {
             float g1 = ld1(G + j);
             if (kClip) g1 = g1 * scale;
@@ -470,7 +568,7 @@ __global__ __launch_bounds__(kUpdThreads) void mi_adamw_update_kernel(
             g1 = g1 * gmul;
             float p1 = ld1(P + j), m1 = IO::ld1(M, j), v1 = IO::ld1(V, j);
             float x1 = kAms ? IO::ld1(X, j) : 0.0f;
-            adamw_elem<kAms>(p1, g1, m1, v1, x1, h);
+            adamw_elem<kAms, kCapt>(p1, g1, m1, v1, x1, h);
             st1(P + j, p1);
             IO::st1(M, j, m1);
             IO::st1(V, j, v1);
@@ -489,7 +587,8 @@ __global__ __launch_bounds__(kUpdThreads) void mi_adamw_scale_kernel(
     for (int64_t c = blockIdx.x; c < n_chunks; c += gridDim.x) {
         mi_adamw_tensor t;
         int64_t begin, end;
-        src.get(c, chunk_elems, t, begin, end);
+        int32_t row;
+        src.get(c, chunk_elems, t, begin, end, row);
         float* __restrict__ G = t.grad;
         int64_t vend = begin;
         if (t.flags & MI_ADAMW_T_VEC) {
@@ -554,25 +653,26 @@ int launch_norm(const Src& src, int64_t n_chunks, int64_t chunk_elems, float max
     return launch_status();
 }
 
-template <class Src, typename StateT, bool kClip, bool kCopy, bool kWriteGrad, bool kAms>
-int launch_update_k(const Src& src, int64_t n_chunks, int64_t chunk_elems, const HyperPack& hp,
+template <class Src, class HS, typename StateT, bool kClip, bool kCopy, bool kWriteGrad,
+          bool kAms>
+int launch_update_k(const Src& src, int64_t n_chunks, int64_t chunk_elems, const HS& hs,
                     const float* scale, unsigned grid, hipStream_t s) {
-    hipLaunchKernelGGL((mi_adamw_update_kernel<Src, StateT, kClip, kCopy, kWriteGrad, kAms>),
-                       dim3(grid), dim3(kUpdThreads), 0, s, src, n_chunks, chunk_elems, hp, scale);
+    hipLaunchKernelGGL((mi_adamw_update_kernel<Src, HS, StateT, kClip, kCopy, kWriteGrad, kAms>),
+                       dim3(grid), dim3(kUpdThreads), 0, s, src, n_chunks, chunk_elems, hs, scale);
     return launch_status();
 }
 
 // Runtime flags -> kernel template: one instantiation per (copy, write-grad, amsgrad).
-template <class Src, typename StateT, bool kClip>
-int launch_update_cw(const Src& src, int64_t n_chunks, int64_t chunk_elems, const HyperPack& hp,
+template <class Src, class HS, typename StateT, bool kClip>
+int launch_update_cw(const Src& src, int64_t n_chunks, int64_t chunk_elems, const HS& hs,
                      const float* scale, int32_t flags, unsigned grid, hipStream_t s) {
     const int sel = ((flags & MI_ADAMW_F_BF16_COPY) ? 1 : 0) |
                     ((flags & MI_ADAMW_F_WRITE_GRAD) ? 2 : 0) |
                     ((flags & MI_ADAMW_F_AMSGRAD) ? 4 : 0);
 #define MI_ADAMW_SEL(k, C, W, A)                                                              \
     case k:                                                                                   \
-        return launch_update_k<Src, StateT, kClip, C, W, A>(src, n_chunks, chunk_elems, hp,  \
-                                                             scale, grid, s);
+        return launch_update_k<Src, HS, StateT, kClip, C, W, A>(src, n_chunks, chunk_elems,  \
+                                                                 hs, scale, grid, s);
     switch (sel) {
         MI_ADAMW_SEL(0, false, false, false)
         MI_ADAMW_SEL(1, true, false, false)
@@ -587,8 +687,8 @@ int launch_update_cw(const Src& src, int64_t n_chunks, int64_t chunk_elems, cons
     return MI_ADAMW_E_INVALID;
 }
 
-template <class Src>
-int launch_update(const Src& src, int64_t n_chunks, int64_t chunk_elems, const HyperPack& hp,
+template <class Src, class HS>
+int launch_update(const Src& src, int64_t n_chunks, int64_t chunk_elems, const HS& hs,
                   const float* scale, int32_t state_dtype, int32_t flags, int32_t max_blocks,
                   hipStream_t s) {
     if (n_chunks <= 0 || !chunk_elems_ok(chunk_elems)) return MI_ADAMW_E_INVALID;
@@ -601,14 +701,14 @@ int launch_update(const Src& src, int64_t n_chunks, int64_t chunk_elems, const H
     if (clip && !scale) return MI_ADAMW_E_INVALID;
     const unsigned grid = grid_for(n_chunks, max_blocks, kUpdThreads);
     if (state_dtype == MI_ADAMW_STATE_F32)
-        return clip ? launch_update_cw<Src, float, true>(src, n_chunks, chunk_elems, hp, scale,
-                                                          flags, grid, s)
-                    : launch_update_cw<Src, float, false>(src, n_chunks, chunk_elems, hp, scale,
-                                                           flags, grid, s);
-    return clip ? launch_update_cw<Src, uint16_t, true>(src, n_chunks, chunk_elems, hp, scale,
-                                                         flags, grid, s)
-                : launch_update_cw<Src, uint16_t, false>(src, n_chunks, chunk_elems, hp, scale,
-                                                          flags, grid, s);
+        return clip ? launch_update_cw<Src, HS, float, true>(src, n_chunks, chunk_elems, hs,
+                                                              scale, flags, grid, s)
+                    : launch_update_cw<Src, HS, float, false>(src, n_chunks, chunk_elems, hs,
+                                                               scale, flags, grid, s);
+    return clip ? launch_update_cw<Src, HS, uint16_t, true>(src, n_chunks, chunk_elems, hs, scale,
+                                                             flags, grid, s)
+                : launch_update_cw<Src, HS, uint16_t, false>(src, n_chunks, chunk_elems, hs,
+                                                              scale, flags, grid, s);
 }
 
 // Validate one host-visible tensor descriptor for the flat entry points.
@@ -636,7 +736,8 @@ int check_flat(const mi_adamw_tensor* t, int32_t state_dtype, int32_t flags) {
 extern "C" {
 
 const char* mi_adamw_version(void) {
-    return "mi_adamw 2 gfx950 fused clip+adamw (fp32/bf16 state, bf16 copy, amsgrad, flat)";
+    return "mi_adamw 3 gfx950 fused clip+adamw (fp32/bf16 state, bf16 copy, amsgrad, flat, "
+           "capturable)";
 }
 
 const char* mi_adamw_strerror(int code) {
@@ -706,11 +807,11 @@ int mi_adamw_step(const mi_adamw_tensor* d_tensors, const mi_adamw_chunk* d_chun
                   int32_t max_blocks, void* stream) {
     if (!d_tensors || !d_chunks || !hypers || n_hyper <= 0 || n_hyper > MI_ADAMW_MAX_HYPER)
         return MI_ADAMW_E_INVALID;
-    HyperPack hp;
-    memset(&hp, 0, sizeof(hp));
-    memcpy(hp.h, hypers, sizeof(mi_adamw_hyper) * n_hyper);
+    StaticHyper hs;
+    memset(&hs, 0, sizeof(hs));
+    memcpy(hs.hp.h, hypers, sizeof(mi_adamw_hyper) * n_hyper);
     TableSource src{d_tensors, d_chunks};
-    return launch_update(src, n_chunks, chunk_elems, hp, d_grad_scale, state_dtype, flags,
+    return launch_update(src, n_chunks, chunk_elems, hs, d_grad_scale, state_dtype, flags,
                          max_blocks, static_cast<hipStream_t>(stream));
 }
 
@@ -720,14 +821,39 @@ int mi_adamw_step_flat(const mi_adamw_tensor* t, const mi_adamw_hyper* hyper,
     if (!hyper || !chunk_elems_ok(chunk_elems)) return MI_ADAMW_E_INVALID;
     int rc = check_flat(t, state_dtype, flags);
     if (rc != MI_ADAMW_OK) return rc;
-    HyperPack hp;
-    memset(&hp, 0, sizeof(hp));
-    hp.h[0] = *hyper;
+    StaticHyper hs;
+    memset(&hs, 0, sizeof(hs));
+    hs.hp.h[0] = *hyper;
     FlatSource src;
     src.t = *t;
     src.t.hyper = 0;
     const int64_t n_chunks = (t->numel + chunk_elems - 1) / chunk_elems;
-    return launch_update(src, n_chunks, chunk_elems, hp, d_grad_scale, state_dtype, flags,
+    return launch_update(src, n_chunks, chunk_elems, hs, d_grad_scale, state_dtype, flags,
+                         max_blocks, static_cast<hipStream_t>(stream));
+}
+
+int mi_adamw_step_capturable(const mi_adamw_tensor* d_tensors, const mi_adamw_chunk* d_chunks,
+                             int64_t n_chunks, int64_t chunk_elems,
+                             const mi_adamw_capt_hyper* hypers, int32_t n_hyper,
+                             const float* d_steps, const int32_t* d_step_index,
+                             const float* d_grad_scale, int32_t state_dtype, int32_t flags,
+                             int32_t max_blocks, void* stream) {
+    if (!d_tensors || !d_chunks || !hypers || n_hyper <= 0 || n_hyper > MI_ADAMW_MAX_HYPER ||
+        !d_steps || !d_step_index)
+        return MI_ADAMW_E_INVALID;
+    for (int32_t i = 0; i < n_hyper; ++i) {
+        const int32_t mode = hypers[i].lr_mode;
+        if (mode != MI_ADAMW_LR_FLOAT && mode != MI_ADAMW_LR_VALUE && mode != MI_ADAMW_LR_DEVICE)
+            return MI_ADAMW_E_INVALID;
+        if (mode == MI_ADAMW_LR_DEVICE && !hypers[i].lr_ptr) return MI_ADAMW_E_INVALID;
+    }
+    CaptHyper hs;
+    memset(&hs, 0, sizeof(hs));
+    memcpy(hs.cp.h, hypers, sizeof(mi_adamw_capt_hyper) * n_hyper);
+    hs.steps = d_steps;
+    hs.step_index = d_step_index;
+    TableSource src{d_tensors, d_chunks};
+    return launch_update(src, n_chunks, chunk_elems, hs, d_grad_scale, state_dtype, flags,
                          max_blocks, static_cast<hipStream_t>(stream));
 }
 

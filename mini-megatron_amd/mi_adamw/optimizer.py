@@ -18,12 +18,16 @@ replaces the per-tensor loop with the kernels of libmi_adamw:
   applied on the device with no host synchronisation;
 * ``mi_adamw_step`` / ``mi_adamw_step_flat`` -- the AdamW update of every
   tensor, with fp32 or bf16 moments, an optional bf16 model copy and amsgrad's
-  running maximum (adam.py:538-543) for the groups that set it.
+  running maximum (adam.py:538-543) for the groups that set it;
+* ``mi_adamw_step_capturable`` -- the same update in torch's capturable chain
+  (capturable=True): step counts on the device, the per-step scalars formed
+  in the kernel, so that step() can be recorded into a HIP graph.
 
 Per-element results match ``torch.optim.AdamW(foreach=False)`` on the same GPU
 tensors: the kernels follow the fp32 op chain and the fused multiply-adds of
 torch-ROCm's ATen kernels, and the per-step scalars below are computed on the
-host in float64 exactly as adam.py:414-536 computes them.
+host in float64 exactly as adam.py:414-536 computes them (with
+capturable=True: on the device in fp32, as adam.py:480-527 does).
 """
 from __future__ import annotations
 
@@ -86,6 +90,50 @@ def _hyper(group: dict, step: float) -> _lib.Hyper:
     )
 
 
+def _capt_hyper(group: dict, device: torch.device) -> _lib.CaptHyper:
+    """The fp32 constants of one group for the capturable chain (adam.py:396-527 with
+    capturable=True).  Nothing depends on the step count, which the kernel reads
+    from the device.  A float lr enters ``lr / bias_correction1`` as
+    ``bc1.reciprocal() * lr`` (Tensor.__rtruediv__); a tensor lr as a true
+    division, read by the kernel when it lives on the device."""
+    lr = group["lr"]
+    beta1, beta2 = (float(b) for b in group["betas"])
+    wd = float(group["weight_decay"])
+    f32 = np.float32
+    h = _lib.CaptHyper(
+        beta1=float(f32(beta1)), beta2=float(f32(beta2)), lerp_w=float(f32(1 - beta1)),
+        one_minus_beta2=float(f32(1 - beta2)), eps=float(f32(group["eps"])),
+        grad_sign=-1.0 if group["maximize"] else 1.0, lr=0.0, wd_factor=1.0, weight_decay=0.0,
+        lr_mode=_lib.LR_FLOAT, lr_ptr=None)
+    if not isinstance(lr, torch.Tensor):
+        h.lr = float(f32(lr))
+        h.wd_factor = float(f32(1 - float(lr) * wd)) if wd != 0 else 1.0
+    elif lr.device.type == "cpu":
+        lr_t = lr.detach().reshape(())
+        if lr_t.dtype != torch.float32:
+            raise NotImplementedError("FusedAdamW(capturable=True): a tensor lr must be float32")
+        h.lr_mode = _lib.LR_VALUE
+        h.lr = float(lr_t.item())
+        h.wd_factor = float(f32((1 - lr_t * wd).item())) if wd != 0 else 1.0
+    else:
+        if lr.dtype != torch.float32 or lr.device != device or lr.numel() != 1:
+            raise NotImplementedError("FusedAdamW(capturable=True): a device lr must be a "
+                                      "one-element float32 tensor on the parameters' device")
+        h.lr_mode = _lib.LR_DEVICE
+        h.lr_ptr = lr.data_ptr()
+        h.weight_decay = float(f32(wd))
+    return h
+
+
+def _refuse_under_capture(what: str) -> None:
+    """Host-to-device uploads cannot be recorded into a graph: a step under capture
+    must find everything an earlier eager step built."""
+    if torch.cuda.is_available() and torch.cuda.is_current_stream_capturing():
+        raise RuntimeError(f"FusedAdamW: step() under graph capture, but {what} since the "
+                           "last eager step; run one eager step with the same parameters and "
+                           "gradient tensors before capturing")
+
+
 def _ptr(t: torch.Tensor | None) -> int:
     return 0 if t is None else t.data_ptr()
 
@@ -116,13 +164,17 @@ def _upload(arr: np.ndarray, device: torch.device) -> torch.Tensor:
 class _Launch:
     """Device-resident tensor and chunk tables for one kernel launch."""
 
-    __slots__ = ("rows", "chunks", "n_chunks", "n_rows", "host_rows", "tables", "src", "rest")
+    __slots__ = ("rows", "chunks", "n_chunks", "n_rows", "host_rows", "tables", "src", "rest",
+                 "step_index")
 
     def __init__(self, rows: np.ndarray, chunk_elems: int, device: torch.device,
                  tables: bool = False, src: np.ndarray | None = None,
-                 rest: np.ndarray | None = None):
+                 rest: np.ndarray | None = None, step_slots: np.ndarray | None = None):
         lib = _lib.load()
         self.n_rows = len(rows)
+        # capturable launches: row i's index into the device step buffer
+        self.step_index = (None if step_slots is None else
+                           _upload(np.ascontiguousarray(step_slots, dtype=np.int32), device))
         self.host_rows = rows.copy()
         self.tables = tables or len(rows) != 1
         # src[i]: the entry whose gradient row i points at (-1: a flat group row, whose
@@ -176,7 +228,11 @@ class FusedAdamW(Optimizer):
     global-norm clip: sum of squares, finalize, update).
 
     The constructor takes torch.optim.AdamW's arguments, with its defaults and
-    its ValueError checks (amsgrad and maximize work as in torch), plus
+    its ValueError checks (amsgrad and maximize work as in torch).  With
+    capturable=True the step counts live on the device and the step follows
+    torch's capturable op chain, so that step() can be recorded into a HIP
+    graph (torch.cuda.graph) once an eager step has built the launch tables;
+    results match torch.optim.AdamW(capturable=True, foreach=False).  Plus
     keyword-only options:
 
     max_grad_norm:    if set, clip the global gradient L2 norm to this value
@@ -196,8 +252,8 @@ class FusedAdamW(Optimizer):
                       stay allocated: zero_grad() zeroes them in place.
     chunk_elems:      elements per work chunk (multiple of 4096).
 
-    Not supported (NotImplementedError at construction): capturable,
-    differentiable, betas as tensors.
+    Not supported (NotImplementedError at construction): differentiable, betas
+    as tensors, param groups with different capturable settings.
     """
 
     def __init__(
@@ -255,8 +311,6 @@ class FusedAdamW(Optimizer):
             raise RuntimeError("`fused` does not support `differentiable`")
         if fused and foreach:
             raise RuntimeError("`fused` and `foreach` cannot be `True` together.")
-        if capturable:
-            raise NotImplementedError("FusedAdamW: capturable=True is not supported")
         if differentiable:
             raise NotImplementedError("FusedAdamW: differentiable=True is not supported")
         if max_grad_norm is not None and not max_grad_norm > 0:
@@ -266,6 +320,7 @@ class FusedAdamW(Optimizer):
         if chunk_elems <= 0 or chunk_elems % _lib.CHUNK_QUANTUM:
             raise ValueError(f"chunk_elems must be a positive multiple of {_lib.CHUNK_QUANTUM}")
 
+        self.capturable = bool(capturable)
         self.max_grad_norm = None if max_grad_norm is None else float(max_grad_norm)
         self.clip_write_grads = bool(clip_write_grads)
         self.state_dtype = state_dtype
@@ -288,8 +343,8 @@ class FusedAdamW(Optimizer):
         if self.flat_buffer:
             self._flat = FlatLayout(self.param_groups, self.state_dtype, self.bf16_copy)
 
-    _OPTIONS = ("max_grad_norm", "clip_write_grads", "state_dtype", "bf16_copy", "flat_buffer",
-                "chunk_elems", "max_blocks")
+    _OPTIONS = ("capturable", "max_grad_norm", "clip_write_grads", "state_dtype", "bf16_copy",
+                "flat_buffer", "chunk_elems", "max_blocks")
 
     def _reset_bookkeeping(self) -> None:
         """The state this class keeps beside torch's: step slots, the packed step buffer,
@@ -305,6 +360,7 @@ class FusedAdamW(Optimizer):
         self._workspace: dict[torch.device, tuple] = {}
         self._flat: FlatLayout | None = None
         self._copy_sync: dict[int, tuple[int, int]] | None = None
+        self._step_idx: tuple[tuple, torch.Tensor] | None = None
         self.timing_events = None
 
     # ------------------------------------------------------------------ torch API
@@ -352,6 +408,10 @@ class FusedAdamW(Optimizer):
             ps = param_group["params"]
             for p in ([ps] if isinstance(ps, torch.Tensor) else list(ps)):
                 self._check_copyable(p)
+        if hasattr(self, "capturable") and \
+                bool(param_group.get("capturable", self.capturable)) != self.capturable:
+            raise NotImplementedError("FusedAdamW: every param group must share the "
+                                      "optimizer's capturable setting")
         super().add_param_group(param_group)
         if not hasattr(self, "_slots"):
             return
@@ -363,26 +423,40 @@ class FusedAdamW(Optimizer):
         if not new:
             return
         old_n = len(self._step_views)
-        steps = torch.zeros(old_n + len(new), dtype=torch.float32)
+        steps = torch.zeros(old_n + len(new), dtype=torch.float32, device=self._steps.device)
         steps[:old_n] = self._steps
-        self._steps = steps
         for i, p in enumerate(new):
             self._slots[id(p)] = old_n + i
         self._step_views.extend([None] * len(new))
-        # Existing per-param step tensors are views of the old buffer: move them.
-        for p_id, slot in list(self._slots.items()):
-            if slot < old_n and self._step_views[slot] is not None:
-                self._step_views[slot] = self._steps[slot]
-        for p, st in self.state.items():
-            if isinstance(p, torch.Tensor) and id(p) in self._slots and "step" in st:
-                slot = self._slots[id(p)]
-                if self._step_views[slot] is not None:
-                    st["step"] = self._step_views[slot]
+        self._set_step_buffer(steps)
         if getattr(self, "bf16_copy", False) and not getattr(self, "flat_buffer", False):
             for p in new:
                 self._copies[id(p)] = self._new_copy(p)
         self._launch_cache = None
         self._recs = None
+
+    def _set_step_buffer(self, steps: torch.Tensor) -> None:
+        """Replace the packed step buffer; the per-param step views and the state's
+        "step" entries are re-pointed at the new one."""
+        self._steps = steps
+        for slot, view in enumerate(self._step_views):
+            if view is not None:
+                self._step_views[slot] = steps[slot]
+        for p, st in self.state.items():
+            if isinstance(p, torch.Tensor) and id(p) in self._slots and "step" in st:
+                view = self._step_views[self._slots[id(p)]]
+                if view is not None:
+                    st["step"] = view
+        self._step_idx = None
+
+    def _steps_for(self, device: torch.device) -> torch.Tensor:
+        """The packed step buffer where the step counts live: host memory, or with
+        capturable=True the parameters' device (adam.py:168-176 keeps a capturable
+        step on the parameter's device), moved there on first use."""
+        want = device if self.capturable else torch.device("cpu")
+        if self._steps.device != want:
+            self._set_step_buffer(self._steps.to(want))
+        return self._steps
 
     def zero_grad(self, set_to_none: bool = True) -> None:
         if self._flat is not None:
@@ -497,18 +571,23 @@ class FusedAdamW(Optimizer):
 
     @staticmethod
     def _after_load_state_dict(self: "FusedAdamW") -> None:
-        """Re-home loaded state: steps into the packed CPU buffer, moments in state_dtype."""
+        """Re-home loaded state: steps into the packed step buffer (host memory, or the
+        device with capturable=True), moments in state_dtype."""
         for group in self.param_groups:
             for p in group["params"]:
                 st = self.state.get(p)
                 if not st:
                     continue
                 slot = self._slots[id(p)]
+                steps = self._steps_for(p.device)
                 step = st.get("step")
                 if isinstance(step, torch.Tensor):
-                    self._steps[slot] = float(step.item())
+                    if self.capturable:
+                        steps[slot] = step.detach().reshape(()).to(steps)   # no host sync
+                    else:
+                        steps[slot] = float(step.item())
                 elif step is not None:
-                    self._steps[slot] = float(step)
+                    steps[slot] = float(step)
                 self._step_views[slot] = self._steps[slot]
                 st["step"] = self._step_views[slot]
                 for key in ("exp_avg", "exp_avg_sq", "max_exp_avg_sq"):
@@ -603,6 +682,9 @@ class FusedAdamW(Optimizer):
             return loss
         flat = self._flat
         ams_g = [bool(g["amsgrad"]) for g in self.param_groups]
+        device = entries[0][0].p.device
+        if self.capturable:
+            self._steps_for(device)
         views = self._step_views
         for i, (rec, g) in enumerate(entries):
             if flat is not None and not flat.is_grad_view(rec.p, g):
@@ -625,32 +707,44 @@ class FusedAdamW(Optimizer):
                 # amsgrad switched on for a group after its state was created
                 self._init_vmax(rec.p, st)
 
-        # step_t += 1 for every param with a grad (adam.py:414), in one op.
-        if len(entries) == len(self._step_views):
-            self._steps += 1
+        if self.capturable:
+            # step_t += 1 on the device (adam.py:414), one op for every param with a
+            # grad; one constant set per group, the kernel forms the per-step values
+            if len(entries) == len(self._step_views):
+                self._steps.add_(1)
+            else:
+                self._steps.index_add_(0, *self._step_increment(entries, device))
+            gis = sorted({rec.gi for rec, _ in entries})
+            remap = {gi: i for i, gi in enumerate(gis)}
+            hyper_idx = [remap[rec.gi] for rec, _ in entries]
+            hypers = [_capt_hyper(self.param_groups[gi], device) for gi in gis]
+            hyper_ams = [ams_g[gi] for gi in gis]
         else:
-            idx = torch.as_tensor([rec.slot for rec, _ in entries], dtype=torch.long)
-            self._steps[idx] += 1
-        steps_np = self._steps.numpy()
+            # step_t += 1 for every param with a grad (adam.py:414), in one op.
+            if len(entries) == len(self._step_views):
+                self._steps += 1
+            else:
+                idx = torch.as_tensor([rec.slot for rec, _ in entries], dtype=torch.long)
+                self._steps[idx] += 1
+            steps_np = self._steps.numpy()
 
-        # One hyperparameter set per distinct (group, step value).
-        keys: dict[tuple[int, float], int] = {}
-        sel = steps_np[[rec.slot for rec, _ in entries]]
-        if len(self.param_groups) == 1 and sel.min() == sel.max():
-            keys[(0, float(sel[0]))] = 0          # the usual case: one set for everything
-            hyper_idx = [0] * len(entries)
-        else:
-            hyper_idx = []
-            for (rec, _), step in zip(entries, sel.tolist()):
-                k = (rec.gi, step)
-                h = keys.get(k)
-                if h is None:
-                    h = keys[k] = len(keys)
-                hyper_idx.append(h)
-        hypers = [_hyper(self.param_groups[gi], step) for (gi, step) in keys]
-        hyper_ams = [ams_g[gi] for (gi, _) in keys]
+            # One hyperparameter set per distinct (group, step value).
+            keys: dict[tuple[int, float], int] = {}
+            sel = steps_np[[rec.slot for rec, _ in entries]]
+            if len(self.param_groups) == 1 and sel.min() == sel.max():
+                keys[(0, float(sel[0]))] = 0          # the usual case: one set for everything
+                hyper_idx = [0] * len(entries)
+            else:
+                hyper_idx = []
+                for (rec, _), step in zip(entries, sel.tolist()):
+                    k = (rec.gi, step)
+                    h = keys.get(k)
+                    if h is None:
+                        h = keys[k] = len(keys)
+                    hyper_idx.append(h)
+            hypers = [_hyper(self.param_groups[gi], step) for (gi, step) in keys]
+            hyper_ams = [ams_g[gi] for (gi, _) in keys]
 
-        device = entries[0][0].p.device
         with torch.cuda.device(device):
             self._launch(entries, hyper_idx, hypers, hyper_ams, device)
         if self._copy_sync is not None:
@@ -659,10 +753,24 @@ class FusedAdamW(Optimizer):
                 self._copy_sync[id(rec.p)] = (rec.p._version, rec.p.data_ptr())
         return loss
 
+    def _step_increment(self, entries, device):
+        """(index, ones) on the device for index_add_ of the stepped params' counts,
+        kept while the same params step (built outside graph capture)."""
+        key = tuple(rec.slot for rec, _ in entries)
+        cached = self._step_idx
+        if cached is None or cached[0] != key or cached[1].device != device:
+            _refuse_under_capture("the set of parameters with gradients changed")
+            idx = torch.as_tensor(key, dtype=torch.long).to(device)
+            cached = self._step_idx = (key, idx, torch.ones(len(key), device=device))
+        return cached[1], cached[2]
+
     def _adopt_step(self, p, st, slot):
         """state["step"] was replaced from outside: copy its value into the buffer."""
         step = st["step"]
-        self._steps[slot] = float(step.item()) if isinstance(step, torch.Tensor) else float(step)
+        if isinstance(step, torch.Tensor) and self.capturable:
+            self._steps[slot] = step.detach().reshape(()).to(self._steps)
+        else:
+            self._steps[slot] = float(step.item()) if isinstance(step, torch.Tensor) else float(step)
         self._step_views[slot] = self._steps[slot]
         st["step"] = self._step_views[slot]
 
@@ -684,6 +792,12 @@ class FusedAdamW(Optimizer):
         return self._tensor_rows(entries, hyper_idx, ams)
 
     def _new_launch(self, entries, hyper_idx, ams, device) -> _Launch:
+        if self.capturable:
+            # one row per tensor (each has its own device step count), always as tables
+            rows, src, rest = self._tensor_rows(entries, hyper_idx, ams)
+            slots = np.asarray([entries[i][0].slot for i in src], dtype=np.int32)
+            return _Launch(rows, self.chunk_elems, device, tables=True, src=src, rest=rest,
+                           step_slots=slots)
         rows, src, rest = self._rows(entries, hyper_idx, ams)
         return _Launch(rows, self.chunk_elems, device, src=src, rest=rest)
 
@@ -810,6 +924,7 @@ class FusedAdamW(Optimizer):
         if cache is not None and cache[0] == sig and cache[1] == device:
             launches, norm_launch = cache[2], cache[3]
             if cache[4] != grads:
+                _refuse_under_capture("gradient tensors moved")
                 # torch checks shape, dtype and device when .grad is assigned; the
                 # kernels also need dense storage
                 for rec, g in entries:
@@ -822,6 +937,7 @@ class FusedAdamW(Optimizer):
                     norm_launch.patch_grads(garr, device)
                 self._launch_cache = (sig, device, launches, norm_launch, grads)
         else:
+            _refuse_under_capture("the parameters, state or hyperparameter grouping changed")
             for rec, g in entries:
                 self._check_param(rec.p, g)
                 if rec.p.device != device:
@@ -864,6 +980,14 @@ class FusedAdamW(Optimizer):
             if launch.n_chunks == 0:
                 continue
             lflags = flags | (_lib.F_AMSGRAD if ams else 0)
+            if self.capturable:
+                carr = (_lib.CaptHyper * len(hs))(*hs)
+                _lib.check(lib.mi_adamw_step_capturable(
+                    launch.rows.data_ptr(), launch.chunks.data_ptr(), launch.n_chunks,
+                    self.chunk_elems, carr, len(hs), self._steps.data_ptr(),
+                    launch.step_index.data_ptr(), coef.data_ptr(), state_code, lflags,
+                    self.max_blocks, stream), "mi_adamw_step_capturable")
+                continue
             harr = (_lib.Hyper * len(hs))(*hs)
             if launch.n_rows == 1:
                 row = self._row_struct(launch)

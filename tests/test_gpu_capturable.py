@@ -1,0 +1,236 @@
+"""GPU: FusedAdamW(capturable=True) against torch.optim.AdamW(capturable=True, foreach=False),
+and its step recorded into a HIP graph (torch.cuda.graph) and replayed.
+
+torch's capturable chain keeps the step counts on the device and forms the
+per-step values there in fp32 (adam.py:480-527): ``beta ** step`` by the device
+pow, ``lr / bc1`` (a float lr as ``bc1.reciprocal() * lr``), ``sqrt(bc2) *
+-step_size`` and ``eps / -step_size``, then ``p += m / (sqrt(v) / (sqrt(bc2) *
+-step_size) + eps / -step_size)``.  The kernel forms the same values in every
+workgroup from the tensor's device step count, so parameters, moments and step
+counts must be bit-identical step after step, eager or replayed from a graph.
+"""
+from __future__ import annotations
+
+import copy
+
+import pytest
+import torch
+
+from _helpers import clone_params, make_params, max_ulp, max_ulp_all, set_grads
+
+pytestmark = [
+    pytest.mark.gpu,
+    # torch warns once per optimizer that capturable=True runs uncaptured
+    pytest.mark.filterwarnings("ignore:This instance was constructed with capturable=True"),
+]
+
+SHAPES = [(64, 48), (48,), (144, 48), (4099,), (3,), (7, 5), (70001,), (65536 + 12,)]
+
+
+@pytest.fixture(scope="module")
+def dev():
+    if not torch.cuda.is_available():
+        pytest.fail("GPU test run without a ROCm GPU")
+    return torch.device("cuda", 0)
+
+
+def _pair(dev, shapes=SHAPES, opt_kw=None, lr=6e-4, lr_ours=None, **hp):
+    import mi_adamw
+    ref = make_params(shapes, dev)
+    ours = clone_params(ref)
+    topt = torch.optim.AdamW(ref, lr=lr, foreach=False, capturable=True, **hp)
+    # foreach=False on both sides: a state dict carries it to whichever optimizer loads it
+    oopt = mi_adamw.FusedAdamW(ours, lr=lr if lr_ours is None else lr_ours, foreach=False,
+                               capturable=True, **hp, **(opt_kw or {}))
+    return ref, ours, topt, oopt
+
+
+def _copy_grads(ref, ours):
+    for p, q in zip(ref, ours):
+        q.grad = p.grad.clone()
+
+
+def _same(ref, ours, topt, oopt):
+    torch.cuda.synchronize()
+    assert max_ulp_all(ref, ours) == 0
+    for p, q in zip(ref, ours):
+        ts, os_ = topt.state[p], oopt.state[q]
+        assert os_["step"].device == q.device and os_["step"].dtype == torch.float32
+        assert torch.equal(ts["step"], os_["step"])
+        assert max_ulp(ts["exp_avg"], os_["exp_avg"]) == 0
+        assert max_ulp(ts["exp_avg_sq"], os_["exp_avg_sq"]) == 0
+        if "max_exp_avg_sq" in ts:
+            assert max_ulp(ts["max_exp_avg_sq"], os_["max_exp_avg_sq"]) == 0
+
+
+@pytest.mark.parametrize("betas,lr,wd,maximize,amsgrad", [
+    ((0.9, 0.999), 6e-4, 0.1, False, False),   # mini-megatron's defaults (config.py:11,13)
+    ((0.9, 0.95), 3e-4, 0.1, True, False),     # maximize
+    ((0.3, 0.95), 1e-3, 0.0, False, False),    # lerp weight 0.7 (other Lerp.h branch), no decay
+    ((0.9, 0.999), 6e-4, 0.1, False, True),    # amsgrad
+    ((0.9, 0.95), 0.0, 0.1, False, False),     # lr 0: step_size 0, both denominator terms -inf
+])
+def test_capturable_chained_matches_torch_bitwise(dev, betas, lr, wd, maximize, amsgrad):
+    ref, ours, topt, oopt = _pair(dev, lr=lr, betas=betas, weight_decay=wd, maximize=maximize,
+                                  amsgrad=amsgrad)
+    for step in range(1, 11):
+        set_grads(ref, step, 1e-3)
+        _copy_grads(ref, ours)
+        topt.step()
+        oopt.step()
+        _same(ref, ours, topt, oopt)
+
+
+@pytest.mark.parametrize("where", ["cuda", "cpu"])
+def test_capturable_tensor_lr_with_scheduler(dev, where):
+    """A tensor lr, driven by LambdaLR (which fill_()s it) with warm-up from 0
+    (main.py:36-43): on the device the kernel reads it, on the host the step passes
+    its value; both divide lr / bc1 truly, as torch does for a tensor lr."""
+    d = dev if where == "cuda" else torch.device("cpu")
+    ref, ours, topt, oopt = _pair(dev, lr=torch.tensor(6e-4, device=d),
+                                  lr_ours=torch.tensor(6e-4, device=d), weight_decay=0.1)
+    lam = lambda s: min(1.0, s / 3) * (0.5 + 0.5 / (1 + s))   # noqa: E731
+    tsch = torch.optim.lr_scheduler.LambdaLR(topt, lam)
+    osch = torch.optim.lr_scheduler.LambdaLR(oopt, lam)
+    for step in range(1, 8):
+        set_grads(ref, step, 1e-3)
+        _copy_grads(ref, ours)
+        topt.step()
+        oopt.step()
+        tsch.step()
+        osch.step()
+        _same(ref, ours, topt, oopt)
+    assert float(oopt.param_groups[0]["lr"]) == float(topt.param_groups[0]["lr"]) > 0
+
+
+def test_capturable_clip_copy_and_flat(dev):
+    """The fused clip, the bf16 copy and the flat layout in the capturable chain,
+    against torch's capturable step after clip_grads_with_norm_ with the same norm."""
+    for flat in (False, True):
+        ref, ours, topt, oopt = _pair(dev, weight_decay=0.1, opt_kw=dict(
+            max_grad_norm=1.0, bf16_copy=True, flat_buffer=flat))
+        for step in range(1, 6):
+            set_grads(ref, step, 1e-2)
+            for p, q in zip(ref, ours):
+                if flat:
+                    q.grad.copy_(p.grad)
+                else:
+                    q.grad = p.grad.clone()
+            oopt.step()
+            want = torch.nn.utils.get_total_norm([p.grad for p in ref])
+            assert abs(oopt.last_grad_norm.item() - want.item()) <= 1e-6 * want.item()
+            torch.nn.utils.clip_grads_with_norm_(ref, 1.0, oopt.last_grad_norm.clone())
+            topt.step()
+            _same(ref, ours, topt, oopt)
+        for q in ours:
+            assert torch.equal(oopt.bf16_param(q), q.detach().to(torch.bfloat16))
+
+
+def test_capturable_state_dict_interchange(dev):
+    """Checkpoints move between torch's capturable AdamW, FusedAdamW(capturable=True)
+    and a non-capturable torch AdamW (host step counts), mid-training.  Each state
+    dict is deep-copied, as torch.save / torch.load hand it over: load_state_dict
+    keeps the very tensors of a live state dict whose dtype and device already fit."""
+    import mi_adamw
+    ref, ours, topt, oopt = _pair(dev, weight_decay=0.1)
+    for step in range(1, 4):
+        set_grads(ref, step, 1e-3)
+        _copy_grads(ref, ours)
+        topt.step()
+        oopt.step()
+    # torch -> ours, into a fresh capturable FusedAdamW
+    ours2 = clone_params(ref)
+    o2 = mi_adamw.FusedAdamW(ours2, lr=6e-4, weight_decay=0.1, foreach=False, capturable=True)
+    o2.load_state_dict(copy.deepcopy(topt.state_dict()))
+    # ours -> torch capturable
+    ref2 = clone_params(ours)
+    t2 = torch.optim.AdamW(ref2, lr=6e-4, weight_decay=0.1, foreach=False, capturable=True)
+    t2.load_state_dict(copy.deepcopy(oopt.state_dict()))
+    for step in range(4, 7):
+        set_grads(ref, step, 1e-3)
+        for group in (ours, ours2, ref2):
+            _copy_grads(ref, group)
+        for o in (topt, oopt, o2, t2):
+            o.step()
+    _same(ref, ours, topt, oopt)
+    _same(ref, ours2, topt, o2)
+    _same(ref, ref2, topt, t2)
+    # a non-capturable checkpoint (host steps) into a capturable FusedAdamW
+    tn = torch.optim.AdamW(clone_params(ref), lr=6e-4, weight_decay=0.1, foreach=False)
+    sd = copy.deepcopy(topt.state_dict())
+    for st in sd["state"].values():
+        st["step"] = st["step"].cpu()
+    tn.load_state_dict(sd)
+    ours3 = clone_params(ref)
+    o3 = mi_adamw.FusedAdamW(ours3, lr=6e-4, weight_decay=0.1, foreach=False, capturable=True)
+    o3.load_state_dict(copy.deepcopy(tn.state_dict()))
+    assert all(o3.state[q]["step"].device == dev for q in ours3)
+    set_grads(ref, 7, 1e-3)
+    _copy_grads(ref, ours3)
+    topt.step()
+    o3.step()
+    _same(ref, ours3, topt, o3)
+
+
+def test_graph_capture_replays_match_eager(dev):
+    """step() (clip, bf16 copy) recorded once into a HIP graph after eager warm-up
+    steps, then replayed with new gradients in the same tensors: every replay is
+    bit-identical to torch's eager capturable step, with other eager work and
+    synchronisation between replays."""
+    ref, ours, topt, oopt = _pair(dev, weight_decay=0.1,
+                                  opt_kw=dict(max_grad_norm=1.0, bf16_copy=True))
+    for p in ref + ours:
+        p.grad = torch.zeros_like(p)
+
+    def fill(step):
+        set_grads(ref, step, 1e-2)
+        for p, q in zip(ref, ours):
+            q.grad.copy_(p.grad)
+
+    def torch_step():
+        torch.nn.utils.clip_grads_with_norm_(ref, 1.0, oopt.last_grad_norm.clone())
+        topt.step()
+
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for step in range(1, 4):
+            fill(step)
+            oopt.step()
+            torch_step()
+    torch.cuda.current_stream().wait_stream(side)
+    _same(ref, ours, topt, oopt)
+
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        oopt.step()
+    captured_norm = oopt.last_grad_norm
+    for step in range(4, 10):
+        fill(step)
+        graph.replay()
+        assert oopt.last_grad_norm is captured_norm
+        torch_step()
+        _same(ref, ours, topt, oopt)
+        for q in ours:
+            assert torch.equal(oopt.bf16_param(q), q.detach().to(torch.bfloat16))
+        # unrelated eager work between replays
+        torch.randn(1 << 20, device=dev).sum().item()
+    assert float(oopt.state[ours[0]]["step"]) == 9.0
+
+
+def test_capture_refuses_moved_gradients(dev):
+    """A step under capture must find the tables of an earlier eager step: with a
+    gradient moved to a new tensor it raises instead of recording an upload."""
+    ref, ours, topt, oopt = _pair(dev)
+    set_grads(ours, 1, 1e-3)
+    oopt.step()
+    torch.cuda.synchronize()
+    ours[0].grad = ours[0].grad.clone()
+    graph = torch.cuda.CUDAGraph()
+    with pytest.raises(RuntimeError, match="under graph capture"):
+        with torch.cuda.graph(graph):
+            oopt.step()
+    torch.cuda.synchronize()
+    oopt.step()          # eager again: the rows are refreshed and the step runs
+    torch.cuda.synchronize()
+    assert float(oopt.state[ours[0]]["step"]) == 2.0

@@ -54,11 +54,42 @@ def test_invalid_arguments_raise_like_torch(kwargs):
     assert str(ours.value) == str(ref.value)
 
 
-@pytest.mark.parametrize("kwargs", [dict(capturable=True), dict(differentiable=True),
+@pytest.mark.parametrize("kwargs", [dict(differentiable=True),
                                     dict(betas=(torch.tensor(0.9), torch.tensor(0.999)))])
 def test_unsupported_flags_fail_loudly(kwargs):
     with pytest.raises(NotImplementedError):
         mi_adamw.FusedAdamW(_params(), **kwargs)
+
+
+def test_capturable_groups_must_agree():
+    opt = mi_adamw.FusedAdamW(_params(), capturable=True)
+    assert opt.capturable and opt.param_groups[0]["capturable"] is True
+    with pytest.raises(NotImplementedError, match="capturable"):
+        opt.add_param_group({"params": _params(), "capturable": False})
+    with pytest.raises(NotImplementedError, match="capturable"):
+        mi_adamw.FusedAdamW([{"params": _params()}, {"params": _params(), "capturable": True}])
+    assert len(opt.param_groups) == 1
+
+
+def test_capturable_group_constants():
+    """The capturable chain's per-group constants: betas, 1-beta1, 1-beta2 and eps
+    rounded to fp32; a float lr with its host weight-decay factor; a CPU tensor lr by
+    value; a device lr by pointer (not built without a GPU)."""
+    from mi_adamw.optimizer import _capt_hyper
+    f32 = np.float32
+    g = dict(lr=6e-4, betas=(0.9, 0.999), eps=1e-8, weight_decay=0.1, maximize=True)
+    h = _capt_hyper(g, torch.device("cpu"))
+    assert (h.beta1, h.beta2) == (float(f32(0.9)), float(f32(0.999)))
+    assert h.lerp_w == float(f32(1 - 0.9)) and h.one_minus_beta2 == float(f32(1 - 0.999))
+    assert h.eps == float(f32(1e-8)) and h.grad_sign == -1.0
+    assert h.lr_mode == _lib.LR_FLOAT and h.lr == float(f32(6e-4))
+    assert h.wd_factor == float(f32(1 - 6e-4 * 0.1))
+    h = _capt_hyper(dict(g, lr=torch.tensor(6e-4), weight_decay=0.0), torch.device("cpu"))
+    assert h.lr_mode == _lib.LR_VALUE and h.lr == float(f32(6e-4)) and h.wd_factor == 1.0
+    h = _capt_hyper(dict(g, lr=torch.tensor(6e-4)), torch.device("cpu"))
+    assert h.wd_factor == float((1 - torch.tensor(6e-4) * 0.1).item())
+    with pytest.raises(NotImplementedError, match="float32"):
+        _capt_hyper(dict(g, lr=torch.tensor(6e-4, dtype=torch.float64)), torch.device("cpu"))
 
 
 def test_extra_options_are_validated():
@@ -194,6 +225,11 @@ def test_header_structs_match_bindings():
     fields = re.findall(r"\*?\s*(\w+);", body)
     assert fields == [f for f, _ in _lib.TensorRow._fields_]
     assert f"#define MI_ADAMW_F_AMSGRAD (1 << 3)" in text and _lib.F_AMSGRAD == 1 << 3
+    body = text[text.index("typedef struct mi_adamw_capt_hyper {"):
+                text.index("} mi_adamw_capt_hyper;")]
+    assert re.findall(r"\*?\s*(\w+);", body) == [f for f, _ in _lib.CaptHyper._fields_]
+    for name in ("LR_FLOAT", "LR_VALUE", "LR_DEVICE"):
+        assert f"#define MI_ADAMW_{name} {getattr(_lib, name)}" in text
 
 
 def test_table_rows_are_built_field_by_field_on_cpu():
