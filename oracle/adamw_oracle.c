@@ -17,6 +17,12 @@
  *       (amsgrad, adam.py:538-543: vmax = maximum(vmax, v), NaN-propagating,
  *        and d is computed from vmax instead of v)
  *       adam.py:547  p  = p + f32(-step_size) * (m / d)              (addcdiv_)
+ *   - torch/optim/adam.py:480-527  the same loop with capturable=True: the step
+ *     counts are device tensors and the per-step values are 0-d fp32 tensor ops,
+ *       adam.py:488,497  bc1 = 1 - beta1**step, bc2 = 1 - beta2**step
+ *       adam.py:499-502  step_size = lr / bc1, neg = -step_size, bc2_sqrt = sqrt(bc2)
+ *       adam.py:520-522  d = sqrt(v) / (bc2_sqrt * neg) + eps / neg
+ *       adam.py:527      p = p + m / d                                  (addcdiv_)
  *   - torch/include/ATen/native/Lerp.h:21-35  the two-branch lerp formula.
  *   - torch/nn/utils/clip_grad.py:50-117,121-183  global L2 norm, then
  *     coef = clamp(max_norm * reciprocal(norm + 1e-6), max=1), g *= coef.
@@ -85,21 +91,34 @@ static inline float maximum_nan(float a, float b)
     return a < b ? b : a;
 }
 
-/* One element of the op chain above.  p, m, v (and vmax with amsgrad, when
- * non-NULL) are updated in place. */
+/* The ops both chains share (adam.py:419-476, amsgrad's maximum at :538-540 or,
+ * capturable, :510-512): p, m, v (and vmax with amsgrad, when non-NULL) updated
+ * in place.  Returns the value whose square root the denominator takes. */
+static inline float shared_ops(float *p, float g, float *m, float *v, float *vmax,
+                               float wd_factor, float lerp_w, float beta2, float omb2,
+                               const oracle_opmodel *om)
+{
+    float pp = *p * wd_factor;                              /* adam.py:419 */
+    float mm = lerp_f32(*m, g, lerp_w, om->lerp_fma);       /* adam.py:457 */
+    float vv = *v * beta2;                                  /* adam.py:476 */
+    vv = addcmul_f32(vv, omb2, g, om->addcmul_mode);
+    float dv = vv;
+    if (vmax) {
+        *vmax = maximum_nan(*vmax, vv);
+        dv = *vmax;
+    }
+    *p = pp; *m = mm; *v = vv;
+    return dv;
+}
+
+/* One element of the default chain. */
 static inline void adamw_elem(float *p, float g, float *m, float *v, float *vmax,
                               const oracle_hyper *h, const oracle_opmodel *om,
                               float inv_bc2, float bc2f)
 {
-    float pp = *p * h->wd_factor;                           /* adam.py:419 */
-    float mm = lerp_f32(*m, g, h->lerp_w, om->lerp_fma);    /* adam.py:457 */
-    float vv = *v * h->beta2;                               /* adam.py:476 */
-    vv = addcmul_f32(vv, h->one_minus_beta2, g, om->addcmul_mode);
-    float dv = vv;
-    if (vmax) {                                             /* adam.py:538-540 */
-        *vmax = maximum_nan(*vmax, vv);
-        dv = *vmax;
-    }
+    float dv = shared_ops(p, g, m, v, vmax, h->wd_factor, h->lerp_w, h->beta2,
+                          h->one_minus_beta2, om);
+    float pp = *p, mm = *m;
     float d = sqrtf(dv);                                    /* adam.py:543,545 */
     d = om->div_recip ? d * inv_bc2 : d / bc2f;
     d = d + h->eps;
@@ -111,7 +130,7 @@ static inline void adamw_elem(float *p, float g, float *m, float *v, float *vmax
         float q = mm / d;
         pp = om->addcdiv_mode == 1 ? fmaf(h->neg_step_size, q, pp) : pp + h->neg_step_size * q;
     }
-    *p = pp; *m = mm; *v = vv;
+    *p = pp;
 }
 
 /* fp32 state: p, g, m, v (and vmax, or NULL without amsgrad) are n contiguous
@@ -147,6 +166,65 @@ void oracle_adamw_bf16state(float *p, const float *g, uint16_t *m, uint16_t *v,
         float vv = oracle_bf16_to_f32(v[i]);
         float mx = vmax ? oracle_bf16_to_f32(vmax[i]) : 0.0f;
         adamw_elem(&p[i], gi, &mm, &vv, vmax ? &mx : NULL, h, om, inv_bc2, bc2f);
+        m[i] = oracle_f32_to_bf16(mm);
+        v[i] = oracle_f32_to_bf16(vv);
+        if (vmax) vmax[i] = oracle_f32_to_bf16(mx);
+    }
+}
+
+/* adam.py:480-502 in fp32, one rounding per 0-d tensor op.  A float lr reaches
+ * `lr / bc1` as bc1.reciprocal() * lr (Tensor.__rtruediv__); a tensor lr as a
+ * true division.  eps / neg is likewise reciprocal(neg) * eps.  powf is this C
+ * library's; torch's device pow may differ from it in the last bit for some
+ * steps, so bit-level comparisons with the GPU pass torch's own values. */
+void oracle_capt_scalars(float beta1, float beta2, float lr, float eps, float step,
+                         int lr_is_tensor, float *den_scale, float *den_add)
+{
+    float bc1 = 1.0f - powf(beta1, step);
+    float bc2 = 1.0f - powf(beta2, step);
+    float step_size = lr_is_tensor ? lr / bc1 : (1.0f / bc1) * lr;
+    float neg = -step_size;
+    float bc2_sqrt = sqrtf(bc2);
+    *den_scale = bc2_sqrt * neg;
+    *den_add = (1.0f / neg) * eps;
+}
+
+/* One element of the capturable chain (adam.py:419-527, capturable=True). */
+static inline void adamw_capt_elem(float *p, float g, float *m, float *v, float *vmax,
+                                   const oracle_capt *h, const oracle_opmodel *om)
+{
+    float dv = shared_ops(p, g, m, v, vmax, h->wd_factor, h->lerp_w, h->beta2,
+                          h->one_minus_beta2, om);
+    float d = sqrtf(dv);                                    /* adam.py:516-522 */
+    d = d / h->den_scale;
+    d = d + h->den_add;
+    *p = *p + *m / d;                                       /* adam.py:527, value 1 */
+}
+
+void oracle_adamw_capt_f32(float *p, const float *g, float *m, float *v, float *vmax,
+                           int64_t n, const oracle_capt *h, const oracle_opmodel *om,
+                           float grad_scale, int apply_scale)
+{
+    for (int64_t i = 0; i < n; ++i) {
+        float gi = g[i];
+        if (apply_scale) gi = gi * grad_scale;
+        gi = gi * h->grad_sign;
+        adamw_capt_elem(&p[i], gi, &m[i], &v[i], vmax ? &vmax[i] : NULL, h, om);
+    }
+}
+
+void oracle_adamw_capt_bf16state(float *p, const float *g, uint16_t *m, uint16_t *v,
+                                 uint16_t *vmax, int64_t n, const oracle_capt *h,
+                                 const oracle_opmodel *om, float grad_scale, int apply_scale)
+{
+    for (int64_t i = 0; i < n; ++i) {
+        float gi = g[i];
+        if (apply_scale) gi = gi * grad_scale;
+        gi = gi * h->grad_sign;
+        float mm = oracle_bf16_to_f32(m[i]);
+        float vv = oracle_bf16_to_f32(v[i]);
+        float mx = vmax ? oracle_bf16_to_f32(vmax[i]) : 0.0f;
+        adamw_capt_elem(&p[i], gi, &mm, &vv, vmax ? &mx : NULL, h, om);
         m[i] = oracle_f32_to_bf16(mm);
         v[i] = oracle_f32_to_bf16(vv);
         if (vmax) vmax[i] = oracle_f32_to_bf16(mx);

@@ -39,6 +39,19 @@ typedef struct oracle_hyper {
     float grad_sign;       /* -1.0f when maximize (adam.py:397), else 1.0f                  */
 } oracle_hyper;
 
+/* Scalars of the capturable chain (adam.py:480-527, capturable=True): the
+ * first four and grad_sign as in oracle_hyper; the two per-step values are
+ * fp32 results of 0-d tensor ops (oracle_capt_scalars, or torch's own). */
+typedef struct oracle_capt {
+    float wd_factor;
+    float lerp_w;
+    float beta2;
+    float one_minus_beta2;
+    float den_scale;       /* sqrt(bc2) * -step_size                (adam.py:521)          */
+    float den_add;         /* eps / -step_size                      (adam.py:522)          */
+    float grad_sign;
+} oracle_capt;
+
 uint16_t oracle_f32_to_bf16(float x);
 float oracle_bf16_to_f32(uint16_t h);
 
@@ -52,6 +65,18 @@ void oracle_adamw_f32(float *p, const float *g, float *m, float *v, float *vmax,
 void oracle_adamw_bf16state(float *p, const float *g, uint16_t *m, uint16_t *v,
                             uint16_t *vmax, int64_t n, const oracle_hyper *h,
                             const oracle_opmodel *om, float grad_scale, int apply_scale);
+
+/* adam.py:480-502: den_scale and den_add of step `step` in fp32 (libm powf). */
+void oracle_capt_scalars(float beta1, float beta2, float lr, float eps, float step,
+                         int lr_is_tensor, float *den_scale, float *den_add);
+
+/* The capturable chain: d = sqrt(v) / den_scale + den_add, p = p + m / d. */
+void oracle_adamw_capt_f32(float *p, const float *g, float *m, float *v, float *vmax,
+                           int64_t n, const oracle_capt *h, const oracle_opmodel *om,
+                           float grad_scale, int apply_scale);
+void oracle_adamw_capt_bf16state(float *p, const float *g, uint16_t *m, uint16_t *v,
+                                 uint16_t *vmax, int64_t n, const oracle_capt *h,
+                                 const oracle_opmodel *om, float grad_scale, int apply_scale);
 
 void oracle_to_bf16(const float *x, uint16_t *out, int64_t n);
 

@@ -13,6 +13,10 @@ It restates, in NumPy plus the C kernels of ``adamw_oracle.c``:
   ``_single_tensor_adam`` (``adam.py:419,457,476,545,547``; with amsgrad
   ``:539-543``) and ``ATen/native/Lerp.h:21-35``, one fp32 rounding per ATen
   kernel.
+* ``capt_scalars`` / ``adamw_step_capt`` / ``adamw_step_capt_bf16state`` -- the
+  same loop with ``capturable=True`` (``adam.py:480-527``): the per-step values
+  as fp32 0-d tensor ops, then ``p + m / (sqrt(v) / (sqrt(bc2) * -step_size) +
+  eps / -step_size)``.
 * ``total_norm`` / ``clip_coef`` -- ``torch/nn/utils/clip_grad.py:50-117``
   (global L2 norm over all gradients) and ``:165-169`` (the clamped
   coefficient), the clip mini-megatron defines at ``config.py:16``
@@ -30,6 +34,11 @@ How each function is pinned (none of it is trusted on its own):
 * The clip norm: fixtures from ``clip_grad_norm_`` (rel 1e-6), the closed form
   ``|c| sqrt(N)`` for constant gradients, and an exact float64 brute force on
   tiny inputs.
+* The capturable chain: torch does not run it on the CPU, so it is pinned
+  bit-for-bit against ``torch.optim.AdamW(capturable=True, foreach=False)`` on
+  the MI355X (a GPU test, with torch's own per-step values), and on the CPU by
+  closed forms (step 1: ``bc1 = 1 - beta1``; lr 0 leaves p unchanged) and the
+  mutation tests.
 * The bf16 paths: a brute-force round-to-nearest-even check of
   ``oracle_f32_to_bf16`` over every rounding boundary class, and torch's own
   ``Tensor.to(torch.bfloat16)`` on the same values.
@@ -92,6 +101,20 @@ OPMODEL_TORCH_CPU = OpModel(lerp_fma=1, addcmul_mode=2, addcdiv_mode=2, div_reci
 OPMODEL_TORCH_ROCM = OpModel(lerp_fma=1, addcmul_mode=1, addcdiv_mode=1, div_recip=1)
 
 
+class Capt(ctypes.Structure):
+    """oracle_capt: the capturable chain's scalars (adamw_oracle.h)."""
+
+    _fields_ = [
+        ("wd_factor", ctypes.c_float),
+        ("lerp_w", ctypes.c_float),
+        ("beta2", ctypes.c_float),
+        ("one_minus_beta2", ctypes.c_float),
+        ("den_scale", ctypes.c_float),
+        ("den_add", ctypes.c_float),
+        ("grad_sign", ctypes.c_float),
+    ]
+
+
 def _load(path: str = _LIB_PATH):
     if not os.path.exists(path):
         raise RuntimeError(f"oracle library missing: build it with `make -C {_HERE}`")
@@ -106,6 +129,16 @@ def _load(path: str = _LIB_PATH):
                                            ctypes.POINTER(Hyper), ctypes.POINTER(OpModel),
                                            ctypes.c_float, ctypes.c_int]
     lib.oracle_adamw_bf16state.restype = None
+    lib.oracle_capt_scalars.argtypes = [ctypes.c_float] * 5 + [ctypes.c_int, f32p, f32p]
+    lib.oracle_capt_scalars.restype = None
+    lib.oracle_adamw_capt_f32.argtypes = [f32p, f32p, f32p, f32p, f32p, i64,
+                                          ctypes.POINTER(Capt), ctypes.POINTER(OpModel),
+                                          ctypes.c_float, ctypes.c_int]
+    lib.oracle_adamw_capt_f32.restype = None
+    lib.oracle_adamw_capt_bf16state.argtypes = [f32p, f32p, u16p, u16p, u16p, i64,
+                                                ctypes.POINTER(Capt), ctypes.POINTER(OpModel),
+                                                ctypes.c_float, ctypes.c_int]
+    lib.oracle_adamw_capt_bf16state.restype = None
     lib.oracle_to_bf16.argtypes = [f32p, u16p, i64]
     lib.oracle_to_bf16.restype = None
     lib.oracle_sumsq_f64.argtypes = [f32p, i64]
@@ -214,6 +247,65 @@ def adamw_step_bf16state(p, g, m_bits, v_bits, *, lr, betas, eps, weight_decay, 
                                  None if vmax_bits is None else _u16(vmax_bits), n,
                                  ctypes.byref(h), ctypes.byref(opmodel), scale,
                                  0 if grad_scale is None else 1)
+
+
+def capt_scalars(lr, beta1, beta2, eps, step, lr_is_tensor=False) -> tuple[float, float]:
+    """(den_scale, den_add) of the capturable chain at step ``step`` (adam.py:480-522),
+    fp32 with this C library's powf."""
+    a, e = ctypes.c_float(), ctypes.c_float()
+    lib().oracle_capt_scalars(float(np.float32(beta1)), float(np.float32(beta2)),
+                              float(np.float32(lr)), float(np.float32(eps)),
+                              float(np.float32(step)), 1 if lr_is_tensor else 0,
+                              ctypes.byref(a), ctypes.byref(e))
+    return a.value, e.value
+
+
+def capt_from_group(lr, beta1, beta2, eps, weight_decay, step, maximize=False,
+                    lr_is_tensor=False, den=None) -> Capt:
+    """The capturable chain's scalars.  ``den``: (den_scale, den_add) formed
+    elsewhere (torch's device values); otherwise ``capt_scalars``.  The
+    weight-decay factor is Python float64 for a float lr and two fp32 tensor ops
+    (``1 - lr * wd``) for a tensor lr."""
+    f32 = np.float32
+    if weight_decay == 0:
+        wd_factor = f32(1.0)
+    elif lr_is_tensor:
+        wd_factor = f32(1) - f32(lr) * f32(weight_decay)
+    else:
+        wd_factor = f32(1 - lr * weight_decay)
+    a, e = den if den is not None else capt_scalars(lr, beta1, beta2, eps, step, lr_is_tensor)
+    return Capt(wd_factor=float(wd_factor), lerp_w=float(f32(1 - beta1)),
+                beta2=float(f32(beta2)), one_minus_beta2=float(f32(1 - beta2)),
+                den_scale=float(a), den_add=float(e), grad_sign=-1.0 if maximize else 1.0)
+
+
+def adamw_step_capt(p, g, m, v, *, lr, betas, eps, weight_decay, step, maximize=False,
+                    grad_scale=None, vmax=None, lr_is_tensor=False, den=None,
+                    opmodel=OPMODEL_TORCH_ROCM) -> None:
+    """One capturable-chain AdamW step on fp32 numpy arrays, in place."""
+    h = capt_from_group(lr, betas[0], betas[1], eps, weight_decay, step, maximize,
+                        lr_is_tensor, den)
+    n = p.size
+    if not (g.size == m.size == v.size == n) or (vmax is not None and vmax.size != n):
+        raise ValueError("p, g, m, v sizes differ")
+    scale = 1.0 if grad_scale is None else float(np.float32(grad_scale))
+    lib().oracle_adamw_capt_f32(_f32(p), _f32(g), _f32(m), _f32(v),
+                                None if vmax is None else _f32(vmax), n, ctypes.byref(h),
+                                ctypes.byref(opmodel), scale, 0 if grad_scale is None else 1)
+
+
+def adamw_step_capt_bf16state(p, g, m_bits, v_bits, *, lr, betas, eps, weight_decay, step,
+                              maximize=False, grad_scale=None, vmax_bits=None,
+                              lr_is_tensor=False, den=None, opmodel=OPMODEL_TORCH_ROCM) -> None:
+    """Capturable-chain step with bf16-stored moments (uint16 bit arrays), fp32 math."""
+    h = capt_from_group(lr, betas[0], betas[1], eps, weight_decay, step, maximize,
+                        lr_is_tensor, den)
+    n = p.size
+    scale = 1.0 if grad_scale is None else float(np.float32(grad_scale))
+    lib().oracle_adamw_capt_bf16state(_f32(p), _f32(g), _u16(m_bits), _u16(v_bits),
+                                      None if vmax_bits is None else _u16(vmax_bits), n,
+                                      ctypes.byref(h), ctypes.byref(opmodel), scale,
+                                      0 if grad_scale is None else 1)
 
 
 def to_bf16_bits(x: np.ndarray) -> np.ndarray:

@@ -13,6 +13,7 @@ from __future__ import annotations
 
 import copy
 
+import numpy as np
 import pytest
 import torch
 
@@ -234,3 +235,86 @@ def test_capture_refuses_moved_gradients(dev):
     oopt.step()          # eager again: the rows are refreshed and the step runs
     torch.cuda.synchronize()
     assert float(oopt.state[ours[0]]["step"]) == 2.0
+
+
+def _torch_den(b1, b2, lr, eps, step, dev, lr_tensor=False):
+    """torch's own per-step values of the capturable chain (adam.py:480-522), run as
+    the same 0-d tensor ops on the GPU: (sqrt(bc2) * -step_size, eps / -step_size)."""
+    step_t = torch.tensor(float(step), device=dev)
+    bc1 = 1 - b1 ** step_t
+    bc2 = 1 - b2 ** step_t
+    lr_v = torch.tensor(lr, device=dev) if lr_tensor else lr
+    step_size = lr_v / bc1
+    neg = step_size.neg()
+    return float(bc2.sqrt() * neg), float(eps / neg)
+
+
+@pytest.mark.parametrize("amsgrad", [False, True])
+def test_oracle_capturable_chain_matches_torch_on_the_gpu(dev, amsgrad):
+    """Pins the oracle's capturable chain: with torch's per-step values, its
+    ROCm op model reproduces torch.optim.AdamW(capturable=True, foreach=False)
+    on the MI355X bit for bit, mid-training, over several steps."""
+    from oracle import oracle as O
+    n = 70001
+    gen_ = torch.Generator(device=dev).manual_seed(5)
+    p = torch.nn.Parameter(torch.randn(n, device=dev, generator=gen_) * 0.02)
+    t = torch.optim.AdamW([p], lr=6e-4, betas=(0.9, 0.999), weight_decay=0.1, foreach=False,
+                          capturable=True, amsgrad=amsgrad)
+    pn = p.detach().cpu().numpy().copy()
+    mn, vn = np.zeros(n, np.float32), np.zeros(n, np.float32)
+    xn = np.zeros(n, np.float32) if amsgrad else None
+    for step in range(1, 6):
+        p.grad = torch.randn(n, device=dev, generator=gen_) * 1e-3
+        gn = p.grad.cpu().numpy().copy()
+        t.step()
+        O.adamw_step_capt(pn, gn, mn, vn, lr=6e-4, betas=(0.9, 0.999), eps=1e-8,
+                          weight_decay=0.1, step=step, vmax=xn,
+                          den=_torch_den(0.9, 0.999, 6e-4, 1e-8, step, dev))
+        st = t.state[p]
+        assert O.max_ulp(pn, p.detach().cpu().numpy())[0] == 0
+        assert np.array_equal(mn, st["exp_avg"].cpu().numpy())
+        assert np.array_equal(vn, st["exp_avg_sq"].cpu().numpy())
+        if amsgrad:
+            assert np.array_equal(xn, st["max_exp_avg_sq"].cpu().numpy())
+
+
+@pytest.mark.parametrize("amsgrad,clip", [(False, True), (True, False)])
+def test_capturable_bf16_state_matches_oracle(dev, amsgrad, clip):
+    """bf16 moments in the capturable chain (torch has no such mode): the kernel
+    against the oracle's capturable bf16-state step, bit for bit, with torch's
+    per-step values, over several steps from a mid-training state."""
+    import mi_adamw
+    from oracle import oracle as O
+    shapes = [(4099,), (64, 48), (70001,)]
+    ps = make_params(shapes, dev)
+    opt = mi_adamw.FusedAdamW(ps, lr=3e-4, betas=(0.9, 0.95), weight_decay=0.1, capturable=True,
+                              state_dtype=torch.bfloat16, amsgrad=amsgrad,
+                              max_grad_norm=1.0 if clip else None)
+    gen_ = torch.Generator(device=dev).manual_seed(9)
+    host = []
+    for q in ps:
+        m0 = (torch.randn(q.numel(), device=dev, generator=gen_) * 1e-3).bfloat16()
+        v0 = (torch.randn(q.numel(), device=dev, generator=gen_) * 1e-6).abs().bfloat16()
+        x0 = (v0.float() * 1.5).bfloat16() if amsgrad else None
+        opt.set_state(q, 40.0, m0.view(q.shape), v0.view(q.shape),
+                      None if x0 is None else x0.view(q.shape))
+        host.append([q.detach().cpu().numpy().reshape(-1).copy(),
+                     m0.view(torch.int16).cpu().numpy().view(np.uint16).copy(),
+                     v0.view(torch.int16).cpu().numpy().view(np.uint16).copy(),
+                     None if x0 is None else x0.view(torch.int16).cpu().numpy().view(np.uint16).copy()])
+    for step in range(41, 45):
+        set_grads(ps, step, 1e-2)
+        opt.step()
+        coef = O.clip_coef(np.float32(opt.last_grad_norm.item()), 1.0) if clip else None
+        den = _torch_den(0.9, 0.95, 3e-4, 1e-8, step, dev)
+        for q, (pn, mb, vb, xb) in zip(ps, host):
+            O.adamw_step_capt_bf16state(pn, q.grad.detach().cpu().numpy().reshape(-1).copy(),
+                                        mb, vb, lr=3e-4, betas=(0.9, 0.95), eps=1e-8,
+                                        weight_decay=0.1, step=step, grad_scale=coef,
+                                        vmax_bits=xb, den=den)
+            st = opt.state[q]
+            assert O.max_ulp(pn, q.detach().cpu().numpy().reshape(-1))[0] == 0
+            assert np.array_equal(mb, st["exp_avg"].view(torch.int16).cpu().numpy().view(np.uint16).reshape(-1))
+            assert np.array_equal(vb, st["exp_avg_sq"].view(torch.int16).cpu().numpy().view(np.uint16).reshape(-1))
+            if amsgrad:
+                assert np.array_equal(xb, st["max_exp_avg_sq"].view(torch.int16).cpu().numpy().view(np.uint16).reshape(-1))

@@ -223,6 +223,82 @@ def test_float64_bound(opmodel, step, b1, b2):
     assert np.all(np.abs(p - p64) <= bound)
 
 
+def test_capt_lr_zero_leaves_params_unchanged():
+    """Capturable chain, lr 0: step_size is 0, both denominator terms are -inf and
+    the update m / d is a signed zero."""
+    p0 = _rand(4096, 21, 0.02)
+    p = p0.copy()
+    g = _rand(4096, 22, 1e-3)
+    m, v = np.zeros_like(p), np.zeros_like(p)
+    O.adamw_step_capt(p, g, m, v, lr=0.0, betas=(0.9, 0.999), eps=1e-8, weight_decay=0.1,
+                      step=1)
+    assert np.array_equal(p.view(np.uint32), p0.view(np.uint32))
+    assert np.array_equal(m, (np.float32(0.1) * g).astype(np.float32))
+
+
+@pytest.mark.parametrize("lr_is_tensor", [False, True])
+def test_capt_first_step_closed_form(lr_is_tensor):
+    """Capturable chain, step 1 from zero state: powf(beta, 1) is beta, and
+    m / (sqrt(v) / (sqrt(bc2) * -step_size) + eps / -step_size) is
+    -lr g / (|g| + eps), the same first step as the default chain."""
+    n = 8192
+    p0 = _rand(n, 23, 0.02)
+    g = _rand(n, 24, 1e-3)
+    p, m, v = p0.copy(), np.zeros(n, np.float32), np.zeros(n, np.float32)
+    lr, wd = 3e-4, 0.1
+    O.adamw_step_capt(p, g, m, v, lr=lr, betas=(0.9, 0.95), eps=1e-8, weight_decay=wd, step=1,
+                      lr_is_tensor=lr_is_tensor)
+    assert np.array_equal(m, (np.float32(1 - 0.9) * g).astype(np.float32))
+    g64 = g.astype(np.float64)
+    expect = p0.astype(np.float64) * (1 - lr * wd) - lr * g64 / (np.abs(g64) + 1e-8)
+    # about eight fp32 roundings reach the update (the two per-step values, sqrt,
+    # two divisions, the add, the final add): 2^-21 of lr, plus p's own rounding
+    assert np.all(np.abs(p - expect) <= 2.0 ** -21 * (np.abs(expect) + lr))
+    a, e = O.capt_scalars(lr, 0.9, 0.95, 1e-8, 1.0, lr_is_tensor)
+    assert abs(a - (-np.sqrt(0.05) * lr / 0.1)) <= 4 * 2.0 ** -24 * abs(a)
+    assert abs(e - (-1e-8 * 0.1 / lr)) <= 4 * 2.0 ** -24 * abs(e)
+
+
+@pytest.mark.parametrize("step,b1,b2,lr_is_tensor,amsgrad", [
+    (1, 0.9, 0.95, False, False), (7, 0.9, 0.999, False, True), (1000, 0.9, 0.95, True, False),
+    (3, 0.3, 0.95, False, False), (250, 0.8, 0.99, True, True)])
+def test_capt_agrees_with_the_default_chain(step, b1, b2, lr_is_tensor, amsgrad):
+    """The capturable and the default chain on the same inputs: m, v (and amsgrad's
+    maximum) bit-identical, being the same ATen ops; the update u = p - p*(1-lr*wd)
+    within the error analysis of the two ways of forming it.  The default chain's
+    bias corrections are float64; the capturable chain's are fp32, and
+    bc = 1 - beta**step cancels: one ulp of beta**step is a relative error of
+    2^-23 * beta**step / bc in bc, which reaches u whole through bc1 and halved
+    through sqrt(bc2).  Add 16 roundings for the ops of both chains.  The
+    default chain is pinned by torch's golden vectors, so a dropped term, a sign
+    or a swapped operand in the capturable one shows here."""
+    n = 4096
+    p0, g = _rand(n, 25, 0.02), _rand(n, 26, 1e-3)
+    m0, v0 = _rand(n, 27, 1e-3), np.abs(_rand(n, 28, 1e-6))
+    x0 = v0 * np.float32(1.5)
+    lr, wd, eps = 6e-4, 0.1, 1e-8
+    out = []
+    for capt in (False, True):
+        p, m, v = p0.copy(), m0.copy(), v0.copy()
+        x = x0.copy() if amsgrad else None
+        kw = dict(lr=lr, betas=(b1, b2), eps=eps, weight_decay=wd, step=step, vmax=x)
+        if capt:
+            O.adamw_step_capt(p, g.copy(), m, v, lr_is_tensor=lr_is_tensor, **kw)
+        else:
+            O.adamw_step(p, g.copy(), m, v, **kw)
+        out.append((p, m, v, x))
+    (pa, ma, va, xa), (pb, mb, vb, xb) = out
+    assert np.array_equal(ma, mb) and np.array_equal(va, vb)
+    if amsgrad:
+        assert np.array_equal(xa, xb)
+    pd = np.float32(p0 * np.float32(1 - lr * wd)).astype(np.float64)   # decayed p, both chains
+    ua, ub = pa - pd, pb - pd
+    bc1, bc2 = 1 - b1 ** step, 1 - b2 ** step
+    rel = 2.0 ** -24 * (16 + 2 * b1 ** step / bc1 + b2 ** step / bc2)
+    # each chain's final rounding of p adds up to half an ulp of p
+    assert np.all(np.abs(ua - ub) <= rel * np.abs(ua) + 2.0 ** -24 * (np.abs(pa) + np.abs(pb)))
+
+
 def test_clip_closed_forms():
     # Constant gradients: norm = |c| sqrt(N), exactly representable here.
     grads = [np.full(1024, 0.5, np.float32), np.full(3072, 0.5, np.float32)]

@@ -5,8 +5,9 @@ Each case compiles a copy of oracle/adamw_oracle.c with one plausible mistake
 clamp, truncation instead of rounding, an off-by-one), points the oracle's
 wrappers at it, and runs the pinning checks of tests/test_oracle.py: golden
 fixtures from torch, closed forms, the float64 bound, bf16 rounding against
-torch.  At least one check must fail for every mutant; the unmodified source
-compiled the same way must pass them all.
+torch, and the capturable chain's closed forms and its agreement with the
+default chain.  At least one check must fail for every mutant; the unmodified
+source compiled the same way must pass them all.
 """
 from __future__ import annotations
 
@@ -23,17 +24,17 @@ ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 SOURCE = os.path.join(ROOT, "oracle", "adamw_oracle.c")
 
 MUTANTS = {
-    "no_weight_decay": ("float pp = *p * h->wd_factor;", "float pp = *p;"),
-    "lerp_weight_beta1": ("lerp_f32(*m, g, h->lerp_w, om->lerp_fma)",
-                          "lerp_f32(*m, g, 1.0f - h->lerp_w, om->lerp_fma)"),
+    "no_weight_decay": ("float pp = *p * wd_factor;", "float pp = *p;"),
+    "lerp_weight_beta1": ("lerp_f32(*m, g, lerp_w, om->lerp_fma)",
+                          "lerp_f32(*m, g, 1.0f - lerp_w, om->lerp_fma)"),
     "update_sign": ("pp = om->addcdiv_mode == 1 ? fmaf(h->neg_step_size, q, pp) : pp + h->neg_step_size * q;",
                     "pp = om->addcdiv_mode == 1 ? fmaf(-h->neg_step_size, q, pp) : pp - h->neg_step_size * q;"),
     "no_bias_correction2": ("d = om->div_recip ? d * inv_bc2 : d / bc2f;", "d = d;"),
     "no_eps": ("d = d + h->eps;", "d = d;"),
-    "m_v_swapped": ("float q = mm / d;", "float q = vv / d;"),
-    "g_not_squared": ("vv = addcmul_f32(vv, h->one_minus_beta2, g, om->addcmul_mode);",
-                      "vv = vv + h->one_minus_beta2 * fabsf(g);"),
-    "beta2_swapped": ("float vv = *v * h->beta2;", "float vv = *v * h->one_minus_beta2;"),
+    "m_v_swapped": ("float q = mm / d;", "float q = *v / d;"),
+    "g_not_squared": ("vv = addcmul_f32(vv, omb2, g, om->addcmul_mode);",
+                      "vv = vv + omb2 * fabsf(g);"),
+    "beta2_swapped": ("float vv = *v * beta2;", "float vv = *v * omb2;"),
     "clip_not_clamped": ("return (c > 1.0f) ? 1.0f : c;", "return c;"),
     "clip_eps_dropped": ("float t = total_norm + (float)1e-6;", "float t = total_norm;"),
     "bf16_truncates": ("u += 0x7fffu + lsb;", "u += 0u * lsb;"),
@@ -41,8 +42,14 @@ MUTANTS = {
                          "for (int64_t i = b; i + 1 < e; ++i) { double x = (double)g[i]; s += x * x; }"),
     "amsgrad_max_unused": ("        dv = *vmax;\n", "        (void)dv;\n"),
     "amsgrad_min": ("return a < b ? b : a;", "return a < b ? a : b;"),
-    "grad_scale_ignored": ("if (apply_scale) gi = gi * grad_scale;\n        gi = gi * h->grad_sign;\n        adamw_elem",
-                           "gi = gi * h->grad_sign;\n        adamw_elem"),
+    "grad_scale_ignored": ("if (apply_scale) gi = gi * grad_scale;\n        gi = gi * h->grad_sign;\n        adamw_elem(",
+                           "gi = gi * h->grad_sign;\n        adamw_elem("),
+    "capt_multiplies_by_den_scale": ("d = d / h->den_scale;", "d = d * h->den_scale;"),
+    "capt_no_den_add": ("d = d + h->den_add;", "d = d;"),
+    "capt_update_sign": ("*p = *p + *m / d;", "*p = *p - *m / d;"),
+    "capt_no_bias_correction1": ("float step_size = lr_is_tensor ? lr / bc1 : (1.0f / bc1) * lr;",
+                                 "float step_size = lr;"),
+    "capt_eps_not_scaled": ("*den_add = (1.0f / neg) * eps;", "*den_add = eps;"),
 }
 
 
@@ -59,6 +66,12 @@ def _checks(gold):
             out.append(("float64_bound",
                         lambda om=om, s=step, a=b1, b=b2: T.test_float64_bound(om, s, a, b)))
     out.append(("zero_grad", T.test_zero_grad_decays_state))
+    out.append(("capt_lr_zero", T.test_capt_lr_zero_leaves_params_unchanged))
+    for lt in (False, True):
+        out.append(("capt_first_step", lambda lt=lt: T.test_capt_first_step_closed_form(lt)))
+    for args in ((1, 0.9, 0.95, False, False), (7, 0.9, 0.999, False, True),
+                 (1000, 0.9, 0.95, True, False), (250, 0.8, 0.99, True, True)):
+        out.append(("capt_vs_default", lambda a=args: T.test_capt_agrees_with_the_default_chain(*a)))
     out.append(("clip_closed_forms", T.test_clip_closed_forms))
     out.append(("sumsq_brute_force", T.test_sumsq_float64_brute_force))
     out.append(("bf16_vs_torch", T.test_bf16_rounding_matches_torch))
