@@ -13,7 +13,9 @@
  *                     coefficient and p, m, v bit-exact;
  *                   - tensor/chunk tables, three tensors, two hyperparameter
  *                     sets, bf16 moments and bf16 model copy: bit-exact;
- *                   - flat range with amsgrad: p, m, v, max_exp_avg_sq bit-exact.
+ *                   - flat range with amsgrad: p, m, v, max_exp_avg_sq bit-exact;
+ *                   - capturable chain through tables: two tensors at different
+ *                     device step counts, a float lr, then a device lr: bit-exact.
  *
  * The per-step scalars are computed here as the header documents (float64 on
  * the host, as torch/optim/adam.py:529-536 does, then cast to fp32), with
@@ -161,6 +163,16 @@ static int cpu_checks(void)
                              NULL) == MI_ADAMW_E_INVALID, "amsgrad without max_exp_avg_sq");
     CHECK(mi_adamw_grad_norm_flat(NULL, 10, 4096, 1.0f, NULL, NULL, NULL, NULL) ==
               MI_ADAMW_E_INVALID, "null gradient");
+    mi_adamw_capt_hyper ch;
+    memset(&ch, 0, sizeof ch);
+    CHECK(mi_adamw_step_capturable(fake, fake, 1, 4096, &ch, 1, NULL, fake, NULL, 0, 0, 0,
+                                   NULL) == MI_ADAMW_E_INVALID, "capturable without steps");
+    ch.lr_mode = 7;
+    CHECK(mi_adamw_step_capturable(fake, fake, 1, 4096, &ch, 1, fake, fake, NULL, 0, 0, 0,
+                                   NULL) == MI_ADAMW_E_INVALID, "unknown lr mode");
+    ch.lr_mode = MI_ADAMW_LR_DEVICE;
+    CHECK(mi_adamw_step_capturable(fake, fake, 1, 4096, &ch, 1, fake, fake, NULL, 0, 0, 0,
+                                   NULL) == MI_ADAMW_E_INVALID, "device lr without a pointer");
     printf("abi_check cpu: ok (%s)\n", mi_adamw_version());
     return 0;
 }
@@ -319,6 +331,108 @@ static void table_case(void)
            (long long)n_chunks);
 }
 
+/* The capturable chain through tables: two tensors at different device step
+ * counts (3 and 1), first with a float lr, then with a device lr.  beta1 = 0.5
+ * and beta2 = 0.75 make beta**step exact at these steps, so the oracle's libm
+ * powf and the device's powf agree by construction. */
+static void capt_case(void)
+{
+    enum { NT = 2 };
+    const int64_t numel[NT] = {2 * 4096 + 3, 70001};
+    const float steps[3] = {7.0f, 1.0f, 3.0f};  /* the device step buffer */
+    const int32_t step_index[NT] = {2, 1};      /* row -> index into steps */
+    float *p[NT], *g[NT], *m[NT], *v[NT], *pr[NT], *mr[NT], *vr[NT];
+    void *dp[NT], *dg[NT], *dm[NT], *dv[NT];
+    mi_adamw_tensor rows[NT];
+    for (int k = 0; k < NT; ++k) {
+        const int64_t n = numel[k];
+        p[k] = malloc(n * 4); g[k] = malloc(n * 4); m[k] = malloc(n * 4); v[k] = malloc(n * 4);
+        pr[k] = malloc(n * 4); mr[k] = malloc(n * 4); vr[k] = malloc(n * 4);
+        CHECK(p[k] && g[k] && m[k] && v[k] && pr[k] && mr[k] && vr[k], "host allocation");
+        fill(p[k], n, 0.02f, 0);
+        fill(g[k], n, 1e-3f, 0);
+        fill(m[k], n, 1e-3f, 0);
+        fill(v[k], n, 1e-6f, 1);
+        memcpy(pr[k], p[k], n * 4);
+        memcpy(mr[k], m[k], n * 4);
+        memcpy(vr[k], v[k], n * 4);
+        dp[k] = dev_copy(p[k], n * 4);
+        dg[k] = dev_copy(g[k], n * 4);
+        dm[k] = dev_copy(m[k], n * 4);
+        dv[k] = dev_copy(v[k], n * 4);
+        memset(&rows[k], 0, sizeof rows[k]);
+        rows[k].param = dp[k];
+        rows[k].grad = dg[k];
+        rows[k].exp_avg = dm[k];
+        rows[k].exp_avg_sq = dv[k];
+        rows[k].numel = n;
+        rows[k].flags = MI_ADAMW_T_VEC;
+    }
+    const int64_t n_chunks = mi_adamw_build_chunks(numel, NT, 4096, NULL, 0);
+    mi_adamw_chunk *chunks = malloc(n_chunks * sizeof *chunks);
+    CHECK(chunks && mi_adamw_build_chunks(numel, NT, 4096, chunks, n_chunks) == n_chunks,
+          "chunk table");
+    void *d_rows = dev_copy(rows, sizeof rows);
+    void *d_chunks = dev_copy(chunks, n_chunks * sizeof *chunks);
+    float *d_steps = dev_copy(steps, sizeof steps);
+    int32_t *d_index = dev_copy(step_index, sizeof step_index);
+    const float lr_dev = 2e-3f;
+    float *d_lr = dev_copy(&lr_dev, sizeof lr_dev);
+    for (int pass = 0; pass < 2; ++pass) {
+        mi_adamw_capt_hyper ch;
+        memset(&ch, 0, sizeof ch);
+        ch.beta1 = 0.5f;
+        ch.beta2 = 0.75f;
+        ch.lerp_w = (float)(1.0 - 0.5);
+        ch.one_minus_beta2 = (float)(1.0 - 0.75);
+        ch.eps = 1e-8f;
+        ch.grad_sign = 1.0f;
+        float lr, wd_factor;
+        if (pass == 0) {
+            ch.lr_mode = MI_ADAMW_LR_FLOAT;
+            ch.lr = lr = (float)1e-3;
+            ch.wd_factor = wd_factor = (float)(1.0 - 1e-3 * 0.1);
+        } else {
+            ch.lr_mode = MI_ADAMW_LR_DEVICE;
+            ch.lr_ptr = d_lr;
+            ch.weight_decay = 0.1f;
+            lr = lr_dev;
+            wd_factor = 1.0f - lr_dev * 0.1f;   /* two fp32 ops, as on the device */
+        }
+        const int rc = mi_adamw_step_capturable(d_rows, d_chunks, n_chunks, 4096, &ch, 1,
+                                                d_steps, d_index, NULL, MI_ADAMW_STATE_F32, 0,
+                                                0, NULL);
+        CHECK(rc == 0, "mi_adamw_step_capturable: %s", mi_adamw_strerror(rc));
+        HIP(hipDeviceSynchronize());
+        for (int k = 0; k < NT; ++k) {
+            const int64_t n = numel[k];
+            oracle_capt oc;
+            oc.wd_factor = wd_factor;
+            oc.lerp_w = ch.lerp_w;
+            oc.beta2 = ch.beta2;
+            oc.one_minus_beta2 = ch.one_minus_beta2;
+            oc.grad_sign = 1.0f;
+            oracle_capt_scalars(ch.beta1, ch.beta2, lr, ch.eps, steps[step_index[k]], pass,
+                                &oc.den_scale, &oc.den_add);
+            oracle_adamw_capt_f32(pr[k], g[k], mr[k], vr[k], NULL, n, &oc, &ROCM_OPS, 1.0f, 0);
+            back(p[k], dp[k], n * 4);
+            back(m[k], dm[k], n * 4);
+            back(v[k], dv[k], n * 4);
+            same_f32(p[k], pr[k], n, "param (capturable)");
+            same_f32(m[k], mr[k], n, "exp_avg (capturable)");
+            same_f32(v[k], vr[k], n, "exp_avg_sq (capturable)");
+        }
+    }
+    for (int k = 0; k < NT; ++k) {
+        HIP(hipFree(dp[k])); HIP(hipFree(dg[k])); HIP(hipFree(dm[k])); HIP(hipFree(dv[k]));
+        free(p[k]); free(g[k]); free(m[k]); free(v[k]); free(pr[k]); free(mr[k]); free(vr[k]);
+    }
+    HIP(hipFree(d_rows)); HIP(hipFree(d_chunks)); HIP(hipFree(d_steps)); HIP(hipFree(d_index));
+    HIP(hipFree(d_lr));
+    free(chunks);
+    printf("abi_check gpu: capturable tables, steps 3 and 1, float then device lr: bit-exact\n");
+}
+
 static int gpu_checks(void)
 {
     int count = 0;
@@ -328,6 +442,7 @@ static int gpu_checks(void)
     flat_case(1000003, 0);
     table_case();
     flat_case(262147, 1);
+    capt_case();
     printf("abi_check gpu: ok (%s)\n", mi_adamw_version());
     return 0;
 }

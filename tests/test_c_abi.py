@@ -30,4 +30,4 @@ def test_c_host_cpu_checks():
 @pytest.mark.gpu
 def test_c_host_gpu_parity_against_oracle():
     out = _run("gpu")
-    assert out.count("bit-exact") == 3 and "abi_check gpu: ok" in out
+    assert out.count("bit-exact") == 4 and "abi_check gpu: ok" in out
