@@ -253,17 +253,27 @@ def training_rows(device, batch: int, variants, iters: int = 20, warmup: int = 5
     """Training iterations of the reference GPT-125M (12 x 768, 12 heads, FFN 3072, vocab
     50304, batch x 512 tokens) as main.py:202-209 runs them with --amp: zero_grad, forward
     under bf16 autocast, backward, optimizer step.  Each variant is an optimizer choice on
-    its own copy of the model (same initialisation); variants alternate round by round."""
+    its own copy of the model (same initialisation); variants alternate round by round.
+    The "_graph" variants keep their gradients in place (the flat layout, or torch's
+    zero_grad(set_to_none=False)) and replay the optimizer step from a HIP graph recorded
+    after the warm-up iterations."""
     import contextlib
+    import warnings
     sys.path.insert(0, os.path.join(ROOT, "tests"))
     import refgpt
     from mi_adamw import FusedAdamW, bf16_weights
+    warnings.filterwarnings("ignore", message="This instance was constructed with capturable")
     ref_hp = dict(lr=6e-4, weight_decay=0.1)          # config.py:11,13; default betas and eps
     makers = {
         "torch_single_tensor": lambda ps: torch.optim.AdamW(ps, **ref_hp, fused=False),
         "torch_fused": lambda ps: torch.optim.AdamW(ps, **ref_hp, fused=True),
+        "torch_fused_graph": lambda ps: torch.optim.AdamW(ps, **ref_hp, fused=True,
+                                                          capturable=True),
         "mi_adamw": lambda ps: FusedAdamW(ps, **ref_hp, fused=False),
         "mi_adamw_bf16_weights": lambda ps: FusedAdamW(ps, **ref_hp, fused=False, bf16_copy=True),
+        "mi_adamw_flat": lambda ps: FusedAdamW(ps, **ref_hp, fused=False, flat_buffer=True),
+        "mi_adamw_flat_graph": lambda ps: FusedAdamW(ps, **ref_hp, fused=False, flat_buffer=True,
+                                                     capturable=True),
     }
     ids, labels, mask = refgpt.batch(device, b=batch, s=512, vocab=50304)
     runs = {}
@@ -273,20 +283,34 @@ def training_rows(device, batch: int, variants, iters: int = 20, warmup: int = 5
         runs[name] = (model, makers[name](model.parameters()))
     n_linear = sum(1 for m in runs[variants[0]][0].modules() if isinstance(m, refgpt.ColumnLinear))
 
+    graphs = {}
+
     def iteration(name):
         model, opt = runs[name]
-        opt.zero_grad()
+        opt.zero_grad(set_to_none=not name.endswith("_graph"))
         ctx = (bf16_weights(opt, model) if name == "mi_adamw_bf16_weights"
                else contextlib.nullcontext())
         with torch.autocast("cuda", dtype=torch.bfloat16), ctx:
             _, loss = model(ids, labels, mask)
         loss.backward()
-        opt.step()
+        if name in graphs:
+            graphs[name].replay()
+        else:
+            opt.step()
 
     times = {name: [] for name in variants}
     for name in variants:
-        for _ in range(warmup):
-            iteration(name)
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            for _ in range(warmup):
+                iteration(name)
+        torch.cuda.current_stream().wait_stream(side)
+        if name.endswith("_graph"):
+            torch.cuda.synchronize()
+            graphs[name] = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graphs[name]):
+                runs[name][1].step()
     torch.cuda.synchronize()
     for _ in range(rounds):
         for name in variants:
@@ -298,7 +322,7 @@ def training_rows(device, batch: int, variants, iters: int = 20, warmup: int = 5
                 e1.record()
             torch.cuda.synchronize()
             times[name] += [e0.elapsed_time(e1) for e0, e1 in evs]
-    del runs
+    del runs, graphs
     torch.cuda.empty_cache()
     rows = {}
     for name in variants:
@@ -449,7 +473,8 @@ def main() -> int:
         # batch for the bf16 copies against autocast's casts
         line["training"] = [
             training_rows(device, 4, ["torch_single_tensor", "torch_fused", "mi_adamw",
-                                      "mi_adamw_bf16_weights"]),
+                                      "mi_adamw_bf16_weights", "mi_adamw_flat",
+                                      "torch_fused_graph", "mi_adamw_flat_graph"]),
             training_rows(device, 16, ["mi_adamw", "mi_adamw_bf16_weights"]),
         ]
         for row in line["training"]:
