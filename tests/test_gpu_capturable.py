@@ -318,3 +318,58 @@ def test_capturable_bf16_state_matches_oracle(dev, amsgrad, clip):
             assert np.array_equal(vb, st["exp_avg_sq"].view(torch.int16).cpu().numpy().view(np.uint16).reshape(-1))
             if amsgrad:
                 assert np.array_equal(xb, st["max_exp_avg_sq"].view(torch.int16).cpu().numpy().view(np.uint16).reshape(-1))
+
+
+def test_capturable_params_without_grads_and_many_groups(dev):
+    """Tensors of one launch at different device step counts (some params skip steps:
+    the counts advance by index_add_ over the stepped ones), over 18 param groups, more
+    than one launch's 16 constant sets."""
+    import mi_adamw
+    shapes = [(37,), (4099,), (64, 48), (5,)] * 9
+    ref = make_params(shapes, dev)
+    ours = clone_params(ref)
+    groups = lambda ps: [dict(params=ps[2 * i:2 * i + 2], lr=1e-4 * (i + 1),   # noqa: E731
+                              weight_decay=0.01 * (i % 3)) for i in range(18)]
+    topt = torch.optim.AdamW(groups(ref), foreach=False, capturable=True)
+    oopt = mi_adamw.FusedAdamW(groups(ours), foreach=False, capturable=True)
+    for step in range(1, 7):
+        set_grads(ref, step, 1e-3)
+        for i, (p, q) in enumerate(zip(ref, ours)):
+            if (i % 5 == 0 and step % 2 == 0) or (i % 3 == 1 and step == 3):   # skips
+                p.grad = None
+                q.grad = None
+            else:
+                q.grad = p.grad.clone()
+        topt.step()
+        oopt.step()
+        torch.cuda.synchronize()
+        assert max_ulp_all(ref, ours) == 0
+        for p, q in zip(ref, ours):
+            if p in topt.state:
+                assert torch.equal(topt.state[p]["step"], oopt.state[q]["step"])
+                assert max_ulp(topt.state[p]["exp_avg_sq"], oopt.state[q]["exp_avg_sq"]) == 0
+    steps = {float(oopt.state[q]["step"]) for q in ours}
+    assert len(steps) > 1
+
+
+def test_capturable_deepcopy_mid_training(dev):
+    """copy.deepcopy of a capturable FusedAdamW mid-training: the copy's device step
+    counts and moments continue exactly as the original's."""
+    ref, ours, topt, oopt = _pair(dev, weight_decay=0.1)
+    for step in range(1, 4):
+        set_grads(ref, step, 1e-3)
+        _copy_grads(ref, ours)
+        topt.step()
+        oopt.step()
+    twin = copy.deepcopy({"params": ours, "opt": oopt})
+    ours2, o2 = twin["params"], twin["opt"]
+    assert all(o2.state[q]["step"].device == dev for q in ours2)
+    for step in range(4, 7):
+        set_grads(ref, step, 1e-3)
+        _copy_grads(ref, ours)
+        _copy_grads(ref, ours2)
+        topt.step()
+        oopt.step()
+        o2.step()
+    _same(ref, ours, topt, oopt)
+    _same(ref, ours2, topt, o2)
