@@ -67,7 +67,7 @@ def log(msg: str) -> None:
     print(msg, file=sys.stderr, flush=True)
 
 
-def build_set(name: str, device):
+def build_set(name: str, device, capturable: bool = False):
     """Params (init as mini-megatron's model), resident grads and the optimizer."""
     import mi_adamw
     from mi_adamw.workloads import SHAPES, init_kind
@@ -87,7 +87,8 @@ def build_set(name: str, device):
         params.append(torch.nn.Parameter(t))
     opt = mi_adamw.FusedAdamW(params, **HP, max_grad_norm=1.0 if clip else None,
                               state_dtype=torch.bfloat16 if state == "bf16" else torch.float32,
-                              bf16_copy=copy, flat_buffer=flat, fused=False)
+                              bf16_copy=copy, flat_buffer=flat, fused=False,
+                              capturable=capturable)
     for i, p in enumerate(params):
         g = torch.Generator(device)
         grad = torch.randn(p.shape, device=device, generator=g.manual_seed(4000 + i)).mul_(gstd)
@@ -349,10 +350,11 @@ def load_traffic(name: str):
     return None if entry is None else entry.get("bytes_per_launch")
 
 
-def run_config(name: str, steps: int, warmup: int, device, with_context: bool) -> dict:
+def run_config(name: str, steps: int, warmup: int, device, with_context: bool,
+               capturable: bool = False) -> dict:
     shape_name, clip, state, copy, flat, start_step, gstd = CONFIGS[name]
-    log(f"[bench] {name}: building {shape_name} set")
-    params, opt, n, n_tensors = build_set(name, device)
+    log(f"[bench] {name}: building {shape_name} set" + (" (capturable)" if capturable else ""))
+    params, opt, n, n_tensors = build_set(name, device, capturable)
     total_b, upd_b = bytes_per_param(clip, state, copy)
     log(f"[bench] {name}: {n} params in {n_tensors} tensors; timing {steps} steps")
     gpu_ms, wall_ms, norm_ms, upd_ms, step_ms = time_fused(opt, steps, warmup)
@@ -393,6 +395,10 @@ def main() -> int:
     ap.add_argument("--training", action="store_true",
                     help="also time gpt-125m training iterations (bf16 autocast) with torch's "
                          "per-tensor and fused AdamW, FusedAdamW, and FusedAdamW + bf16_weights")
+    ap.add_argument("--capturable", action="store_true",
+                    help="step with FusedAdamW(capturable=True): torch's capturable op chain, "
+                         "device step counts (the step-count increment runs before the timed "
+                         "norm/update events)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="after the timed steps, run 3 plain 1 GiB device copies (torch copy_) "
                          "so a counter run (rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE) sees a "
@@ -410,8 +416,12 @@ def main() -> int:
     log(f"[bench] {mi_adamw.version()} on {torch.cuda.get_device_name(0)}")
 
     names = list(CONFIGS) if args.config == "all" else [args.config]
+    if args.capturable:
+        import warnings
+        warnings.filterwarnings("ignore", message="This instance was constructed with capturable")
     results = [run_config(nm, args.steps, args.warmup, device,
-                          with_context=not args.no_context and nm == names[0]) for nm in names]
+                          with_context=not args.no_context and nm == names[0],
+                          capturable=args.capturable) for nm in names]
     if args.calibrate_copy:
         src = torch.ones(1 << 28, device=device)
         dst = torch.empty_like(src)
@@ -421,7 +431,8 @@ def main() -> int:
         del src, dst
     head = results[0]
     shape_name, clip, state, copy, flat, start_step, gstd = CONFIGS[head["config"]]
-    traffic = load_traffic(head["config"])
+    # the PMC figures in profiles/ are for the default chain's update kernel
+    traffic = None if args.capturable else load_traffic(head["config"])
     line = {
         "metric": METRIC,
         "value": round(head["gbs"], 2),
@@ -443,6 +454,7 @@ def main() -> int:
             "stored_step": start_step, "lr": HP["lr"], "betas": list(HP["betas"]),
             "eps": HP["eps"], "weight_decay": HP["weight_decay"],
             "bytes_per_step": head["bytes_per_step"],
+            **({"capturable": True} if args.capturable else {}),
         },
         "pct_of_peak": round(100 * head["gbs"] / PEAK_HBM_GBS, 2),
         "params_per_s": round(head["params_per_s"], 1),
