@@ -408,3 +408,33 @@ def test_flat_layout_makes_no_per_parameter_copies():
         with pytest.raises(RuntimeError, match="ROCm GPU"):
             mi_adamw.FusedAdamW([torch.nn.Parameter(torch.zeros(3))], bf16_copy=True,
                                 flat_buffer=True)
+
+
+def test_capturable_launch_maps_rows_to_step_slots_on_cpu():
+    """A capturable launch (built on CPU tensors, no kernel): one row per non-empty
+    tensor, always as tables (each tensor has its own device step count), and a
+    step index giving each row its parameter's slot in the packed step buffer."""
+    from mi_adamw.optimizer import _Rec
+    params = [torch.nn.Parameter(torch.zeros(n)) for n in (6, 0, 4097, 3)]
+    opt = mi_adamw.FusedAdamW(params, capturable=True)
+    entries = []
+    for p in params:
+        rec = _Rec(0, p, opt._slots[id(p)])
+        rec.st = opt.state[p]
+        opt._init_state(p, rec.st, False)
+        entries.append((rec, torch.zeros_like(p)))
+    launch = opt._new_launch(entries, [0] * 4, False, torch.device("cpu"))
+    assert launch.tables and launch.n_rows == 3
+    assert list(launch.host_rows["numel"]) == [6, 4097, 3]
+    # uploaded as raw bytes; the kernel reads them as int32
+    assert launch.step_index.view(torch.int32).tolist() == [opt._slots[id(params[i])]
+                                                            for i in (0, 2, 3)]
+    one = opt._new_launch(entries[2:3], [0], False, torch.device("cpu"))
+    assert one.tables and one.n_rows == 1
+    assert one.step_index.view(torch.int32).tolist() == [opt._slots[id(params[2])]]
+    # the state's step tensors are views of the packed buffer, as torch's capturable layout
+    # has one 0-d fp32 step per parameter
+    for p in params:
+        st = opt.state[p]["step"]
+        assert st.dim() == 0 and st.dtype == torch.float32
+        assert st.data_ptr() == opt._steps[opt._slots[id(p)]].data_ptr()
