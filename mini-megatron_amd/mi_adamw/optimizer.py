@@ -406,8 +406,13 @@ class FusedAdamW(Optimizer):
                                       "construction is not supported")
         if getattr(self, "bf16_copy", False):
             ps = param_group["params"]
-            for p in ([ps] if isinstance(ps, torch.Tensor) else list(ps)):
-                self._check_copyable(p)
+            if not isinstance(ps, (torch.Tensor, set)):
+                # materialised in place, as torch's add_param_group does, so that a
+                # generator is not consumed by this check
+                ps = param_group["params"] = list(ps)
+            for p in ([ps] if isinstance(ps, torch.Tensor) else ps):
+                # torch also takes (name, parameter) pairs (named_parameters())
+                self._check_copyable(p[1] if isinstance(p, tuple) else p)
         if hasattr(self, "capturable") and \
                 bool(param_group.get("capturable", self.capturable)) != self.capturable:
             raise NotImplementedError("FusedAdamW: every param group must share the "

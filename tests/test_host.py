@@ -438,3 +438,21 @@ def test_capturable_launch_maps_rows_to_step_slots_on_cpu():
         st = opt.state[p]["step"]
         assert st.dim() == 0 and st.dtype == torch.float32
         assert st.data_ptr() == opt._steps[opt._slots[id(p)]].data_ptr()
+
+
+def test_param_groups_from_generators_and_named_parameters():
+    """A group dict holding a generator, and torch's (name, parameter) pairs, register
+    every parameter, with and without bf16 copies (the copy check must not consume
+    the generator)."""
+    m = torch.nn.Linear(4, 3)
+    for copy in (False, True):
+        o = mi_adamw.FusedAdamW([{"params": m.parameters()}], bf16_copy=copy)
+        assert len(o.param_groups[0]["params"]) == 2
+        o.add_param_group({"params": (p for p in [torch.nn.Parameter(torch.zeros(5))])})
+        assert len(o.param_groups[1]["params"]) == 1
+        # named groups (torch refuses to mix them with unnamed ones, and so do we)
+        o = mi_adamw.FusedAdamW(m.named_parameters(), bf16_copy=copy)
+        assert o.param_groups[0]["param_names"] == ["weight", "bias"]
+        assert [id(p) for p in o.param_groups[0]["params"]] == [id(m.weight), id(m.bias)]
+        if copy:
+            assert o.bf16_param(m.weight).dtype == torch.bfloat16
