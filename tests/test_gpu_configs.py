@@ -247,3 +247,34 @@ def test_config5_6p7b_flat_clip_bf16_copy(dev):
         assert max_ulp(opt.state[q]["exp_avg_sq"], tref.state[p]["exp_avg_sq"]) == 0
         assert float(opt.state[q]["step"]) == 1001.0
         assert torch.equal(opt.bf16_param(q), q.detach().to(torch.bfloat16))
+
+
+@pytest.mark.filterwarnings("ignore:This instance was constructed with capturable=True")
+def test_config2_125m_clip_100_chained_capturable(dev):
+    """Config 2 in capturable mode: 100 chained clipped steps from step 1000 at gpt-125m,
+    bit-exact against torch.optim.AdamW(capturable=True, foreach=False) driven by the
+    kernel's norm, the step counts on the device."""
+    import mi_adamw
+    from mi_adamw.workloads import GPT_125M
+    ref = gpt_params(GPT_125M, dev)
+    ours = clone_params(ref)
+    topt = torch.optim.AdamW(ref, foreach=False, capturable=True, **HP)
+    oopt = mi_adamw.FusedAdamW(ours, max_grad_norm=1.0, capturable=True, **HP)
+    states = midtrain_state(ref, 1000.0)
+    load_states(topt, ref, states)
+    load_states(oopt, ours, states)
+    del states
+    for step in range(100):
+        set_grads(ref, step, 1e-2)
+        for p, q in zip(ref, ours):
+            q.grad.copy_(p.grad) if q.grad is not None else setattr(q, "grad", p.grad.clone())
+        oopt.step()
+        torch.nn.utils.clip_grads_with_norm_(ref, 1.0, oopt.last_grad_norm.clone())
+        topt.step()
+    torch.cuda.synchronize()
+    d = _same_state(ref, ours, topt, oopt)
+    print("config2 capturable ulp vs torch capturable with the same norms (p, m, v):", d,
+          flush=True)
+    assert max(d) == 0
+    assert all(float(oopt.state[q]["step"]) == 1100.0 for q in ours)
+    assert all(oopt.state[q]["step"].device == dev for q in ours)
