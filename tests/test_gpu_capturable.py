@@ -373,3 +373,54 @@ def test_capturable_deepcopy_mid_training(dev):
         o2.step()
     _same(ref, ours, topt, oopt)
     _same(ref, ours2, topt, o2)
+
+
+def test_whole_training_iteration_in_one_graph(dev):
+    """zero_grad, a bf16-autocast forward and backward of a reference-shaped GPT and the
+    capturable step (flat layout, clip), recorded into one HIP graph: every replay, with
+    new batches copied into the static inputs and eager work in between, is bit-identical
+    to the same iteration run eagerly on a twin model (loss, gradients, parameters)."""
+    import mi_adamw
+    import refgpt
+
+    def build():
+        model = refgpt.tiny(dev, seed=4)
+        opt = mi_adamw.FusedAdamW(model.parameters(), lr=6e-4, weight_decay=0.1,
+                                  capturable=True, flat_buffer=True, max_grad_norm=1.0)
+        return model, opt
+
+    def iteration(model, opt, ids, labels, mask):
+        opt.zero_grad()
+        with torch.autocast("cuda", dtype=torch.bfloat16, cache_enabled=False):
+            _, loss = model(ids, labels, mask)
+        loss.backward()
+        opt.step()
+        return loss
+
+    eager, graphed = build(), build()
+    data = [refgpt.batch(dev, seed=s) for s in range(10)]
+    static = [t.clone() for t in data[0]]
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for k in range(3):
+            for t, src in zip(static, data[k]):
+                t.copy_(src)
+            iteration(*graphed, *static)
+            iteration(*eager, *data[k])
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        static_loss = iteration(*graphed, *static)
+    for k in range(3, 10):
+        for t, src in zip(static, data[k]):
+            t.copy_(src)
+        graph.replay()
+        loss = iteration(*eager, *data[k])
+        torch.cuda.synchronize()
+        assert torch.equal(static_loss, loss)
+        for p, q in zip(eager[0].parameters(), graphed[0].parameters()):
+            assert torch.equal(p.grad, q.grad) and torch.equal(p, q)
+        torch.randn(1 << 16, device=dev).sum().item()
+    assert float(graphed[1].state[next(graphed[0].parameters())]["step"]) == 10.0
