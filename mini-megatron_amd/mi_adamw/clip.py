@@ -18,14 +18,21 @@ import torch
 from . import _lib
 
 _CHUNK = 4096
-_workspace: dict[torch.device, tuple] = {}
+_workspace: dict[tuple, tuple] = {}
 _cache: dict[tuple, tuple] = {}
 
 
-def _ws(device):
-    ws = _workspace.get(device)
+def _ws(device, stream: int):
+    """Partial sums and coefficient, one set per (device, stream): calls on different
+    streams may overlap and must not share scratch (calls on one stream are ordered)."""
+    key = (device, stream)
+    ws = _workspace.get(key)
     if ws is None:
-        ws = _workspace[device] = (
+        if len(_workspace) > 16:
+            # a freed block returns to the pool of the stream it was allocated on, and
+            # any reuse there is ordered after the work already queued on that stream
+            _workspace.clear()
+        ws = _workspace[key] = (
             torch.zeros(_lib.MAX_NORM_BLOCKS, dtype=torch.float64, device=device),
             torch.zeros(1, dtype=torch.float32, device=device),
         )
@@ -77,11 +84,11 @@ def clip_grad_norm_(parameters, max_norm: float, norm_type: float = 2.0,
             raise NotImplementedError("mi_adamw.clip_grad_norm_ supports dense contiguous fp32 "
                                       "gradients only")
     lib = _lib.load()
-    partials, coef = _ws(device)
     norm = torch.empty((), dtype=torch.float32, device=device)
     with torch.cuda.device(device):
         launch = _tables(grads, device)
         stream = torch.cuda.current_stream(device).cuda_stream
+        partials, coef = _ws(device, stream)
         if launch.n_chunks == 0:
             norm.zero_()
             return norm

@@ -217,6 +217,30 @@ def test_clip_grad_norm_with_moving_gradients(dev):
     assert len(keys) == 1, "one chunk table for one set of sizes"
 
 
+def test_clip_grad_norm_on_two_streams(dev):
+    """Two clip_grad_norm_ calls on two streams with no ordering between them (their
+    scratch is per stream): each norm and each scaled gradient as torch's alone."""
+    import mi_adamw
+    sets = []
+    for k, shapes in enumerate((MINI_SHAPES, MINI_SHAPES[::-1])):
+        ref = make_params(shapes, dev, seed=1000 + 100 * k)
+        set_grads(ref, 7 + k, 1e-2 * (k + 1))
+        sets.append((ref, clone_params(ref)))
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    for s_ in streams:
+        s_.wait_stream(torch.cuda.current_stream())
+    norms = []
+    for (ref, ours), s_ in zip(sets, streams):
+        with torch.cuda.stream(s_):
+            norms.append(mi_adamw.clip_grad_norm_(ours, 1.0))
+    torch.cuda.synchronize()
+    for (ref, ours), on in zip(sets, norms):
+        tn = torch.nn.utils.clip_grad_norm_(ref, 1.0)
+        assert rel_err(on, tn) <= 1e-6
+        for p, q in zip(ref, ours):
+            assert close_rel(q.grad, p.grad, 1e-6, 1e-12) <= 1.0
+
+
 def test_bf16_copy_and_state(dev):
     import mi_adamw
     params = make_params(MINI_SHAPES, dev)
