@@ -40,7 +40,7 @@
 extern "C" {
 #endif
 
-#define MI_ADAMW_ABI_VERSION 3
+#define MI_ADAMW_ABI_VERSION 4
 #define MI_ADAMW_MAX_HYPER 16      /* hyperparameter sets per launch */
 #define MI_ADAMW_MAX_NORM_BLOCKS 4096 /* partial sums per grad-norm launch */
 
@@ -168,6 +168,18 @@ int mi_adamw_grad_norm_flat(const float *d_grad, int64_t n, int64_t chunk_elems,
 int mi_adamw_scale_grads(const mi_adamw_tensor *d_tensors, const mi_adamw_chunk *d_chunks,
                          int64_t n_chunks, int64_t chunk_elems, const float *d_coef,
                          void *stream);
+
+/* bf16 -> fp32 of every tensor of the tables in one launch: for each row,
+ * param[i] = (float)param_copy[i] (param_copy holds the bf16 source, param the fp32
+ * destination), exact.  Replaces one Tensor.to(torch.float32) per weight: the
+ * backward of the bf16 cast that autocast applies to every linear weight in
+ * mini-megatron's --amp forward (main.py:93; F.linear at
+ * parallel/tensor_parallel.py:55,79), which widens each bf16 weight gradient for its
+ * fp32 master.  mi_adamw.bf16_weights, which replaces the forward cast, widens all
+ * of them with this one launch.  MI_ADAMW_T_VEC: param 16-byte and param_copy 8-byte
+ * aligned. */
+int mi_adamw_widen_bf16(const mi_adamw_tensor *d_tensors, const mi_adamw_chunk *d_chunks,
+                        int64_t n_chunks, int64_t chunk_elems, void *stream);
 
 /* The fused AdamW update over every chunk of the tables (one launch).
  * Replaces the per-tensor loop body of adam.py:396-547.

@@ -35,14 +35,71 @@ parameters this context replaces.
 """
 from __future__ import annotations
 
+import numpy as np
 import torch
+
+from . import _lib
+
+_WIDEN_CHUNK = 4096
+_widen_tables: dict[tuple, object] = {}
+
+
+def _widen_on_gpu(srcs: list[torch.Tensor], device: torch.device) -> list[torch.Tensor]:
+    """fp32 copies of contiguous bf16 tensors on one GPU, one launch for all of them
+    (mi_adamw_widen_bf16).  The chunk table depends on the sizes only and is kept; the
+    rows, whose pointers change with every backward, are rewritten."""
+    from .optimizer import _ROW_DTYPE, _Launch
+    dsts = [torch.empty(t.shape, dtype=torch.float32, device=device) for t in srcs]
+    rows = np.zeros(len(srcs), dtype=_ROW_DTYPE)
+    rows["param"] = [d.data_ptr() for d in dsts]
+    rows["param_copy"] = [t.data_ptr() for t in srcs]
+    rows["numel"] = [t.numel() for t in srcs]
+    rows["flags"] = np.where((rows["param"] % 16 == 0) & (rows["param_copy"] % 8 == 0),
+                             _lib.T_VEC, 0)
+    rows = rows[rows["numel"] > 0]
+    if len(rows) == 0:
+        return dsts
+    key = (device, tuple(int(n) for n in rows["numel"]))
+    launch = _widen_tables.get(key)
+    if launch is None:
+        if len(_widen_tables) > 8:
+            _widen_tables.clear()
+        launch = _widen_tables[key] = _Launch(rows, _WIDEN_CHUNK, device, tables=True)
+    else:
+        launch.set_rows(rows, device)
+    lib = _lib.load()
+    with torch.cuda.device(device):
+        _lib.check(lib.mi_adamw_widen_bf16(
+            launch.rows.data_ptr(), launch.chunks.data_ptr(), launch.n_chunks, _WIDEN_CHUNK,
+            torch.cuda.current_stream(device).cuda_stream), "mi_adamw_widen_bf16")
+    return dsts
+
+
+def _widen(grads) -> tuple:
+    """Each bf16 gradient widened to fp32 (exact: a bf16 value is the upper half of
+    its fp32 bits).  The GPU ones, all of a backward's weight gradients, in one launch
+    per device; CPU tensors (the CPU autocast of the tests) by torch's cast."""
+    out: list = [None] * len(grads)
+    by_device: dict[torch.device, list[int]] = {}
+    for i, g in enumerate(grads):
+        if g is None:
+            continue
+        if g.is_cuda and g.dtype == torch.bfloat16:
+            by_device.setdefault(g.device, []).append(i)
+        else:
+            out[i] = g.to(torch.float32)
+    for device, idx in by_device.items():
+        for i, d in zip(idx, _widen_on_gpu([grads[i].contiguous() for i in idx], device)):
+            out[i] = d
+    return tuple(out)
 
 
 class _MastersAsBf16(torch.autograd.Function):
     """Forward: the bf16 copies of n masters.  Backward: each copy's gradient
     widened to fp32 for its master (what ``Tensor.to``'s backward does for
-    autocast's cast).  One node for every swapped weight, so the host pays one
-    Python call per forward and one per backward, not one per weight."""
+    autocast's cast), all of them in one launch.  One node for every swapped
+    weight, so the host pays one Python call per forward and one per backward,
+    not one per weight."""
 
     @staticmethod
     def forward(ctx, copies, *masters):
@@ -52,7 +109,7 @@ class _MastersAsBf16(torch.autograd.Function):
 
     @staticmethod
     def backward(ctx, *grads):
-        return (None,) + tuple(None if g is None else g.to(torch.float32) for g in grads)
+        return (None,) + _widen(grads)
 
 
 def linear_layers(module: torch.nn.Module) -> bool:

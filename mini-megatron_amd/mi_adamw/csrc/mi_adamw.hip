@@ -16,6 +16,8 @@
 //                          capturable one (per-step scalars formed per workgroup
 //                          from a device step count, for HIP graph capture).
 //   mi_adamw_scale_kernel  g *= coef in place (clip_grad_norm_'s write-back).
+//   mi_adamw_widen_kernel  bf16 -> fp32 of many tensors in one launch (the backward of
+//                          the bf16 weight copies the forward runs on), exact.
 //
 // Every launch walks a chunk table (one entry per `chunk_elems` slice of a
 // tensor) so that all parameter tensors go through one launch, or one
@@ -603,6 +605,30 @@ __global__ __launch_bounds__(kUpdThreads) void mi_adamw_scale_kernel(
 }
 
 // ---------------------------------------------------------------------------
+// bf16 -> fp32 of every tensor of the tables: param = (float)param_copy, exact (the bf16
+// bits are the upper half of the fp32 value, NaN payloads included).
+
+__global__ __launch_bounds__(kUpdThreads) void mi_adamw_widen_kernel(
+    TableSource src, int64_t n_chunks, int64_t chunk_elems) {
+    for (int64_t c = blockIdx.x; c < n_chunks; c += gridDim.x) {
+        mi_adamw_tensor t;
+        int64_t begin, end;
+        int32_t row;
+        src.get(c, chunk_elems, t, begin, end, row);
+        const uint16_t* __restrict__ S = t.param_copy;
+        float* __restrict__ D = t.param;
+        int64_t vend = begin;
+        if (t.flags & MI_ADAMW_T_VEC) {
+            vend = begin + ((end - begin) & ~static_cast<int64_t>(kVec - 1));
+            for (int64_t i = begin + threadIdx.x * kVec; i < vend; i += kUpdTile)
+                st4(D + i, ld4_bf16(S + i));
+        }
+        for (int64_t j = vend + threadIdx.x; j < end; j += kUpdThreads)
+            st1(D + j, bf16_to_f32(ld1_u16(S + j)));
+    }
+}
+
+// ---------------------------------------------------------------------------
 // Host side
 
 // Workgroups (and partial sums) of the norm pass: two 256-thread workgroups per CU.
@@ -736,8 +762,8 @@ int check_flat(const mi_adamw_tensor* t, int32_t state_dtype, int32_t flags) {
 extern "C" {
 
 const char* mi_adamw_version(void) {
-    return "mi_adamw 3 gfx950 fused clip+adamw (fp32/bf16 state, bf16 copy, amsgrad, flat, "
-           "capturable)";
+    return "mi_adamw 4 gfx950 fused clip+adamw (fp32/bf16 state, bf16 copy, amsgrad, flat, "
+           "capturable, bf16 widen)";
 }
 
 const char* mi_adamw_strerror(int code) {
@@ -798,6 +824,17 @@ int mi_adamw_scale_grads(const mi_adamw_tensor* d_tensors, const mi_adamw_chunk*
     hipLaunchKernelGGL(mi_adamw_scale_kernel, dim3(grid_for(n_chunks, 0, kUpdThreads)),
                        dim3(kUpdThreads), 0,
                        static_cast<hipStream_t>(stream), src, n_chunks, chunk_elems, d_coef);
+    return launch_status();
+}
+
+int mi_adamw_widen_bf16(const mi_adamw_tensor* d_tensors, const mi_adamw_chunk* d_chunks,
+                        int64_t n_chunks, int64_t chunk_elems, void* stream) {
+    if (!d_tensors || !d_chunks || n_chunks <= 0 || !chunk_elems_ok(chunk_elems))
+        return MI_ADAMW_E_INVALID;
+    TableSource src{d_tensors, d_chunks};
+    hipLaunchKernelGGL(mi_adamw_widen_kernel, dim3(grid_for(n_chunks, 0, kUpdThreads)),
+                       dim3(kUpdThreads), 0, static_cast<hipStream_t>(stream), src, n_chunks,
+                       chunk_elems);
     return launch_status();
 }
 

@@ -173,6 +173,12 @@ static int cpu_checks(void)
     ch.lr_mode = MI_ADAMW_LR_DEVICE;
     CHECK(mi_adamw_step_capturable(fake, fake, 1, 4096, &ch, 1, fake, fake, NULL, 0, 0, 0,
                                    NULL) == MI_ADAMW_E_INVALID, "device lr without a pointer");
+    CHECK(mi_adamw_widen_bf16(NULL, fake, 1, 4096, NULL) == MI_ADAMW_E_INVALID,
+          "widen without tensors");
+    CHECK(mi_adamw_widen_bf16(fake, fake, 0, 4096, NULL) == MI_ADAMW_E_INVALID,
+          "widen with no chunks");
+    CHECK(mi_adamw_widen_bf16(fake, fake, 1, 1000, NULL) == MI_ADAMW_E_INVALID,
+          "widen chunk size");
     printf("abi_check cpu: ok (%s)\n", mi_adamw_version());
     return 0;
 }

@@ -66,3 +66,22 @@ def test_weight_casts_disappear_on_the_gpu(dev):
     n_linear = sum(1 for m in model.modules() if isinstance(m, refgpt.ColumnLinear))
     print("aten::_to_copy per forward", plain, swapped, flush=True)
     assert plain - swapped == n_linear
+
+
+def test_widen_every_bf16_pattern_like_torch(dev):
+    """The one-launch widening of the weight gradients: all 2^16 bf16 bit patterns (NaN
+    payloads, infinities, denormals, signed zeros) give torch's Tensor.to(float32) bits,
+    through the vector path, a ragged tail and a 2-byte-misaligned view (scalar path)."""
+    from mi_adamw.bf16_forward import _widen
+    every = torch.arange(-32768, 32768, dtype=torch.int32).to(torch.int16).view(torch.bfloat16)
+    every = every.to(dev)
+    srcs = [every, every[:4099], every[1:4098], every[5:8], every[:0],
+            every.view(256, 256).t().contiguous()]
+    outs = _widen(srcs)
+    for s_, o in zip(srcs, outs):
+        assert o.dtype == torch.float32 and o.shape == s_.shape
+        assert torch.equal(o.view(torch.int32), s_.to(torch.float32).view(torch.int32))
+    # a None gradient stays None, and a CPU tensor takes torch's cast
+    cpu = every[:10].cpu()
+    none, host = _widen([None, cpu])
+    assert none is None and torch.equal(host.view(torch.int32), cpu.float().view(torch.int32))
