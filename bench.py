@@ -52,14 +52,16 @@ DEFAULT_CONFIG = "125m-clip"
 HP = dict(lr=3e-4, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.1)
 
 
-def bytes_per_param(clip: bool, state: str, copy: bool) -> tuple[int, int]:
+def bytes_per_param(clip: bool, state: str, copy: bool,
+                    write_grads: bool = False) -> tuple[int, int]:
     """(whole step, update kernel) algorithmic bytes per parameter.
 
     Update: read p, g (4 B each) and m, v (4 or 2 B each); write p, m, v and
-    the bf16 copy (2 B).  The clip adds one more read of g in the norm pass.
+    the bf16 copy (2 B), and with write_grads the clipped g (4 B).  The clip adds
+    one more read of g in the norm pass.
     """
     s = 4 if state == "fp32" else 2
-    update = 4 + 4 + 2 * s + 4 + 2 * s + (2 if copy else 0)
+    update = 4 + 4 + 2 * s + 4 + 2 * s + (2 if copy else 0) + (4 if write_grads else 0)
     return update + (4 if clip else 0), update
 
 
@@ -67,7 +69,7 @@ def log(msg: str) -> None:
     print(msg, file=sys.stderr, flush=True)
 
 
-def build_set(name: str, device, capturable: bool = False):
+def build_set(name: str, device, capturable: bool = False, write_grads: bool = False):
     """Params (init as mini-megatron's model), resident grads and the optimizer."""
     import mi_adamw
     from mi_adamw.workloads import SHAPES, init_kind
@@ -88,7 +90,7 @@ def build_set(name: str, device, capturable: bool = False):
     opt = mi_adamw.FusedAdamW(params, **HP, max_grad_norm=1.0 if clip else None,
                               state_dtype=torch.bfloat16 if state == "bf16" else torch.float32,
                               bf16_copy=copy, flat_buffer=flat, fused=False,
-                              capturable=capturable)
+                              capturable=capturable, clip_write_grads=write_grads)
     for i, p in enumerate(params):
         g = torch.Generator(device)
         grad = torch.randn(p.shape, device=device, generator=g.manual_seed(4000 + i)).mul_(gstd)
@@ -351,11 +353,12 @@ def load_traffic(name: str):
 
 
 def run_config(name: str, steps: int, warmup: int, device, with_context: bool,
-               capturable: bool = False) -> dict:
+               capturable: bool = False, write_grads: bool = False) -> dict:
     shape_name, clip, state, copy, flat, start_step, gstd = CONFIGS[name]
-    log(f"[bench] {name}: building {shape_name} set" + (" (capturable)" if capturable else ""))
-    params, opt, n, n_tensors = build_set(name, device, capturable)
-    total_b, upd_b = bytes_per_param(clip, state, copy)
+    log(f"[bench] {name}: building {shape_name} set" + (" (capturable)" if capturable else "")
+        + (" (clipped grads written back)" if write_grads else ""))
+    params, opt, n, n_tensors = build_set(name, device, capturable, write_grads)
+    total_b, upd_b = bytes_per_param(clip, state, copy, write_grads)
     log(f"[bench] {name}: {n} params in {n_tensors} tensors; timing {steps} steps")
     gpu_ms, wall_ms, norm_ms, upd_ms, step_ms = time_fused(opt, steps, warmup)
     upd_avg = statistics.mean(upd_ms)
@@ -399,6 +402,10 @@ def main() -> int:
                     help="step with FusedAdamW(capturable=True): torch's capturable op chain, "
                          "device step counts (the step-count increment runs before the timed "
                          "norm/update events)")
+    ap.add_argument("--clip-write-grads", action="store_true",
+                    help="FusedAdamW(clip_write_grads=True): the update also stores the clipped "
+                         "gradients back, as torch's clip_grad_norm_ does (+4 B per parameter; "
+                         "clip configurations only)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="after the timed steps, run 3 plain 1 GiB device copies (torch copy_) "
                          "so a counter run (rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE) sees a "
@@ -416,12 +423,18 @@ def main() -> int:
     log(f"[bench] {mi_adamw.version()} on {torch.cuda.get_device_name(0)}")
 
     names = list(CONFIGS) if args.config == "all" else [args.config]
+    if args.clip_write_grads:
+        names = [nm for nm in names if CONFIGS[nm][1]]
+        if not names:
+            print("--clip-write-grads needs a configuration with the clip", file=sys.stderr)
+            return 2
     if args.capturable:
         import warnings
         warnings.filterwarnings("ignore", message="This instance was constructed with capturable")
     results = [run_config(nm, args.steps, args.warmup, device,
                           with_context=not args.no_context and nm == names[0],
-                          capturable=args.capturable) for nm in names]
+                          capturable=args.capturable, write_grads=args.clip_write_grads)
+               for nm in names]
     if args.calibrate_copy:
         src = torch.ones(1 << 28, device=device)
         dst = torch.empty_like(src)
@@ -431,8 +444,9 @@ def main() -> int:
         del src, dst
     head = results[0]
     shape_name, clip, state, copy, flat, start_step, gstd = CONFIGS[head["config"]]
-    # the PMC figures in profiles/ are for the default chain's update kernel
-    traffic = None if args.capturable else load_traffic(head["config"])
+    # the PMC figures in profiles/ are for the default chain's update kernel, without
+    # the clipped-gradient store
+    traffic = None if args.capturable or args.clip_write_grads else load_traffic(head["config"])
     line = {
         "metric": METRIC,
         "value": round(head["gbs"], 2),
@@ -455,6 +469,7 @@ def main() -> int:
             "eps": HP["eps"], "weight_decay": HP["weight_decay"],
             "bytes_per_step": head["bytes_per_step"],
             **({"capturable": True} if args.capturable else {}),
+            **({"clip_write_grads": True} if args.clip_write_grads else {}),
         },
         "pct_of_peak": round(100 * head["gbs"] / PEAK_HBM_GBS, 2),
         "params_per_s": round(head["params_per_s"], 1),

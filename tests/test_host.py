@@ -456,3 +456,23 @@ def test_param_groups_from_generators_and_named_parameters():
         assert [id(p) for p in o.param_groups[0]["params"]] == [id(m.weight), id(m.bias)]
         if copy:
             assert o.bf16_param(m.weight).dtype == torch.bfloat16
+
+
+def test_bench_bytes_per_parameter():
+    """bench.py's algorithmic bytes per parameter, per configuration: p, g, m, v read and
+    p, m, v written once each (fp32 4 B, bf16 moments 2 B), +2 B for the bf16 copy,
+    +4 B for the norm pass's read of g, +4 B when the clipped g is stored back."""
+    import importlib.util
+    spec = importlib.util.spec_from_file_location("bench_under_test", os.path.join(ROOT, "bench.py"))
+    bench = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(bench)
+    expected = {"125m-step1": 28, "125m-clip": 32, "350m-master-clip-copy": 34,
+                "1.3b-bf16state-copy": 22, "1.3b-bf16state-copy-clip": 26,
+                "6.7b-flat-clip-copy": 34}
+    assert set(expected) == set(bench.CONFIGS)
+    for name, total in expected.items():
+        _, clip, state, copy, *_ = bench.CONFIGS[name]
+        step, update = bench.bytes_per_param(clip, state, copy)
+        assert step == total and update == total - (4 if clip else 0), name
+        step_w, update_w = bench.bytes_per_param(clip, state, copy, write_grads=True)
+        assert (step_w, update_w) == (step + 4, update + 4), name
