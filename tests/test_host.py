@@ -476,3 +476,22 @@ def test_bench_bytes_per_parameter():
         assert step == total and update == total - (4 if clip else 0), name
         step_w, update_w = bench.bytes_per_param(clip, state, copy, write_grads=True)
         assert (step_w, update_w) == (step + 4, update + 4), name
+
+
+def test_step_hooks_and_scheduler_see_step():
+    """step() is the Optimizer's hooked step: pre/post hooks run, and LambdaLR (main.py:178-180)
+    sees it called, so it raises no order warning.  No gradients: nothing reaches the GPU."""
+    import warnings
+    p = torch.nn.Parameter(torch.randn(4))
+    opt = mi_adamw.FusedAdamW([p], lr=6e-4, weight_decay=0.1, fused=False)
+    calls = []
+    opt.register_step_pre_hook(lambda o, a, k: calls.append("pre"))
+    opt.register_step_post_hook(lambda o, a, k: calls.append("post"))
+    sched = torch.optim.lr_scheduler.LambdaLR(opt, lambda it: min(1.0, it / 10))
+    assert opt.param_groups[0]["lr"] == 0.0
+    with warnings.catch_warnings():
+        warnings.simplefilter("error")
+        assert opt.step() is None
+        sched.step()
+    assert calls == ["pre", "post"]
+    assert opt.param_groups[0]["lr"] == pytest.approx(6e-5)
