@@ -8,7 +8,8 @@ iteration 0, main.py:36-43), zero_grad -> forward -> backward -> step.  The
 two runs see identical forward/backward kernels, so parameters, moments and
 losses must stay bit-identical step after step.  Also: param groups with
 different hyperparameters (decay / no-decay), more distinct hyperparameter
-sets than one launch holds, a tensor lr, clip write-back and complex params.
+sets than one launch holds, a tensor lr, clip write-back (in every update
+variant) and complex params.
 """
 from __future__ import annotations
 
@@ -178,6 +179,53 @@ def test_clip_write_grads_matches_clip_grad_norm(dev):
     torch.cuda.synchronize()
     assert max_ulp_all([p.grad for p in params], [q.grad for q in ours]) == 0
     assert max_ulp_all(params, ours) == 0
+
+
+@pytest.mark.parametrize("state_dtype,copy,flat,capt", [
+    (torch.bfloat16, True, False, False),
+    (torch.float32, True, True, False),
+    (torch.bfloat16, False, True, False),
+    (torch.float32, False, False, True),
+])
+def test_clip_write_grads_in_every_update_variant(dev, state_dtype, copy, flat, capt):
+    """The clipped-gradient store in the bf16-state, bf16-copy, flat and capturable
+    update variants, three chained steps: the stored gradients equal
+    clip_grads_with_norm_'s, and parameters, moments and copies equal those of the
+    same optimizer without the store (which the other tests pin to torch)."""
+    import warnings
+    import mi_adamw
+    shapes = [(4096,), (33, 17), (5,), (8192,)]
+    a = make_params(shapes, dev)
+    b = clone_params(a)
+    kw = dict(lr=3e-4, weight_decay=0.1, max_grad_norm=0.5, state_dtype=state_dtype,
+              bf16_copy=copy, flat_buffer=flat, capturable=capt)
+    with warnings.catch_warnings():
+        warnings.filterwarnings("ignore", message="This instance was constructed with capturable")
+        stored = mi_adamw.FusedAdamW(a, clip_write_grads=True, **kw)
+        plain = mi_adamw.FusedAdamW(b, **kw)
+        for step in range(1, 4):
+            grads = [torch.randn(s, device=dev, generator=gen(dev, 4000 + 10000 * step + i)) * 1e-1
+                     for i, s in enumerate(shapes)]
+            for p, q, g in zip(a, b, grads):
+                p.grad = g.clone()
+                q.grad = g.clone()
+            stored.step()
+            plain.step()
+            holders = [torch.nn.Parameter(torch.empty_like(g)) for g in grads]
+            for h, g in zip(holders, grads):
+                h.grad = g.clone()
+            torch.nn.utils.clip_grads_with_norm_(holders, 0.5, stored.last_grad_norm.clone())
+            torch.cuda.synchronize()
+            assert torch.equal(stored.last_grad_norm, plain.last_grad_norm)
+            assert max_ulp_all([p.grad for p in a], [h.grad for h in holders]) == 0, step
+            assert max_ulp_all([q.grad for q in b], grads) == 0, step   # no store: unchanged
+            assert max_ulp_all(a, b) == 0, step
+            for p, q in zip(a, b):
+                for key in ("exp_avg", "exp_avg_sq"):
+                    assert torch.equal(stored.state[p][key], plain.state[q][key]), (step, key)
+            if copy:
+                for x, y in zip(stored.bf16_params(), plain.bf16_params()):
+                    assert torch.equal(x, y), step
 
 
 def test_complex_params_follow_view_as_real(dev):
