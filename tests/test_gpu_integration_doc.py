@@ -1,4 +1,4 @@
-"""GPU: the ctypes stub that INTEGRATION.md gives a maintainer, run as written.
+"""GPU: the ctypes stub of the repository's integration guide, run as written.
 
 The stub binds libmi_adamw.so with ctypes alone (no mi_adamw package) and steps
 one flat range.  Its result must equal FusedAdamW's on the same tensors, bit for
