@@ -27,9 +27,12 @@ def _params():
     return [torch.nn.Parameter(torch.randn(10, 3)), torch.nn.Parameter(torch.randn(4))]
 
 
-def test_defaults_and_param_groups_match_torch():
-    ours = mi_adamw.FusedAdamW(_params(), lr=6e-4, weight_decay=0.1, fused=False)
-    ref = torch.optim.AdamW(_params(), lr=6e-4, weight_decay=0.1, fused=False)
+@pytest.mark.parametrize("fused", [False, True, None])
+def test_defaults_and_param_groups_match_torch(fused):
+    """main.py:177 passes fused=args.fused: either value builds the same defaults and
+    param_groups as torch's AdamW (the step is fused either way)."""
+    ours = mi_adamw.FusedAdamW(_params(), lr=6e-4, weight_decay=0.1, fused=fused)
+    ref = torch.optim.AdamW(_params(), lr=6e-4, weight_decay=0.1, fused=fused)
     assert ours.defaults == ref.defaults
     assert ours.param_groups[0].keys() == ref.param_groups[0].keys()
     for k in ref.param_groups[0]:
