@@ -1,0 +1,116 @@
+"""GPU: seeded random configurations of FusedAdamW against torch.optim.AdamW, bit for bit.
+
+Each seed draws a parameter set and an optimizer configuration the fixed-case tests
+cover one at a time, then runs a few chained steps of both optimizers on the same
+values:
+
+* 1-10 tensors, 1-D and 2-D, sizes around the 4-element vector width and the
+  4096-element chunk (1, 3, 31-33, 4095-4097, 65537 ...);
+* parameters and gradients that are views at 1-3 element offsets into a larger
+  buffer (not 16-byte aligned: the scalar path);
+* 1-3 param groups with their own lr (0 included), betas (the other lerp branch
+  included), eps, weight decay, maximize and amsgrad (adam.py:396-547);
+* the fused clip (clip_grad.py:50-183) or none, chunk sizes 4096-65536, the default
+  or the capturable chain (adam.py:480-527);
+* params that have no gradient at some steps (skipped, their step counts stay).
+
+torch's clip computes its norm in fp32; the reference applies our float64 norm with
+clip_grads_with_norm_ (torch's own scaling), so the update is compared bit for bit.
+"""
+from __future__ import annotations
+
+import random
+import warnings
+
+import pytest
+import torch
+
+from _helpers import max_ulp
+
+pytestmark = pytest.mark.gpu
+
+SIZES = [1, 3, 31, 32, 33, 1000, 4095, 4096, 4097, 8191, 12289, 65537]
+BETAS = [(0.9, 0.999), (0.9, 0.95), (0.5, 0.9), (0.2, 0.99)]
+
+
+@pytest.fixture(scope="module")
+def dev():
+    if not torch.cuda.is_available():
+        pytest.fail("GPU test run without a ROCm GPU")
+    return torch.device("cuda", 0)
+
+
+def _shape(rng: random.Random) -> tuple:
+    if rng.random() < 0.6:
+        return (rng.choice(SIZES),)
+    return (rng.choice([1, 3, 17, 64]), rng.choice([1, 5, 64, 129]))
+
+
+def _placed(values: torch.Tensor, offset: int) -> torch.Tensor:
+    """values copied into a fresh buffer at `offset` elements (a contiguous view)."""
+    if offset == 0:
+        return values.clone()
+    store = torch.zeros(values.numel() + offset + 7, device=values.device)
+    v = store[offset:offset + values.numel()].view(values.shape)
+    v.copy_(values)
+    return v
+
+
+@pytest.mark.parametrize("seed", range(24))
+def test_random_configuration_matches_torch(dev, seed):
+    import mi_adamw
+    rng = random.Random(seed)
+    g = torch.Generator(device=dev).manual_seed(seed)
+    shapes = [_shape(rng) for _ in range(rng.randint(1, 10))]
+    offsets = [rng.choice([0, 0, 0, 1, 2, 3]) for _ in shapes]
+    n_groups = rng.randint(1, min(3, len(shapes)))
+    group_of = [rng.randrange(n_groups) for _ in shapes]
+    hp = [dict(lr=rng.choice([0.0, 1e-4, 3e-4, 6e-4, 1e-2]), betas=rng.choice(BETAS),
+               eps=rng.choice([1e-8, 1e-6]), weight_decay=rng.choice([0.0, 0.01, 0.1]),
+               maximize=rng.random() < 0.3, amsgrad=rng.random() < 0.3)
+          for _ in range(n_groups)]
+    clip = rng.choice([None, None, 0.05, 1.0, 1e3])
+    chunk = rng.choice([4096, 8192, 65536])
+    capturable = rng.random() < 0.3
+    gstd = rng.choice([1e-4, 1e-2, 1.0])
+    print(f"seed {seed}: shapes {shapes} offsets {offsets} groups {group_of} {hp} clip {clip} "
+          f"chunk {chunk} capturable {capturable}", flush=True)
+
+    values = [torch.randn(s, device=dev, generator=g) * 0.02 for s in shapes]
+    ref = [torch.nn.Parameter(v.clone()) for v in values]
+    ours = [torch.nn.Parameter(_placed(v, o)) for v, o in zip(values, offsets)]
+
+    def groups(ps):
+        return [dict(params=[p for p, gi in zip(ps, group_of) if gi == k], **hp[k])
+                for k in range(n_groups) if k in group_of]
+
+    with warnings.catch_warnings():
+        warnings.filterwarnings("ignore", message="This instance was constructed with capturable")
+        topt = torch.optim.AdamW(groups(ref), foreach=False, capturable=capturable)
+        oopt = mi_adamw.FusedAdamW(groups(ours), capturable=capturable, max_grad_norm=clip,
+                                   chunk_elems=chunk)
+        for step in range(1, rng.randint(2, 5)):
+            for i, (p, q) in enumerate(zip(ref, ours)):
+                if step > 1 and rng.random() < 0.15:
+                    p.grad = None
+                    q.grad = None
+                    continue
+                grad = torch.randn(shapes[i], device=dev, generator=g) * gstd
+                p.grad = grad.clone()
+                q.grad = _placed(grad, offsets[i] if rng.random() < 0.5 else 0)
+            if all(p.grad is None for p in ref):
+                continue
+            oopt.step()
+            if clip is not None:
+                torch.nn.utils.clip_grads_with_norm_(ref, clip, oopt.last_grad_norm.clone())
+            topt.step()
+            torch.cuda.synchronize()
+            for i, (p, q) in enumerate(zip(ref, ours)):
+                assert max_ulp(p, q) == 0, (seed, step, i, "param")
+                ts, os_ = topt.state.get(p, {}), oopt.state.get(q, {})
+                assert ts.keys() == os_.keys(), (seed, step, i)
+                for key in ("exp_avg", "exp_avg_sq", "max_exp_avg_sq"):
+                    if key in ts:
+                        assert max_ulp(ts[key], os_[key]) == 0, (seed, step, i, key)
+                if "step" in ts:
+                    assert float(ts["step"]) == float(os_["step"]), (seed, step, i, "step")
