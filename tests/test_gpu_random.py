@@ -16,12 +16,15 @@ values:
 
 torch's clip computes its norm in fp32; the reference applies our float64 norm with
 clip_grads_with_norm_ (torch's own scaling), so the update is compared bit for bit.
+With bf16 moments and the bf16 copy, which torch has no counterpart for, the same kind
+of draws are checked against the oracle's bf16-state model instead.
 """
 from __future__ import annotations
 
 import random
 import warnings
 
+import numpy as np
 import pytest
 import torch
 
@@ -114,3 +117,99 @@ def test_random_configuration_matches_torch(dev, seed):
                         assert max_ulp(ts[key], os_[key]) == 0, (seed, step, i, key)
                 if "step" in ts:
                     assert float(ts["step"]) == float(os_["step"]), (seed, step, i, "step")
+
+
+def _torch_den(b1, b2, lr, eps, step, dev):
+    """torch's per-step values of the capturable chain (adam.py:480-522) as the same
+    0-d tensor ops on the GPU: (sqrt(bc2) * -step_size, eps / -step_size)."""
+    step_t = torch.tensor(float(step), device=dev)
+    bc1 = 1 - b1 ** step_t
+    bc2 = 1 - b2 ** step_t
+    neg = (lr / bc1).neg()
+    return float(bc2.sqrt() * neg), float(eps / neg)
+
+
+def _bits(t: torch.Tensor) -> np.ndarray:
+    return t.detach().view(torch.int16).cpu().numpy().view("uint16").reshape(-1).copy()
+
+
+@pytest.mark.parametrize("seed", range(12))
+def test_random_bf16_state_configuration_matches_oracle(dev, seed):
+    """bf16 moments (and amsgrad maximum) with the bf16 copy, which torch has no
+    counterpart for: every tensor after every step equals the oracle's bf16-state
+    model (default or capturable chain) applied to the tensor's values before the
+    step, with the clip coefficient from the step's own norm."""
+    import mi_adamw
+    from oracle import oracle as O
+    rng = random.Random(1000 + seed)
+    g = torch.Generator(device=dev).manual_seed(1000 + seed)
+    shapes = [_shape(rng) for _ in range(rng.randint(1, 8))]
+    offsets = [rng.choice([0, 0, 1, 2, 3]) for _ in shapes]
+    n_groups = rng.randint(1, min(3, len(shapes)))
+    group_of = [rng.randrange(n_groups) for _ in shapes]
+    hp = [dict(lr=rng.choice([0.0, 1e-4, 6e-4, 1e-2]), betas=rng.choice(BETAS),
+               eps=rng.choice([1e-8, 1e-6]), weight_decay=rng.choice([0.0, 0.1]),
+               maximize=rng.random() < 0.3, amsgrad=rng.random() < 0.3)
+          for _ in range(n_groups)]
+    clip = rng.choice([None, 0.05, 1e3])
+    chunk = rng.choice([4096, 8192, 65536])
+    capturable = rng.random() < 0.4
+    gstd = rng.choice([1e-4, 1e-2, 1.0])
+    print(f"seed {seed}: shapes {shapes} offsets {offsets} groups {group_of} {hp} clip {clip} "
+          f"chunk {chunk} capturable {capturable}", flush=True)
+    ours = [torch.nn.Parameter(_placed(torch.randn(s, device=dev, generator=g) * 0.02, o))
+            for s, o in zip(shapes, offsets)]
+    groups = [dict(params=[p for p, gi in zip(ours, group_of) if gi == k], **hp[k])
+              for k in range(n_groups) if k in group_of]
+    with warnings.catch_warnings():
+        warnings.filterwarnings("ignore", message="This instance was constructed with capturable")
+        opt = mi_adamw.FusedAdamW(groups, state_dtype=torch.bfloat16, bf16_copy=True,
+                                  capturable=capturable, max_grad_norm=clip, chunk_elems=chunk)
+        for step in range(1, rng.randint(2, 5)):
+            for i, q in enumerate(ours):
+                if step > 1 and rng.random() < 0.15:
+                    q.grad = None
+                    continue
+                grad = torch.randn(shapes[i], device=dev, generator=g) * gstd
+                q.grad = _placed(grad, offsets[i] if rng.random() < 0.5 else 0)
+            if all(q.grad is None for q in ours):
+                continue
+            before = []
+            for q in ours:
+                st = opt.state.get(q, {})
+                n = q.numel()
+                zero = np.zeros(n, dtype=np.uint16)
+                before.append((q.detach().cpu().numpy().reshape(-1).copy(),
+                               _bits(st["exp_avg"]) if "exp_avg" in st else zero.copy(),
+                               _bits(st["exp_avg_sq"]) if "exp_avg_sq" in st else zero.copy(),
+                               _bits(st["max_exp_avg_sq"]) if "max_exp_avg_sq" in st
+                               else zero.copy(),
+                               float(st["step"]) if "step" in st else 0.0))
+            opt.step()
+            torch.cuda.synchronize()
+            coef = None
+            if clip is not None:
+                coef = O.clip_coef(np.float32(opt.last_grad_norm.item()), clip)
+            for i, q in enumerate(ours):
+                if q.grad is None:
+                    continue
+                h = hp[group_of[i]]
+                p, mb, vb, xb, s0 = before[i]
+                gr = q.grad.detach().cpu().numpy().reshape(-1).copy()
+                kw = dict(lr=h["lr"], betas=h["betas"], eps=h["eps"],
+                          weight_decay=h["weight_decay"], step=s0 + 1, maximize=h["maximize"],
+                          grad_scale=coef, vmax_bits=xb if h["amsgrad"] else None)
+                if capturable:
+                    O.adamw_step_capt_bf16state(
+                        p, gr, mb, vb, den=_torch_den(*h["betas"], h["lr"], h["eps"], s0 + 1, dev),
+                        **kw)
+                else:
+                    O.adamw_step_bf16state(p, gr, mb, vb, **kw)
+                st = opt.state[q]
+                assert O.max_ulp(p, q.detach().cpu().numpy().reshape(-1))[0] == 0, (seed, step, i)
+                assert np.array_equal(mb, _bits(st["exp_avg"])), (seed, step, i, "m")
+                assert np.array_equal(vb, _bits(st["exp_avg_sq"])), (seed, step, i, "v")
+                if h["amsgrad"]:
+                    assert np.array_equal(xb, _bits(st["max_exp_avg_sq"])), (seed, step, i)
+                assert float(st["step"]) == s0 + 1
+                assert torch.equal(opt.bf16_param(q), q.detach().to(torch.bfloat16))
