@@ -213,3 +213,35 @@ def test_random_bf16_state_configuration_matches_oracle(dev, seed):
                     assert np.array_equal(xb, _bits(st["max_exp_avg_sq"])), (seed, step, i)
                 assert float(st["step"]) == s0 + 1
                 assert torch.equal(opt.bf16_param(q), q.detach().to(torch.bfloat16))
+
+
+@pytest.mark.parametrize("seed", range(8))
+def test_random_clip_grad_norm_matches_torch(dev, seed):
+    """mi_adamw.clip_grad_norm_ over random ragged and misaligned gradients: the norm
+    equals the float64 norm of the fp32 gradients (rounded to fp32) and is within 1e-6
+    of torch's fp32 norm; the scaled gradients equal clip_grads_with_norm_'s with that
+    norm, bit for bit."""
+    import mi_adamw
+    from oracle import oracle as O
+    rng = random.Random(2000 + seed)
+    g = torch.Generator(device=dev).manual_seed(2000 + seed)
+    shapes = [_shape(rng) for _ in range(rng.randint(1, 12))]
+    scale = rng.choice([1e-6, 1e-3, 1.0, 1e3])
+    max_norm = rng.choice([0.01, 1.0, 1e6])
+    grads = [torch.randn(s, device=dev, generator=g) * scale for s in shapes]
+    ours = [torch.nn.Parameter(torch.zeros(s, device=dev)) for s in shapes]
+    ref = [torch.nn.Parameter(torch.zeros(s, device=dev)) for s in shapes]
+    for q, p, gr in zip(ours, ref, grads):
+        q.grad = _placed(gr, rng.choice([0, 0, 1, 2, 3]))
+        p.grad = gr.clone()
+    exact = O.total_norm([gr.cpu().numpy() for gr in grads])
+    norm = mi_adamw.clip_grad_norm_(ours, max_norm)
+    tnorm = torch.nn.utils.get_total_norm([p.grad for p in ref])
+    torch.nn.utils.clip_grads_with_norm_(ref, max_norm, norm.clone())
+    torch.cuda.synchronize()
+    print(f"seed {seed}: {len(shapes)} tensors, scale {scale}, max_norm {max_norm}: norm "
+          f"{norm.item():.9g} float64 {float(exact):.9g} torch {tnorm.item():.9g}", flush=True)
+    assert np.float32(norm.item()) == exact
+    assert abs(norm.item() - tnorm.item()) <= 1e-6 * tnorm.item()
+    for q, p in zip(ours, ref):
+        assert max_ulp(q.grad, p.grad) == 0
