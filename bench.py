@@ -361,6 +361,9 @@ def run_config(name: str, steps: int, warmup: int, device, with_context: bool,
     total_b, upd_b = bytes_per_param(clip, state, copy, write_grads)
     log(f"[bench] {name}: {n} params in {n_tensors} tensors; timing {steps} steps")
     gpu_ms, wall_ms, norm_ms, upd_ms, step_ms = time_fused(opt, steps, warmup)
+    # after the timed region: the update's memory-only twin on the same tensors
+    from mi_adamw.probe import time_probe
+    probe_ms = time_probe(opt)
     upd_avg = statistics.mean(upd_ms)
     norm_avg = statistics.mean(norm_ms) if clip else 0.0
     step_bytes = total_b * n
@@ -373,11 +376,15 @@ def run_config(name: str, steps: int, warmup: int, device, with_context: bool,
         "update_kernel_ms_p90": _pct(upd_ms, 0.9),
         "step_ms_median": statistics.median(step_ms), "step_ms_p90": _pct(step_ms, 0.9),
         "update_bytes_per_launch": upd_b * n, "update_gbs": achieved_upd,
+        "probe_ms": probe_ms,
+        "probe_gbs": None if probe_ms is None else upd_b * n / probe_ms / 1e6,
         "dtype": "f32" if state == "fp32" else "f32 math, bf16 moments",
     }
     log(f"[bench] {name}: {gpu_ms:.4f} ms/step, {res['gbs']:.1f} GB/s "
         f"({100 * res['gbs'] / PEAK_HBM_GBS:.1f}% of peak); update {upd_avg:.4f} ms "
-        f"({achieved_upd:.1f} GB/s), norm {norm_avg:.4f} ms")
+        f"({achieved_upd:.1f} GB/s), norm {norm_avg:.4f} ms"
+        + ("" if probe_ms is None else
+           f"; memory-only probe {probe_ms:.4f} ms ({res['probe_gbs']:.1f} GB/s)"))
     del params, opt
     torch.cuda.empty_cache()
     if with_context:
@@ -487,6 +494,13 @@ def main() -> int:
             "traffic": traffic,
             "kernel": "mi_adamw_update_kernel",
             "bytes_per_launch": head["update_bytes_per_launch"],
+            # the same launch with the arithmetic left out, on the same tensors, right
+            # after the timed region: the bandwidth this read/write mix gets here
+            "mix_probe": None if head["probe_ms"] is None else {
+                "achieved": round(head["probe_gbs"], 2),
+                "frac": round(head["probe_gbs"] / PEAK_HBM_GBS, 4),
+                "update_vs_probe": round(head["update_gbs"] / head["probe_gbs"], 4),
+            },
         },
     }
     if "torch_gpu" in head:

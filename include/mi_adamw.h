@@ -40,7 +40,7 @@
 extern "C" {
 #endif
 
-#define MI_ADAMW_ABI_VERSION 4
+#define MI_ADAMW_ABI_VERSION 5
 #define MI_ADAMW_MAX_HYPER 16      /* hyperparameter sets per launch */
 #define MI_ADAMW_MAX_NORM_BLOCKS 4096 /* partial sums per grad-norm launch */
 
@@ -215,6 +215,21 @@ int mi_adamw_step_capturable(const mi_adamw_tensor *d_tensors, const mi_adamw_ch
                              const float *d_steps, const int32_t *d_step_index,
                              const float *d_grad_scale, int32_t state_dtype, int32_t flags,
                              int32_t max_blocks, void *stream);
+
+/* Measurement helper with no counterpart in the reference, for benchmarks that want
+ * the memory ceiling of the update on the tensors it actually runs on: the same
+ * launch as mi_adamw_step / mi_adamw_step_flat (tables or one flat range, launch
+ * shape, access widths, cache hints, software pipelining) with the arithmetic left
+ * out.  Every loaded value is stored back unchanged and the bf16 copy is written as
+ * the bf16 of its master (equal to what the step leaves there), so the bytes moved
+ * are exactly the step's and the tensors keep their values.  MI_ADAMW_F_CLIP is
+ * accepted and ignored (the gradient is read either way); the other flags select
+ * the same streams as in the step. */
+int mi_adamw_probe(const mi_adamw_tensor *d_tensors, const mi_adamw_chunk *d_chunks,
+                   int64_t n_chunks, int64_t chunk_elems, int32_t state_dtype, int32_t flags,
+                   int32_t max_blocks, void *stream);
+int mi_adamw_probe_flat(const mi_adamw_tensor *t, int64_t chunk_elems, int32_t state_dtype,
+                        int32_t flags, int32_t max_blocks, void *stream);
 
 #ifdef __cplusplus
 }

@@ -16,7 +16,7 @@ import torch
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libmi_adamw.so")
 
-ABI_VERSION = 4
+ABI_VERSION = 5
 MAX_HYPER = 16
 MAX_NORM_BLOCKS = 4096
 CHUNK_QUANTUM = 4096
@@ -51,6 +51,8 @@ EXPORTS = (
     "mi_adamw_step_flat",
     "mi_adamw_step_capturable",
     "mi_adamw_widen_bf16",
+    "mi_adamw_probe",
+    "mi_adamw_probe_flat",
 )
 
 
@@ -131,6 +133,8 @@ _SIGNATURES = {
     "mi_adamw_step_capturable": ([_vp, _vp, _i64, _i64, _vp, _i32, _vp, _vp, _vp, _i32, _i32,
                                   _i32, _vp], ctypes.c_int),
     "mi_adamw_widen_bf16": ([_vp, _vp, _i64, _i64, _vp], ctypes.c_int),
+    "mi_adamw_probe": ([_vp, _vp, _i64, _i64, _i32, _i32, _i32, _vp], ctypes.c_int),
+    "mi_adamw_probe_flat": ([_vp, _i64, _i32, _i32, _i32, _vp], ctypes.c_int),
 }
 
 _lib = None

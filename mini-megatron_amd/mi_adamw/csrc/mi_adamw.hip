@@ -18,6 +18,8 @@
 //   mi_adamw_scale_kernel  g *= coef in place (clip_grad_norm_'s write-back).
 //   mi_adamw_widen_kernel  bf16 -> fp32 of many tensors in one launch (the backward of
 //                          the bf16 weight copies the forward runs on), exact.
+//   mi_adamw_update_kernel<..., ProbeHyper, ...>  the update's memory traffic without its
+//                          arithmetic, values stored back unchanged (a measurement twin).
 //
 // Every launch walks a chunk table (one entry per `chunk_elems` slice of a
 // tensor) so that all parameter tensors go through one launch, or one
@@ -282,6 +284,7 @@ struct FlatSource {
 // Default chain: the host formed every per-step value (adam.py:529-536).
 struct StaticHyper {
     static constexpr bool kCapt = false;
+    static constexpr bool kProbe = false;
     HyperPack hp;
     __device__ __forceinline__ ElemScalars get(const mi_adamw_tensor& t, int32_t) const {
         const mi_adamw_hyper& x = hp.h[t.hyper];
@@ -302,6 +305,7 @@ struct CaptPack {
 // space (scalar loads).
 struct CaptHyper {
     static constexpr bool kCapt = true;
+    static constexpr bool kProbe = false;
     CaptPack cp;
     const float* steps;
     const int32_t* step_index;
@@ -334,6 +338,25 @@ struct CaptHyper {
         return h;
     }
 };
+
+// Memory-only twin of the update, for measurement (mi_adamw_probe): the same
+// loads and stores, launch shape and cache hints, with the arithmetic left out.
+// Every value is stored back as it was read (the bf16 copy as the bf16 of the
+// master, which the step keeps it equal to), so running it leaves the tensors
+// unchanged.
+struct ProbeHyper {
+    static constexpr bool kCapt = false;
+    static constexpr bool kProbe = true;
+    __device__ __forceinline__ ElemScalars get(const mi_adamw_tensor&, int32_t) const {
+        return ElemScalars{};
+    }
+};
+
+// Keeps a loaded value live without using it, so its load stays in the code.
+__device__ __forceinline__ void keep(f32x4 v) {
+    asm volatile("" ::"v"(v.x), "v"(v.y), "v"(v.z), "v"(v.w));
+}
+__device__ __forceinline__ void keep(float v) { asm volatile("" ::"v"(v)); }
 
 // ---------------------------------------------------------------------------
 // Reductions
@@ -508,6 +531,7 @@ __global__ __launch_bounds__(kUpdThreads) void mi_adamw_update_kernel(
     using IO = StateIO<StateT>;
     using T = Tile<StateT, kAms>;
     constexpr bool kCapt = HS::kCapt;
+    constexpr bool kProbe = HS::kProbe;
     const float scale = kClip ? *grad_scale : 1.0f;
     for (int64_t c = blockIdx.x; c < n_chunks; c += gridDim.x) {
         mi_adamw_tensor t;
@@ -546,8 +570,12 @@ __global__ __launch_bounds__(kUpdThreads) void mi_adamw_update_kernel(
                     f32x4 gs = cur.g;
                     if (kClip) gs = f32x4{gs.x * scale, gs.y * scale, gs.z * scale, gs.w * scale};
                     if (kWriteGrad) st4(G + i, gs);
-                    gs = f32x4{gs.x * gmul, gs.y * gmul, gs.z * gmul, gs.w * gmul};
-                    adamw_vec<kAms, kCapt>(cur.p, gs, cur.m, cur.v, cur.x, h);
+                    if (kProbe) {
+                        keep(gs);
+                    } else {
+                        gs = f32x4{gs.x * gmul, gs.y * gmul, gs.z * gmul, gs.w * gmul};
+                        adamw_vec<kAms, kCapt>(cur.p, gs, cur.m, cur.v, cur.x, h);
+                    }
                     st4(P + i, cur.p);
                     IO::st(M, i, cur.m);
                     IO::st(V, i, cur.v);
@@ -570,7 +598,10 @@ __global__ __launch_bounds__(kUpdThreads) void mi_adamw_update_kernel(
             g1 = g1 * gmul;
             float p1 = ld1(P + j), m1 = IO::ld1(M, j), v1 = IO::ld1(V, j);
             float x1 = kAms ? IO::ld1(X, j) : 0.0f;
-            adamw_elem<kAms, kCapt>(p1, g1, m1, v1, x1, h);
+            if (kProbe)
+                keep(g1);
+            else
+                adamw_elem<kAms, kCapt>(p1, g1, m1, v1, x1, h);
             st1(P + j, p1);
             IO::st1(M, j, m1);
             IO::st1(V, j, v1);
@@ -737,6 +768,25 @@ int launch_update(const Src& src, int64_t n_chunks, int64_t chunk_elems, const H
                                                               scale, flags, grid, s);
 }
 
+// The memory-only twin of launch_update (no clip: the gradient is read either way).
+template <class Src>
+int launch_probe(const Src& src, int64_t n_chunks, int64_t chunk_elems, int32_t state_dtype,
+                 int32_t flags, int32_t max_blocks, hipStream_t s) {
+    if (n_chunks <= 0 || !chunk_elems_ok(chunk_elems)) return MI_ADAMW_E_INVALID;
+    if (state_dtype != MI_ADAMW_STATE_F32 && state_dtype != MI_ADAMW_STATE_BF16)
+        return MI_ADAMW_E_INVALID;
+    flags &= ~MI_ADAMW_F_CLIP;
+    if (flags & ~(MI_ADAMW_F_BF16_COPY | MI_ADAMW_F_WRITE_GRAD | MI_ADAMW_F_AMSGRAD))
+        return MI_ADAMW_E_INVALID;
+    const unsigned grid = grid_for(n_chunks, max_blocks, kUpdThreads);
+    const ProbeHyper hs;
+    if (state_dtype == MI_ADAMW_STATE_F32)
+        return launch_update_cw<Src, ProbeHyper, float, false>(src, n_chunks, chunk_elems, hs,
+                                                               nullptr, flags, grid, s);
+    return launch_update_cw<Src, ProbeHyper, uint16_t, false>(src, n_chunks, chunk_elems, hs,
+                                                              nullptr, flags, grid, s);
+}
+
 // Validate one host-visible tensor descriptor for the flat entry points.
 int check_flat(const mi_adamw_tensor* t, int32_t state_dtype, int32_t flags) {
     if (!t || t->numel <= 0 || !t->param || !t->grad || !t->exp_avg || !t->exp_avg_sq)
@@ -762,8 +812,8 @@ int check_flat(const mi_adamw_tensor* t, int32_t state_dtype, int32_t flags) {
 extern "C" {
 
 const char* mi_adamw_version(void) {
-    return "mi_adamw 4 gfx950 fused clip+adamw (fp32/bf16 state, bf16 copy, amsgrad, flat, "
-           "capturable, bf16 widen)";
+    return "mi_adamw 5 gfx950 fused clip+adamw (fp32/bf16 state, bf16 copy, amsgrad, flat, "
+           "capturable, bf16 widen, memory probe)";
 }
 
 const char* mi_adamw_strerror(int code) {
@@ -892,6 +942,28 @@ int mi_adamw_step_capturable(const mi_adamw_tensor* d_tensors, const mi_adamw_ch
     TableSource src{d_tensors, d_chunks};
     return launch_update(src, n_chunks, chunk_elems, hs, d_grad_scale, state_dtype, flags,
                          max_blocks, static_cast<hipStream_t>(stream));
+}
+
+int mi_adamw_probe(const mi_adamw_tensor* d_tensors, const mi_adamw_chunk* d_chunks,
+                   int64_t n_chunks, int64_t chunk_elems, int32_t state_dtype, int32_t flags,
+                   int32_t max_blocks, void* stream) {
+    if (!d_tensors || !d_chunks) return MI_ADAMW_E_INVALID;
+    TableSource src{d_tensors, d_chunks};
+    return launch_probe(src, n_chunks, chunk_elems, state_dtype, flags, max_blocks,
+                        static_cast<hipStream_t>(stream));
+}
+
+int mi_adamw_probe_flat(const mi_adamw_tensor* t, int64_t chunk_elems, int32_t state_dtype,
+                        int32_t flags, int32_t max_blocks, void* stream) {
+    if (!chunk_elems_ok(chunk_elems)) return MI_ADAMW_E_INVALID;
+    int rc = check_flat(t, state_dtype, flags);
+    if (rc != MI_ADAMW_OK) return rc;
+    FlatSource src;
+    src.t = *t;
+    src.t.hyper = 0;
+    const int64_t n_chunks = (t->numel + chunk_elems - 1) / chunk_elems;
+    return launch_probe(src, n_chunks, chunk_elems, state_dtype, flags, max_blocks,
+                        static_cast<hipStream_t>(stream));
 }
 
 }  // extern "C"

@@ -179,6 +179,16 @@ static int cpu_checks(void)
           "widen with no chunks");
     CHECK(mi_adamw_widen_bf16(fake, fake, 1, 1000, NULL) == MI_ADAMW_E_INVALID,
           "widen chunk size");
+    CHECK(mi_adamw_probe(NULL, fake, 1, 4096, MI_ADAMW_STATE_F32, 0, 0, NULL) ==
+              MI_ADAMW_E_INVALID, "probe without tensors");
+    CHECK(mi_adamw_probe(fake, fake, 1, 4096, 7, 0, 0, NULL) == MI_ADAMW_E_INVALID,
+          "probe state dtype");
+    CHECK(mi_adamw_probe(fake, fake, 1, 4096, MI_ADAMW_STATE_F32, 1 << 9, 0, NULL) ==
+              MI_ADAMW_E_INVALID, "probe unknown flag");
+    CHECK(mi_adamw_probe_flat(NULL, 4096, MI_ADAMW_STATE_F32, 0, 0, NULL) == MI_ADAMW_E_INVALID,
+          "flat probe without a range");
+    CHECK(mi_adamw_probe_flat(&t, 1000, MI_ADAMW_STATE_F32, 0, 0, NULL) == MI_ADAMW_E_INVALID,
+          "flat probe chunk size");
     printf("abi_check cpu: ok (%s)\n", mi_adamw_version());
     return 0;
 }
