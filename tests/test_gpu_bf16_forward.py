@@ -59,6 +59,37 @@ def test_training_on_bf16_copies_is_bit_identical(dev, flat):
         print(f"iteration {it}: loss {la.item():.6f} identical", flush=True)
 
 
+@pytest.mark.parametrize("flat", [False, True])
+def test_gradient_accumulation_over_micro_batches_is_bit_identical(dev, flat):
+    """Several forward/backward passes per step, as a pipeline schedule's micro-batches
+    run them (parallel/pipeline_parallel.py): each backward's widened gradients add
+    into the masters' .grad exactly as the cast's do under plain autocast."""
+    a = refgpt.tiny(dev, seed=12)
+    b = refgpt.tiny(dev, seed=12)
+    hp = dict(lr=1e-3, weight_decay=0.1, bf16_copy=True, flat_buffer=flat)
+    oa = mi_adamw.FusedAdamW(a.parameters(), **hp)
+    ob = mi_adamw.FusedAdamW(b.parameters(), **hp)
+    for it in range(3):
+        oa.zero_grad()
+        ob.zero_grad()
+        for mb in range(3):
+            ids, labels, mask = refgpt.batch(dev, seed=200 + 10 * it + mb)
+            with torch.autocast("cuda", dtype=torch.bfloat16):
+                _, la = a(ids, labels, mask)
+            (la / 3).backward()
+            with torch.autocast("cuda", dtype=torch.bfloat16), mi_adamw.bf16_weights(ob, b):
+                _, lb = b(ids, labels, mask)
+            (lb / 3).backward()
+            assert _bits_equal(la.detach(), lb.detach()), (it, mb)
+        for p, q in zip(a.parameters(), b.parameters()):
+            assert _bits_equal(p.grad, q.grad), it
+        oa.step()
+        ob.step()
+        torch.cuda.synchronize()
+        for p, q in zip(a.parameters(), b.parameters()):
+            assert _bits_equal(p.detach(), q.detach()), it
+
+
 def test_weight_casts_disappear_on_the_gpu(dev):
     model = refgpt.tiny(dev)
     opt = mi_adamw.FusedAdamW(model.parameters(), bf16_copy=True)
