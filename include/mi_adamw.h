@@ -40,7 +40,7 @@
 extern "C" {
 #endif
 
-#define MI_ADAMW_ABI_VERSION 5
+#define MI_ADAMW_ABI_VERSION 6
 #define MI_ADAMW_MAX_HYPER 16      /* hyperparameter sets per launch */
 #define MI_ADAMW_MAX_NORM_BLOCKS 4096 /* partial sums per grad-norm launch */
 
@@ -48,6 +48,7 @@ extern "C" {
 #define MI_ADAMW_OK 0
 #define MI_ADAMW_E_INVALID (-1)    /* a size, count or pointer argument is out of range */
 #define MI_ADAMW_E_ALIGN (-2)      /* a tensor flagged aligned has a misaligned pointer */
+#define MI_ADAMW_E_SCRATCH (-3)    /* a no-alloc launch needs more than the static scratch holds */
 
 /* Storage dtype of exp_avg / exp_avg_sq. */
 #define MI_ADAMW_STATE_F32 0
@@ -162,6 +163,27 @@ int mi_adamw_grad_norm(const mi_adamw_tensor *d_tensors, const mi_adamw_chunk *d
 /* Same over one contiguous fp32 gradient range of n elements. */
 int mi_adamw_grad_norm_flat(const float *d_grad, int64_t n, int64_t chunk_elems, float max_norm,
                             double *d_partials, float *d_norm, float *d_coef, void *stream);
+
+/* Bytes of device scratch that mi_adamw_grad_norm_flat_noalloc uses on each GPU: one
+ * float64 partial sum per workgroup of the norm pass, which never runs more than 512. */
+#define MI_ADAMW_NOALLOC_SCRATCH_BYTES 4096
+
+/* mi_adamw_grad_norm_flat without the d_partials workspace: allocates nothing, and
+ * calls no hipMalloc, hipFree or allocating library routine.  No counterpart in the
+ * reference: it is for callers that cannot allocate device memory (code under HIP
+ * graph capture, tight serving loops, harnesses that forbid hipMalloc).  Same
+ * results as mi_adamw_grad_norm_flat, bit for bit.
+ * The partial sums live in a static device array of MI_ADAMW_NOALLOC_SCRATCH_BYTES
+ * that the library holds on every GPU it runs on until the process ends; its device
+ * address is looked up on the first call on each device.  Every call on one GPU
+ * shares that array: calls that may overlap on one GPU (on different streams) race
+ * and must be ordered by the caller.  Each call writes every partial it reads, so
+ * nothing needs clearing between calls.  Any n is accepted (the pass runs at most
+ * 512 workgroups); a launch needing more partials than the scratch holds would
+ * return MI_ADAMW_E_SCRATCH.  The stream must belong to the current device
+ * (MI_ADAMW_E_INVALID otherwise). */
+int mi_adamw_grad_norm_flat_noalloc(const float *d_grad, int64_t n, int64_t chunk_elems,
+                                    float max_norm, float *d_norm, float *d_coef, void *stream);
 
 /* Multiply every gradient of the tables by *d_coef in place.
  * Replaces clip_grad.py:170-183 (_clip_grads_with_norm_'s foreach mul). */

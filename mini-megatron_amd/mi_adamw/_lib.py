@@ -16,14 +16,16 @@ import torch
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libmi_adamw.so")
 
-ABI_VERSION = 5
+ABI_VERSION = 6
 MAX_HYPER = 16
 MAX_NORM_BLOCKS = 4096
+NOALLOC_SCRATCH_BYTES = 4096
 CHUNK_QUANTUM = 4096
 
 OK = 0
 E_INVALID = -1
 E_ALIGN = -2
+E_SCRATCH = -3
 
 STATE_F32 = 0
 STATE_BF16 = 1
@@ -46,6 +48,7 @@ EXPORTS = (
     "mi_adamw_build_chunks",
     "mi_adamw_grad_norm",
     "mi_adamw_grad_norm_flat",
+    "mi_adamw_grad_norm_flat_noalloc",
     "mi_adamw_scale_grads",
     "mi_adamw_step",
     "mi_adamw_step_flat",
@@ -127,6 +130,7 @@ _SIGNATURES = {
     "mi_adamw_build_chunks": ([_vp, _i32, _i64, _vp, _i64], _i64),
     "mi_adamw_grad_norm": ([_vp, _vp, _i64, _i64, _f32, _vp, _vp, _vp, _vp], ctypes.c_int),
     "mi_adamw_grad_norm_flat": ([_vp, _i64, _i64, _f32, _vp, _vp, _vp, _vp], ctypes.c_int),
+    "mi_adamw_grad_norm_flat_noalloc": ([_vp, _i64, _i64, _f32, _vp, _vp, _vp], ctypes.c_int),
     "mi_adamw_scale_grads": ([_vp, _vp, _i64, _i64, _vp, _vp], ctypes.c_int),
     "mi_adamw_step": ([_vp, _vp, _i64, _i64, _vp, _i32, _vp, _i32, _i32, _i32, _vp], ctypes.c_int),
     "mi_adamw_step_flat": ([_vp, _vp, _vp, _i64, _i32, _i32, _i32, _vp], ctypes.c_int),

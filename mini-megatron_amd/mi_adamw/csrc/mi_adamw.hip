@@ -35,6 +35,9 @@
 #include <stddef.h>
 #include <string.h>
 
+#include <atomic>
+#include <mutex>
+
 #include "mi_adamw.h"
 
 namespace {
@@ -693,12 +696,15 @@ unsigned grid_for(int64_t n_chunks, int32_t max_blocks, int threads) {
 
 bool aligned(const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0; }
 
+// partials_cap: doubles available at `partials` (one per workgroup of the pass).
 template <class Src>
 int launch_norm(const Src& src, int64_t n_chunks, int64_t chunk_elems, float max_norm,
-                double* partials, float* norm, float* coef, hipStream_t s) {
+                double* partials, float* norm, float* coef, hipStream_t s,
+                int64_t partials_cap = MI_ADAMW_MAX_NORM_BLOCKS) {
     if (n_chunks <= 0 || !chunk_elems_ok(chunk_elems) || !partials || !norm || !coef)
         return MI_ADAMW_E_INVALID;
     const unsigned grid = grid_for(n_chunks, kNormBlocks, kNormThreads);
+    if (grid > partials_cap) return MI_ADAMW_E_SCRATCH;
     const int64_t keep_chunks = kNormKeepBytes / (chunk_elems * static_cast<int64_t>(sizeof(float)));
     const int64_t keep_from = n_chunks > keep_chunks ? n_chunks - keep_chunks : 0;
     hipLaunchKernelGGL(mi_adamw_sumsq_kernel<Src>, dim3(grid), dim3(kNormThreads), 0, s, src,
@@ -807,19 +813,71 @@ int check_flat(const mi_adamw_tensor* t, int32_t state_dtype, int32_t flags) {
 }  // namespace
 
 // ---------------------------------------------------------------------------
+// Library-owned scratch of mi_adamw_grad_norm_flat_noalloc: the norm pass's partial
+// sums, one float64 per workgroup.  Each GPU holds its own copy from module load until
+// the process ends.  Host code never names the array in a launch or a copy: it looks
+// up each device's address once (scratch_on) and passes that pointer.
+
+constexpr int kScratchDoubles = MI_ADAMW_NOALLOC_SCRATCH_BYTES / sizeof(double);
+static_assert(kScratchDoubles >= kNormBlocks, "the scratch holds one partial per norm workgroup");
+
+static __device__ __align__(256) double scratch[kScratchDoubles];
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::atomic<double*> g_scratch_ptr[kMaxDevices];
+std::mutex g_scratch_mu;
+
+// The device address of `scratch` on the stream's device, looked up on that device's
+// first call (with the device current) and kept.  The stream must belong to the current
+// device; the null stream is the current device's.
+int scratch_on(hipStream_t s, double** out) {
+    int dev = -1;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return static_cast<int>(e);
+    if (s) {
+        hipDevice_t sdev = -1;
+        e = hipStreamGetDevice(s, &sdev);
+        if (e != hipSuccess) return static_cast<int>(e);
+        if (sdev != dev) return MI_ADAMW_E_INVALID;
+    }
+    if (dev < 0 || dev >= kMaxDevices) return MI_ADAMW_E_INVALID;
+    double* p = g_scratch_ptr[dev].load(std::memory_order_acquire);
+    if (!p) {
+        std::lock_guard<std::mutex> lock(g_scratch_mu);
+        p = g_scratch_ptr[dev].load(std::memory_order_relaxed);
+        if (!p) {
+            void* addr = nullptr;
+            e = hipGetSymbolAddress(&addr, HIP_SYMBOL(scratch));
+            if (e != hipSuccess) return static_cast<int>(e);
+            if (!addr) return MI_ADAMW_E_INVALID;
+            p = static_cast<double*>(addr);
+            g_scratch_ptr[dev].store(p, std::memory_order_release);
+        }
+    }
+    *out = p;
+    return MI_ADAMW_OK;
+}
+
+}  // namespace
+
+// ---------------------------------------------------------------------------
 // C ABI
 
 extern "C" {
 
 const char* mi_adamw_version(void) {
-    return "mi_adamw 5 gfx950 fused clip+adamw (fp32/bf16 state, bf16 copy, amsgrad, flat, "
-           "capturable, bf16 widen, memory probe)";
+    return "mi_adamw 6 gfx950 fused clip+adamw (fp32/bf16 state, bf16 copy, amsgrad, flat, "
+           "capturable, bf16 widen, memory probe, no-alloc norm)";
 }
 
 const char* mi_adamw_strerror(int code) {
     if (code == MI_ADAMW_OK) return "success";
     if (code == MI_ADAMW_E_INVALID) return "mi_adamw: invalid argument (size, count or pointer)";
     if (code == MI_ADAMW_E_ALIGN) return "mi_adamw: pointer not aligned for the vector path";
+    if (code == MI_ADAMW_E_SCRATCH)
+        return "mi_adamw: the launch needs more partial sums than the library's static scratch holds";
     if (code > 0) return hipGetErrorString(static_cast<hipError_t>(code));
     return "mi_adamw: unknown error";
 }
@@ -863,6 +921,24 @@ int mi_adamw_grad_norm_flat(const float* d_grad, int64_t n, int64_t chunk_elems,
     const int64_t n_chunks = (n + chunk_elems - 1) / chunk_elems;
     return launch_norm(src, n_chunks, chunk_elems, max_norm, d_partials, d_norm, d_coef,
                        static_cast<hipStream_t>(stream));
+}
+
+int mi_adamw_grad_norm_flat_noalloc(const float* d_grad, int64_t n, int64_t chunk_elems,
+                                    float max_norm, float* d_norm, float* d_coef, void* stream) {
+    if (!d_grad || n <= 0 || !chunk_elems_ok(chunk_elems) || !d_norm || !d_coef)
+        return MI_ADAMW_E_INVALID;
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    double* partials = nullptr;
+    const int rc = scratch_on(s, &partials);
+    if (rc != MI_ADAMW_OK) return rc;
+    FlatSource src;
+    memset(&src.t, 0, sizeof(src.t));
+    src.t.grad = const_cast<float*>(d_grad);
+    src.t.numel = n;
+    src.t.flags = aligned(d_grad, 16) ? MI_ADAMW_T_VEC : 0;
+    const int64_t n_chunks = (n + chunk_elems - 1) / chunk_elems;
+    return launch_norm(src, n_chunks, chunk_elems, max_norm, partials, d_norm, d_coef, s,
+                       kScratchDoubles);
 }
 
 int mi_adamw_scale_grads(const mi_adamw_tensor* d_tensors, const mi_adamw_chunk* d_chunks,
