@@ -40,7 +40,7 @@
 extern "C" {
 #endif
 
-#define MI_ADAMW_ABI_VERSION 6
+#define MI_ADAMW_ABI_VERSION 7
 #define MI_ADAMW_MAX_HYPER 16      /* hyperparameter sets per launch */
 #define MI_ADAMW_MAX_NORM_BLOCKS 4096 /* partial sums per grad-norm launch */
 
@@ -185,6 +185,45 @@ int mi_adamw_grad_norm_flat(const float *d_grad, int64_t n, int64_t chunk_elems,
 int mi_adamw_grad_norm_flat_noalloc(const float *d_grad, int64_t n, int64_t chunk_elems,
                                     float max_norm, float *d_norm, float *d_coef, void *stream);
 
+/* The clip split at the all-reduce, for ZeRO-1 range sharding (the flat layout cut into
+ * one contiguous range per data-parallel rank).  Each rank sums the squares of its own
+ * range's gradients into one float64 (8 bytes); the ranks' sums are all-reduced (or, on
+ * one GPU, gathered) and every rank forms the same norm and coefficient from them.  This
+ * replaces the per-tensor all-reduce + div_(world) of parallel/data_parallel.py:14-15
+ * followed by clip_grad.py:50-117 and :165-169, with the world-size division folded in
+ * as a gradient pre-scale.
+ *
+ * grad_prescale: every gradient is first multiplied by this fp32 factor, rounding once,
+ * which is what `grad.div_(world)` stores on the GPU (torch divides a tensor by a host
+ * scalar as a multiply by f32(1 / world)); 1 leaves the gradients as they are.
+ *
+ * mi_adamw_grad_sumsq / _flat: *d_sumsq <- float64 sum of (grad_prescale * g)^2 over the
+ * tables' chunks or the range, reduced from MI_ADAMW_MAX_NORM_BLOCKS doubles of scratch at
+ * d_partials in a fixed order (bitwise reproducible).
+ * mi_adamw_norm_from_sumsq: d_sumsq[0..n) summed in a fixed order (1 <= n <=
+ * MI_ADAMW_MAX_NORM_BLOCKS), then the norm and coefficient exactly as mi_adamw_grad_norm
+ * forms them.  With n == 1 and the sum of one range, the result equals mi_adamw_grad_norm
+ * over that range bit for bit. */
+int mi_adamw_grad_sumsq(const mi_adamw_tensor *d_tensors, const mi_adamw_chunk *d_chunks,
+                        int64_t n_chunks, int64_t chunk_elems, float grad_prescale,
+                        double *d_partials, double *d_sumsq, void *stream);
+int mi_adamw_grad_sumsq_flat(const float *d_grad, int64_t n, int64_t chunk_elems,
+                             float grad_prescale, double *d_partials, double *d_sumsq,
+                             void *stream);
+int mi_adamw_norm_from_sumsq(const double *d_sumsq, int32_t n, float max_norm, float *d_norm,
+                             float *d_coef, void *stream);
+
+/* New gradient pointers for rows of a device tensor table of n_rows rows: row rows[i]
+ * gets grads[i], and its MI_ADAMW_T_VEC flag set if vec[i] is non-zero, cleared if not
+ * (the caller sets vec[i] when every pointer of the row, the new gradient included, is
+ * aligned for the vector path).  For the step after zero_grad() freed the gradients and
+ * backward allocated new ones (main.py:204-209): only the gradient column of the table
+ * changes.  rows, grads and vec are host arrays of n entries, carried to the device as
+ * kernel arguments, so they may be reused as soon as the call returns.  Ordered on the
+ * stream like every other call: launches queued earlier on it still see the old rows. */
+int mi_adamw_set_grads(mi_adamw_tensor *d_tensors, int32_t n_rows, int32_t n, const int32_t *rows,
+                       const uint64_t *grads, const uint8_t *vec, void *stream);
+
 /* Multiply every gradient of the tables by *d_coef in place.
  * Replaces clip_grad.py:170-183 (_clip_grads_with_norm_'s foreach mul). */
 int mi_adamw_scale_grads(const mi_adamw_tensor *d_tensors, const mi_adamw_chunk *d_chunks,
@@ -222,6 +261,22 @@ int mi_adamw_step(const mi_adamw_tensor *d_tensors, const mi_adamw_chunk *d_chun
 int mi_adamw_step_flat(const mi_adamw_tensor *t, const mi_adamw_hyper *hyper,
                        const float *d_grad_scale, int64_t chunk_elems, int32_t state_dtype,
                        int32_t flags, int32_t max_blocks, void *stream);
+
+/* mi_adamw_step and mi_adamw_step_flat with the gradient pre-scale of
+ * mi_adamw_grad_sumsq: every gradient is multiplied by grad_prescale (one fp32 rounding),
+ * then by *d_grad_scale with MI_ADAMW_F_CLIP, as torch's div_(world), clip and AdamW do in
+ * turn.  With MI_ADAMW_F_WRITE_GRAD the stored gradient is the pre-scaled, clipped one.
+ * The flat variant is the owned-range step of a ZeRO-1 rank: its range may cut through
+ * tensors (the element chain does not depend on tensor boundaries). */
+int mi_adamw_step_prescaled(const mi_adamw_tensor *d_tensors, const mi_adamw_chunk *d_chunks,
+                            int64_t n_chunks, int64_t chunk_elems, const mi_adamw_hyper *hypers,
+                            int32_t n_hyper, const float *d_grad_scale, float grad_prescale,
+                            int32_t state_dtype, int32_t flags, int32_t max_blocks,
+                            void *stream);
+int mi_adamw_step_flat_prescaled(const mi_adamw_tensor *t, const mi_adamw_hyper *hyper,
+                                 const float *d_grad_scale, float grad_prescale,
+                                 int64_t chunk_elems, int32_t state_dtype, int32_t flags,
+                                 int32_t max_blocks, void *stream);
 
 /* The fused AdamW update of torch's capturable chain (adam.py:480-527) over
  * every chunk of the tables, for a step that may be recorded into a HIP graph:

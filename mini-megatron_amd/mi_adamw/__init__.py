@@ -12,8 +12,9 @@ from .optimizer import FusedAdamW, DEFAULT_CHUNK_ELEMS
 from .clip import clip_grad_norm_
 from .bf16_forward import bf16_weights, linear_layers
 from ._lib import version, MiAdamwError
+from .zero import ZeroRangeStep, dp_prescale, shard_bounds
 
 AdamW = FusedAdamW
 
 __all__ = ["FusedAdamW", "AdamW", "clip_grad_norm_", "bf16_weights", "linear_layers", "version",
-           "MiAdamwError", "DEFAULT_CHUNK_ELEMS"]
+           "MiAdamwError", "DEFAULT_CHUNK_ELEMS", "ZeroRangeStep", "dp_prescale", "shard_bounds"]

@@ -16,7 +16,7 @@ import torch
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libmi_adamw.so")
 
-ABI_VERSION = 6
+ABI_VERSION = 7
 MAX_HYPER = 16
 MAX_NORM_BLOCKS = 4096
 NOALLOC_SCRATCH_BYTES = 4096
@@ -49,9 +49,15 @@ EXPORTS = (
     "mi_adamw_grad_norm",
     "mi_adamw_grad_norm_flat",
     "mi_adamw_grad_norm_flat_noalloc",
+    "mi_adamw_grad_sumsq",
+    "mi_adamw_grad_sumsq_flat",
+    "mi_adamw_norm_from_sumsq",
+    "mi_adamw_set_grads",
     "mi_adamw_scale_grads",
     "mi_adamw_step",
     "mi_adamw_step_flat",
+    "mi_adamw_step_prescaled",
+    "mi_adamw_step_flat_prescaled",
     "mi_adamw_step_capturable",
     "mi_adamw_widen_bf16",
     "mi_adamw_probe",
@@ -131,9 +137,17 @@ _SIGNATURES = {
     "mi_adamw_grad_norm": ([_vp, _vp, _i64, _i64, _f32, _vp, _vp, _vp, _vp], ctypes.c_int),
     "mi_adamw_grad_norm_flat": ([_vp, _i64, _i64, _f32, _vp, _vp, _vp, _vp], ctypes.c_int),
     "mi_adamw_grad_norm_flat_noalloc": ([_vp, _i64, _i64, _f32, _vp, _vp, _vp], ctypes.c_int),
+    "mi_adamw_grad_sumsq": ([_vp, _vp, _i64, _i64, _f32, _vp, _vp, _vp], ctypes.c_int),
+    "mi_adamw_grad_sumsq_flat": ([_vp, _i64, _i64, _f32, _vp, _vp, _vp], ctypes.c_int),
+    "mi_adamw_norm_from_sumsq": ([_vp, _i32, _f32, _vp, _vp, _vp], ctypes.c_int),
+    "mi_adamw_set_grads": ([_vp, _i32, _i32, _vp, _vp, _vp, _vp], ctypes.c_int),
     "mi_adamw_scale_grads": ([_vp, _vp, _i64, _i64, _vp, _vp], ctypes.c_int),
     "mi_adamw_step": ([_vp, _vp, _i64, _i64, _vp, _i32, _vp, _i32, _i32, _i32, _vp], ctypes.c_int),
     "mi_adamw_step_flat": ([_vp, _vp, _vp, _i64, _i32, _i32, _i32, _vp], ctypes.c_int),
+    "mi_adamw_step_prescaled": ([_vp, _vp, _i64, _i64, _vp, _i32, _vp, _f32, _i32, _i32, _i32,
+                                 _vp], ctypes.c_int),
+    "mi_adamw_step_flat_prescaled": ([_vp, _vp, _vp, _f32, _i64, _i32, _i32, _i32, _vp],
+                                     ctypes.c_int),
     "mi_adamw_step_capturable": ([_vp, _vp, _i64, _i64, _vp, _i32, _vp, _vp, _vp, _i32, _i32,
                                   _i32, _vp], ctypes.c_int),
     "mi_adamw_widen_bf16": ([_vp, _vp, _i64, _i64, _vp], ctypes.c_int),

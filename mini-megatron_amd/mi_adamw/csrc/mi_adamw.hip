@@ -399,9 +399,13 @@ __device__ __forceinline__ double block_sum(double x) {
 // next chunk's table entry is fetched before the current chunk's loads are
 // consumed, so the scalar-load latency of the lookup overlaps the stream.
 
-__device__ __forceinline__ void sumsq4(f32x4 a, double& acc0, double& acc1) {
-    acc0 += (double)a.x * a.x + (double)a.y * a.y;
-    acc1 += (double)a.z * a.z + (double)a.w * a.w;
+// The squares of pre*g, each product rounded to fp32 first: the value a caller's
+// `grad.div_(world)` (parallel/data_parallel.py:15) would have stored.  pre == 1 leaves
+// every gradient as it is (x * 1 == x).
+__device__ __forceinline__ void sumsq4(f32x4 a, float pre, double& acc0, double& acc1) {
+    const float x = a.x * pre, y = a.y * pre, z = a.z * pre, w = a.w * pre;
+    acc0 += (double)x * x + (double)y * y;
+    acc1 += (double)z * z + (double)w * w;
 }
 
 // Sum of squares over chunks c, c + stride, ... below c_end.  The next chunk's
@@ -409,7 +413,7 @@ __device__ __forceinline__ void sumsq4(f32x4 a, double& acc0, double& acc1) {
 // the first chunk of the sequence at or past c_end.
 template <bool kKeep, class Src>
 __device__ __forceinline__ int64_t sumsq_chunks(const Src& src, int64_t c, int64_t c_end,
-                                                int64_t stride, int64_t chunk_elems,
+                                                int64_t stride, int64_t chunk_elems, float pre,
                                                 double& acc0, double& acc1) {
     mi_adamw_tensor t;
     int64_t begin = 0, end = 0;
@@ -439,25 +443,25 @@ __device__ __forceinline__ int64_t sumsq_chunks(const Src& src, int64_t c, int64
         if (more) src.get(c + stride, chunk_elems, tn, bn, en, row);
         __builtin_amdgcn_sched_barrier(0);
         if (full) {
-            sumsq4(a, acc0, acc1);
-            sumsq4(b, acc0, acc1);
-            sumsq4(d, acc0, acc1);
-            sumsq4(e, acc0, acc1);
+            sumsq4(a, pre, acc0, acc1);
+            sumsq4(b, pre, acc0, acc1);
+            sumsq4(d, pre, acc0, acc1);
+            sumsq4(e, pre, acc0, acc1);
             i += 4 * kNormTile;
             for (; i + 3 * kNormTile < vend; i += 4 * kNormTile) {
                 a = ld4_norm<kKeep>(g + i);
                 b = ld4_norm<kKeep>(g + i + kNormTile);
                 d = ld4_norm<kKeep>(g + i + 2 * kNormTile);
                 e = ld4_norm<kKeep>(g + i + 3 * kNormTile);
-                sumsq4(a, acc0, acc1);
-                sumsq4(b, acc0, acc1);
-                sumsq4(d, acc0, acc1);
-                sumsq4(e, acc0, acc1);
+                sumsq4(a, pre, acc0, acc1);
+                sumsq4(b, pre, acc0, acc1);
+                sumsq4(d, pre, acc0, acc1);
+                sumsq4(e, pre, acc0, acc1);
             }
         }
-        for (; i < vend; i += kNormTile) sumsq4(ld4_norm<kKeep>(g + i), acc0, acc1);
+        for (; i < vend; i += kNormTile) sumsq4(ld4_norm<kKeep>(g + i), pre, acc0, acc1);
         for (int64_t j = vend + threadIdx.x; j < end; j += kNormThreads) {
-            double x = ld1(g + j);
+            const double x = ld1(g + j) * pre;
             acc0 += x * x;
         }
         if (more) {
@@ -476,11 +480,11 @@ __device__ __forceinline__ int64_t sumsq_chunks(const Src& src, int64_t c, int64
 template <class Src>
 __global__ __launch_bounds__(kNormThreads) void mi_adamw_sumsq_kernel(
     Src src, int64_t n_chunks, int64_t chunk_elems, double* __restrict__ partials,
-    int64_t keep_from) {
+    int64_t keep_from, float pre) {
     double acc0 = 0.0, acc1 = 0.0;
     int64_t c = blockIdx.x;
-    c = sumsq_chunks<false>(src, c, keep_from, gridDim.x, chunk_elems, acc0, acc1);
-    sumsq_chunks<true>(src, c, n_chunks, gridDim.x, chunk_elems, acc0, acc1);
+    c = sumsq_chunks<false>(src, c, keep_from, gridDim.x, chunk_elems, pre, acc0, acc1);
+    sumsq_chunks<true>(src, c, n_chunks, gridDim.x, chunk_elems, pre, acc0, acc1);
     const double total = block_sum<kNormThreads>(acc0 + acc1);
     if (threadIdx.x == 0) partials[blockIdx.x] = total;
 }
@@ -503,6 +507,18 @@ __global__ __launch_bounds__(kNormThreads) void mi_adamw_norm_finalize_kernel(
         *norm_out = norm;
         *coef_out = coef > 1.0f ? 1.0f : coef;  // NaN stays NaN, as torch.clamp
     }
+}
+
+// One workgroup: the partial sums of one range reduced to its float64 sum of squares,
+// in the same fixed order as the finalize above.  Fed back to the finalize as a
+// one-element array, the sum gives the same norm, bit for bit, as the finalize over
+// the partials themselves (0 + s == s, and s + 0 == s for s >= 0).
+__global__ __launch_bounds__(kNormThreads) void mi_adamw_sumsq_reduce_kernel(
+    const double* __restrict__ partials, int n_partials, double* __restrict__ sumsq_out) {
+    double s = 0.0;
+    for (int i = threadIdx.x; i < n_partials; i += kNormThreads) s += partials[i];
+    s = block_sum<kNormThreads>(s);
+    if (threadIdx.x == 0) *sumsq_out = s;
 }
 
 // ---------------------------------------------------------------------------
@@ -530,7 +546,7 @@ struct Tile {
 template <class Src, class HS, typename StateT, bool kClip, bool kCopy, bool kWriteGrad, bool kAms>
 __global__ __launch_bounds__(kUpdThreads) void mi_adamw_update_kernel(
     Src src, int64_t n_chunks, int64_t chunk_elems, HS hs,
-    const float* __restrict__ grad_scale) {
+    const float* __restrict__ grad_scale, float pre) {
     using IO = StateIO<StateT>;
     using T = Tile<StateT, kAms>;
     constexpr bool kCapt = HS::kCapt;
@@ -570,7 +586,8 @@ __global__ __launch_bounds__(kUpdThreads) void mi_adamw_update_kernel(
                     const bool more = j < vend;
                     T nxt = cur;
                     if (more) nxt.load(P, G, M, V, X, j);
-                    f32x4 gs = cur.g;
+                    // the stored value of div_(world), then of the clip, then -g with maximize
+                    f32x4 gs = f32x4{cur.g.x * pre, cur.g.y * pre, cur.g.z * pre, cur.g.w * pre};
                     if (kClip) gs = f32x4{gs.x * scale, gs.y * scale, gs.z * scale, gs.w * scale};
                     if (kWriteGrad) st4(G + i, gs);
                     if (kProbe) {
@@ -595,7 +612,7 @@ __global__ __launch_bounds__(kUpdThreads) void mi_adamw_update_kernel(
         if (kCapt && vend < end) h = hs.get(t, row);
         const float gmul = h.grad_sign;
         for (int64_t j = vend + threadIdx.x; j < end; j += kUpdThreads) {
-            float g1 = ld1(G + j);
+            float g1 = ld1(G + j) * pre;
             if (kClip) g1 = g1 * scale;
             if (kWriteGrad) st1(G + j, g1);
             g1 = g1 * gmul;
@@ -663,6 +680,30 @@ __global__ __launch_bounds__(kUpdThreads) void mi_adamw_widen_kernel(
 }
 
 // ---------------------------------------------------------------------------
+// New gradient addresses for rows of a tensor table, for when only the gradients moved
+// (zero_grad freed them and backward allocated new ones).  The values travel as kernel
+// arguments, so the host needs no staging buffer and may reuse its arrays at once.
+
+constexpr int kPatchRows = 128;
+struct GradPatch {
+    uint64_t grad[kPatchRows];
+    int32_t row[kPatchRows];
+    uint32_t vec[kPatchRows / 32];   // bit i: row[i] may take the dwordx4 path
+    int32_t count;
+};
+
+__global__ __launch_bounds__(kPatchRows) void mi_adamw_set_grads_kernel(
+    mi_adamw_tensor* __restrict__ tensors, GradPatch patch) {
+    const int i = threadIdx.x;
+    if (i < patch.count) {
+        mi_adamw_tensor* t = tensors + patch.row[i];
+        t->grad = reinterpret_cast<float*>(patch.grad[i]);
+        const bool vec = (patch.vec[i >> 5] >> (i & 31)) & 1u;
+        t->flags = (t->flags & ~MI_ADAMW_T_VEC) | (vec ? MI_ADAMW_T_VEC : 0);
+    }
+}
+
+// ---------------------------------------------------------------------------
 // Host side
 
 // Workgroups (and partial sums) of the norm pass: two 256-thread workgroups per CU.
@@ -696,46 +737,74 @@ unsigned grid_for(int64_t n_chunks, int32_t max_blocks, int threads) {
 
 bool aligned(const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0; }
 
-// partials_cap: doubles available at `partials` (one per workgroup of the pass).
+bool finite(float x) { return x - x == 0.0f; }
+
+// Pass 1 alone: one float64 partial sum of (pre*g)^2 per workgroup into `partials`
+// (partials_cap doubles available).  Sets *grid_out to the number of partials written.
 template <class Src>
-int launch_norm(const Src& src, int64_t n_chunks, int64_t chunk_elems, float max_norm,
-                double* partials, float* norm, float* coef, hipStream_t s,
-                int64_t partials_cap = MI_ADAMW_MAX_NORM_BLOCKS) {
-    if (n_chunks <= 0 || !chunk_elems_ok(chunk_elems) || !partials || !norm || !coef)
-        return MI_ADAMW_E_INVALID;
+int launch_sumsq(const Src& src, int64_t n_chunks, int64_t chunk_elems, float pre,
+                 double* partials, int64_t partials_cap, unsigned* grid_out, hipStream_t s) {
+    if (n_chunks <= 0 || !chunk_elems_ok(chunk_elems) || !partials) return MI_ADAMW_E_INVALID;
     const unsigned grid = grid_for(n_chunks, kNormBlocks, kNormThreads);
     if (grid > partials_cap) return MI_ADAMW_E_SCRATCH;
     const int64_t keep_chunks = kNormKeepBytes / (chunk_elems * static_cast<int64_t>(sizeof(float)));
     const int64_t keep_from = n_chunks > keep_chunks ? n_chunks - keep_chunks : 0;
     hipLaunchKernelGGL(mi_adamw_sumsq_kernel<Src>, dim3(grid), dim3(kNormThreads), 0, s, src,
-                       n_chunks, chunk_elems, partials, keep_from);
-    int rc = launch_status();
+                       n_chunks, chunk_elems, partials, keep_from, pre);
+    *grid_out = grid;
+    return launch_status();
+}
+
+// Pass 1 and the finalize: norm and clip coefficient of one range.
+template <class Src>
+int launch_norm(const Src& src, int64_t n_chunks, int64_t chunk_elems, float max_norm,
+                double* partials, float* norm, float* coef, hipStream_t s,
+                int64_t partials_cap = MI_ADAMW_MAX_NORM_BLOCKS, float pre = 1.0f) {
+    if (!norm || !coef) return MI_ADAMW_E_INVALID;
+    unsigned grid = 0;
+    int rc = launch_sumsq(src, n_chunks, chunk_elems, pre, partials, partials_cap, &grid, s);
     if (rc != MI_ADAMW_OK) return rc;
     hipLaunchKernelGGL(mi_adamw_norm_finalize_kernel, dim3(1), dim3(kNormThreads), 0, s, partials,
                        static_cast<int>(grid), max_norm, norm, coef);
     return launch_status();
 }
 
+// Pass 1 and the reduction of its partials to one float64 sum of squares.
+template <class Src>
+int launch_sumsq_total(const Src& src, int64_t n_chunks, int64_t chunk_elems, float pre,
+                       double* partials, double* sumsq, hipStream_t s) {
+    if (!sumsq) return MI_ADAMW_E_INVALID;
+    unsigned grid = 0;
+    int rc = launch_sumsq(src, n_chunks, chunk_elems, pre, partials, MI_ADAMW_MAX_NORM_BLOCKS,
+                          &grid, s);
+    if (rc != MI_ADAMW_OK) return rc;
+    hipLaunchKernelGGL(mi_adamw_sumsq_reduce_kernel, dim3(1), dim3(kNormThreads), 0, s, partials,
+                       static_cast<int>(grid), sumsq);
+    return launch_status();
+}
+
 template <class Src, class HS, typename StateT, bool kClip, bool kCopy, bool kWriteGrad,
           bool kAms>
 int launch_update_k(const Src& src, int64_t n_chunks, int64_t chunk_elems, const HS& hs,
-                    const float* scale, unsigned grid, hipStream_t s) {
+                    const float* scale, float pre, unsigned grid, hipStream_t s) {
     hipLaunchKernelGGL((mi_adamw_update_kernel<Src, HS, StateT, kClip, kCopy, kWriteGrad, kAms>),
-                       dim3(grid), dim3(kUpdThreads), 0, s, src, n_chunks, chunk_elems, hs, scale);
+                       dim3(grid), dim3(kUpdThreads), 0, s, src, n_chunks, chunk_elems, hs, scale,
+                       pre);
     return launch_status();
 }
 
 // Runtime flags -> kernel template: one instantiation per (copy, write-grad, amsgrad).
 template <class Src, class HS, typename StateT, bool kClip>
 int launch_update_cw(const Src& src, int64_t n_chunks, int64_t chunk_elems, const HS& hs,
-                     const float* scale, int32_t flags, unsigned grid, hipStream_t s) {
+                     const float* scale, float pre, int32_t flags, unsigned grid,
+                     hipStream_t s) {
     const int sel = ((flags & MI_ADAMW_F_BF16_COPY) ? 1 : 0) |
                     ((flags & MI_ADAMW_F_WRITE_GRAD) ? 2 : 0) |
                     ((flags & MI_ADAMW_F_AMSGRAD) ? 4 : 0);
 #define MI_ADAMW_SEL(k, C, W, A)                                                              \
     case k:                                                                                   \
         return launch_update_k<Src, HS, StateT, kClip, C, W, A>(src, n_chunks, chunk_elems,  \
-                                                                 hs, scale, grid, s);
+                                                                 hs, scale, pre, grid, s);
     switch (sel) {
         MI_ADAMW_SEL(0, false, false, false)
         MI_ADAMW_SEL(1, true, false, false)
@@ -753,7 +822,7 @@ int launch_update_cw(const Src& src, int64_t n_chunks, int64_t chunk_elems, cons
 template <class Src, class HS>
 int launch_update(const Src& src, int64_t n_chunks, int64_t chunk_elems, const HS& hs,
                   const float* scale, int32_t state_dtype, int32_t flags, int32_t max_blocks,
-                  hipStream_t s) {
+                  hipStream_t s, float pre = 1.0f) {
     if (n_chunks <= 0 || !chunk_elems_ok(chunk_elems)) return MI_ADAMW_E_INVALID;
     if (state_dtype != MI_ADAMW_STATE_F32 && state_dtype != MI_ADAMW_STATE_BF16)
         return MI_ADAMW_E_INVALID;
@@ -765,13 +834,13 @@ int launch_update(const Src& src, int64_t n_chunks, int64_t chunk_elems, const H
     const unsigned grid = grid_for(n_chunks, max_blocks, kUpdThreads);
     if (state_dtype == MI_ADAMW_STATE_F32)
         return clip ? launch_update_cw<Src, HS, float, true>(src, n_chunks, chunk_elems, hs,
-                                                              scale, flags, grid, s)
+                                                              scale, pre, flags, grid, s)
                     : launch_update_cw<Src, HS, float, false>(src, n_chunks, chunk_elems, hs,
-                                                               scale, flags, grid, s);
+                                                               scale, pre, flags, grid, s);
     return clip ? launch_update_cw<Src, HS, uint16_t, true>(src, n_chunks, chunk_elems, hs, scale,
-                                                             flags, grid, s)
+                                                             pre, flags, grid, s)
                 : launch_update_cw<Src, HS, uint16_t, false>(src, n_chunks, chunk_elems, hs,
-                                                              scale, flags, grid, s);
+                                                              scale, pre, flags, grid, s);
 }
 
 // The memory-only twin of launch_update (no clip: the gradient is read either way).
@@ -788,9 +857,9 @@ int launch_probe(const Src& src, int64_t n_chunks, int64_t chunk_elems, int32_t 
     const ProbeHyper hs;
     if (state_dtype == MI_ADAMW_STATE_F32)
         return launch_update_cw<Src, ProbeHyper, float, false>(src, n_chunks, chunk_elems, hs,
-                                                               nullptr, flags, grid, s);
+                                                               nullptr, 1.0f, flags, grid, s);
     return launch_update_cw<Src, ProbeHyper, uint16_t, false>(src, n_chunks, chunk_elems, hs,
-                                                              nullptr, flags, grid, s);
+                                                              nullptr, 1.0f, flags, grid, s);
 }
 
 // Validate one host-visible tensor descriptor for the flat entry points.
@@ -868,8 +937,9 @@ int scratch_on(hipStream_t s, double** out) {
 extern "C" {
 
 const char* mi_adamw_version(void) {
-    return "mi_adamw 6 gfx950 fused clip+adamw (fp32/bf16 state, bf16 copy, amsgrad, flat, "
-           "capturable, bf16 widen, memory probe, no-alloc norm)";
+    return "mi_adamw 7 gfx950 fused clip+adamw (fp32/bf16 state, bf16 copy, amsgrad, flat, "
+           "capturable, bf16 widen, memory probe, no-alloc norm, range norm, grad prescale, "
+           "grad patch)";
 }
 
 const char* mi_adamw_strerror(int code) {
@@ -941,6 +1011,65 @@ int mi_adamw_grad_norm_flat_noalloc(const float* d_grad, int64_t n, int64_t chun
                        kScratchDoubles);
 }
 
+int mi_adamw_grad_sumsq(const mi_adamw_tensor* d_tensors, const mi_adamw_chunk* d_chunks,
+                        int64_t n_chunks, int64_t chunk_elems, float grad_prescale,
+                        double* d_partials, double* d_sumsq, void* stream) {
+    if (!d_tensors || !d_chunks || !finite(grad_prescale)) return MI_ADAMW_E_INVALID;
+    TableSource src{d_tensors, d_chunks};
+    return launch_sumsq_total(src, n_chunks, chunk_elems, grad_prescale, d_partials, d_sumsq,
+                              static_cast<hipStream_t>(stream));
+}
+
+int mi_adamw_grad_sumsq_flat(const float* d_grad, int64_t n, int64_t chunk_elems,
+                             float grad_prescale, double* d_partials, double* d_sumsq,
+                             void* stream) {
+    if (!d_grad || n <= 0 || !chunk_elems_ok(chunk_elems) || !finite(grad_prescale))
+        return MI_ADAMW_E_INVALID;
+    FlatSource src;
+    memset(&src.t, 0, sizeof(src.t));
+    src.t.grad = const_cast<float*>(d_grad);
+    src.t.numel = n;
+    src.t.flags = aligned(d_grad, 16) ? MI_ADAMW_T_VEC : 0;
+    const int64_t n_chunks = (n + chunk_elems - 1) / chunk_elems;
+    return launch_sumsq_total(src, n_chunks, chunk_elems, grad_prescale, d_partials, d_sumsq,
+                              static_cast<hipStream_t>(stream));
+}
+
+int mi_adamw_norm_from_sumsq(const double* d_sumsq, int32_t n, float max_norm, float* d_norm,
+                             float* d_coef, void* stream) {
+    if (!d_sumsq || n <= 0 || n > MI_ADAMW_MAX_NORM_BLOCKS || !d_norm || !d_coef)
+        return MI_ADAMW_E_INVALID;
+    hipLaunchKernelGGL(mi_adamw_norm_finalize_kernel, dim3(1), dim3(kNormThreads), 0,
+                       static_cast<hipStream_t>(stream), d_sumsq, static_cast<int>(n), max_norm,
+                       d_norm, d_coef);
+    return launch_status();
+}
+
+int mi_adamw_set_grads(mi_adamw_tensor* d_tensors, int32_t n_rows, int32_t n,
+                       const int32_t* rows, const uint64_t* grads, const uint8_t* vec,
+                       void* stream) {
+    if (!d_tensors || n_rows <= 0 || n < 0 || (n > 0 && (!rows || !grads || !vec)))
+        return MI_ADAMW_E_INVALID;
+    for (int32_t i = 0; i < n; ++i)
+        if (rows[i] < 0 || rows[i] >= n_rows) return MI_ADAMW_E_INVALID;
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    for (int32_t base = 0; base < n; base += kPatchRows) {
+        GradPatch patch;
+        memset(&patch, 0, sizeof(patch));
+        patch.count = n - base < kPatchRows ? n - base : kPatchRows;
+        for (int32_t i = 0; i < patch.count; ++i) {
+            patch.grad[i] = grads[base + i];
+            patch.row[i] = rows[base + i];
+            if (vec[base + i]) patch.vec[i >> 5] |= 1u << (i & 31);
+        }
+        hipLaunchKernelGGL(mi_adamw_set_grads_kernel, dim3(1), dim3(kPatchRows), 0, s, d_tensors,
+                           patch);
+        const int rc = launch_status();
+        if (rc != MI_ADAMW_OK) return rc;
+    }
+    return MI_ADAMW_OK;
+}
+
 int mi_adamw_scale_grads(const mi_adamw_tensor* d_tensors, const mi_adamw_chunk* d_chunks,
                          int64_t n_chunks, int64_t chunk_elems, const float* d_coef,
                          void* stream) {
@@ -964,24 +1093,36 @@ int mi_adamw_widen_bf16(const mi_adamw_tensor* d_tensors, const mi_adamw_chunk* 
     return launch_status();
 }
 
-int mi_adamw_step(const mi_adamw_tensor* d_tensors, const mi_adamw_chunk* d_chunks,
-                  int64_t n_chunks, int64_t chunk_elems, const mi_adamw_hyper* hypers,
-                  int32_t n_hyper, const float* d_grad_scale, int32_t state_dtype, int32_t flags,
-                  int32_t max_blocks, void* stream) {
-    if (!d_tensors || !d_chunks || !hypers || n_hyper <= 0 || n_hyper > MI_ADAMW_MAX_HYPER)
+int mi_adamw_step_prescaled(const mi_adamw_tensor* d_tensors, const mi_adamw_chunk* d_chunks,
+                            int64_t n_chunks, int64_t chunk_elems, const mi_adamw_hyper* hypers,
+                            int32_t n_hyper, const float* d_grad_scale, float grad_prescale,
+                            int32_t state_dtype, int32_t flags, int32_t max_blocks,
+                            void* stream) {
+    if (!d_tensors || !d_chunks || !hypers || n_hyper <= 0 || n_hyper > MI_ADAMW_MAX_HYPER ||
+        !finite(grad_prescale))
         return MI_ADAMW_E_INVALID;
     StaticHyper hs;
     memset(&hs, 0, sizeof(hs));
     memcpy(hs.hp.h, hypers, sizeof(mi_adamw_hyper) * n_hyper);
     TableSource src{d_tensors, d_chunks};
     return launch_update(src, n_chunks, chunk_elems, hs, d_grad_scale, state_dtype, flags,
-                         max_blocks, static_cast<hipStream_t>(stream));
+                         max_blocks, static_cast<hipStream_t>(stream), grad_prescale);
 }
 
-int mi_adamw_step_flat(const mi_adamw_tensor* t, const mi_adamw_hyper* hyper,
-                       const float* d_grad_scale, int64_t chunk_elems, int32_t state_dtype,
-                       int32_t flags, int32_t max_blocks, void* stream) {
-    if (!hyper || !chunk_elems_ok(chunk_elems)) return MI_ADAMW_E_INVALID;
+int mi_adamw_step(const mi_adamw_tensor* d_tensors, const mi_adamw_chunk* d_chunks,
+                  int64_t n_chunks, int64_t chunk_elems, const mi_adamw_hyper* hypers,
+                  int32_t n_hyper, const float* d_grad_scale, int32_t state_dtype, int32_t flags,
+                  int32_t max_blocks, void* stream) {
+    return mi_adamw_step_prescaled(d_tensors, d_chunks, n_chunks, chunk_elems, hypers, n_hyper,
+                                   d_grad_scale, 1.0f, state_dtype, flags, max_blocks, stream);
+}
+
+int mi_adamw_step_flat_prescaled(const mi_adamw_tensor* t, const mi_adamw_hyper* hyper,
+                                 const float* d_grad_scale, float grad_prescale,
+                                 int64_t chunk_elems, int32_t state_dtype, int32_t flags,
+                                 int32_t max_blocks, void* stream) {
+    if (!hyper || !chunk_elems_ok(chunk_elems) || !finite(grad_prescale))
+        return MI_ADAMW_E_INVALID;
     int rc = check_flat(t, state_dtype, flags);
     if (rc != MI_ADAMW_OK) return rc;
     StaticHyper hs;
@@ -992,7 +1133,14 @@ int mi_adamw_step_flat(const mi_adamw_tensor* t, const mi_adamw_hyper* hyper,
     src.t.hyper = 0;
     const int64_t n_chunks = (t->numel + chunk_elems - 1) / chunk_elems;
     return launch_update(src, n_chunks, chunk_elems, hs, d_grad_scale, state_dtype, flags,
-                         max_blocks, static_cast<hipStream_t>(stream));
+                         max_blocks, static_cast<hipStream_t>(stream), grad_prescale);
+}
+
+int mi_adamw_step_flat(const mi_adamw_tensor* t, const mi_adamw_hyper* hyper,
+                       const float* d_grad_scale, int64_t chunk_elems, int32_t state_dtype,
+                       int32_t flags, int32_t max_blocks, void* stream) {
+    return mi_adamw_step_flat_prescaled(t, hyper, d_grad_scale, 1.0f, chunk_elems, state_dtype,
+                                        flags, max_blocks, stream);
 }
 
 int mi_adamw_step_capturable(const mi_adamw_tensor* d_tensors, const mi_adamw_chunk* d_chunks,

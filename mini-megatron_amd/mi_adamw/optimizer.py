@@ -251,6 +251,13 @@ class FusedAdamW(Optimizer):
                       step each param group as one contiguous range.  Gradients
                       stay allocated: zero_grad() zeroes them in place.
     chunk_elems:      elements per work chunk (multiple of 4096).
+    grad_prescale:    multiply every gradient by this fp32 factor first, in the
+                      kernels (one rounding, as ``grad.div_(world)`` stores it):
+                      with ``dp_prescale(world)`` it takes the place of the
+                      world-size division of parallel/data_parallel.py:15 after
+                      a summing all-reduce.  ``p.grad`` is left as it was (with
+                      clip_write_grads the stored gradient is the pre-scaled,
+                      clipped one).
 
     Not supported (NotImplementedError at construction): differentiable, betas
     as tensors, param groups with different capturable settings.
@@ -276,6 +283,7 @@ class FusedAdamW(Optimizer):
         bf16_copy: bool = False,
         flat_buffer: bool = False,
         chunk_elems: int = DEFAULT_CHUNK_ELEMS,
+        grad_prescale: float = 1.0,
     ) -> None:
         # adam.py:58-86, in the same order and with the same messages.
         if isinstance(lr, torch.Tensor):
@@ -319,6 +327,12 @@ class FusedAdamW(Optimizer):
             raise ValueError(f"state_dtype must be torch.float32 or torch.bfloat16, got {state_dtype}")
         if chunk_elems <= 0 or chunk_elems % _lib.CHUNK_QUANTUM:
             raise ValueError(f"chunk_elems must be a positive multiple of {_lib.CHUNK_QUANTUM}")
+        grad_prescale = float(np.float32(grad_prescale))
+        if not (np.isfinite(grad_prescale) and grad_prescale > 0):
+            raise ValueError(f"Invalid grad_prescale: {grad_prescale}")
+        if capturable and grad_prescale != 1.0:
+            raise NotImplementedError("FusedAdamW: grad_prescale with capturable=True is not "
+                                      "supported")
 
         self.capturable = bool(capturable)
         self.max_grad_norm = None if max_grad_norm is None else float(max_grad_norm)
@@ -327,6 +341,7 @@ class FusedAdamW(Optimizer):
         self.bf16_copy = bool(bf16_copy)
         self.flat_buffer = bool(flat_buffer)
         self.chunk_elems = int(chunk_elems)
+        self.grad_prescale = grad_prescale
         self.max_blocks = 0
         self._reset_bookkeeping()
 
@@ -344,7 +359,7 @@ class FusedAdamW(Optimizer):
             self._flat = FlatLayout(self.param_groups, self.state_dtype, self.bf16_copy)
 
     _OPTIONS = ("capturable", "max_grad_norm", "clip_write_grads", "state_dtype", "bf16_copy",
-                "flat_buffer", "chunk_elems", "max_blocks")
+                "flat_buffer", "chunk_elems", "grad_prescale", "max_blocks")
 
     def _reset_bookkeeping(self) -> None:
         """The state this class keeps beside torch's: step slots, the packed step buffer,
@@ -789,6 +804,14 @@ class FusedAdamW(Optimizer):
             ws = self._workspace[device] = (partials, coef)
         return ws
 
+    def _sumsq_buf(self, device: torch.device) -> torch.Tensor:
+        """One float64 on the device: the pre-scaled gradients' sum of squares."""
+        buf = self._workspace.get(("sumsq", device))
+        if buf is None:
+            buf = self._workspace[("sumsq", device)] = torch.zeros(1, dtype=torch.float64,
+                                                                    device=device)
+        return buf
+
     def _rows(self, entries, hyper_idx, ams):
         """(rows, src, rest): the table rows of `entries`, the entry each row's gradient
         belongs to (-1 for a flat group row) and whether its other pointers are aligned."""
@@ -963,6 +986,22 @@ class FusedAdamW(Optimizer):
                 # nothing but empty tensors: torch's norm of no elements is 0
                 norm.zero_()
                 coef.fill_(1.0)
+            elif self.grad_prescale != 1.0:
+                # the sum of squares of the pre-scaled gradients, then the finalize over it
+                sumsq = self._sumsq_buf(device)
+                if norm_launch.n_rows == 1:
+                    row = self._row_struct(norm_launch)
+                    _lib.check(lib.mi_adamw_grad_sumsq_flat(
+                        row.grad, row.numel, self.chunk_elems, self.grad_prescale,
+                        partials.data_ptr(), sumsq.data_ptr(), stream), "mi_adamw_grad_sumsq_flat")
+                else:
+                    _lib.check(lib.mi_adamw_grad_sumsq(
+                        norm_launch.rows.data_ptr(), norm_launch.chunks.data_ptr(),
+                        norm_launch.n_chunks, self.chunk_elems, self.grad_prescale,
+                        partials.data_ptr(), sumsq.data_ptr(), stream), "mi_adamw_grad_sumsq")
+                _lib.check(lib.mi_adamw_norm_from_sumsq(
+                    sumsq.data_ptr(), 1, float(self.max_grad_norm), norm.data_ptr(),
+                    coef.data_ptr(), stream), "mi_adamw_norm_from_sumsq")
             elif norm_launch.n_rows == 1:
                 row = self._row_struct(norm_launch)
                 _lib.check(lib.mi_adamw_grad_norm_flat(
@@ -994,12 +1033,25 @@ class FusedAdamW(Optimizer):
                     self.max_blocks, stream), "mi_adamw_step_capturable")
                 continue
             harr = (_lib.Hyper * len(hs))(*hs)
+            pre = self.grad_prescale
             if launch.n_rows == 1:
                 row = self._row_struct(launch)
                 row_h = hs[int(launch.host_rows[0]["hyper"])]
+                if pre != 1.0:
+                    _lib.check(lib.mi_adamw_step_flat_prescaled(
+                        ctypes.byref(row), ctypes.byref(row_h), coef.data_ptr(), pre,
+                        self.chunk_elems, state_code, lflags, self.max_blocks, stream),
+                        "mi_adamw_step_flat_prescaled")
+                    continue
                 _lib.check(lib.mi_adamw_step_flat(
                     ctypes.byref(row), ctypes.byref(row_h), coef.data_ptr(), self.chunk_elems,
                     state_code, lflags, self.max_blocks, stream), "mi_adamw_step_flat")
+                continue
+            if pre != 1.0:
+                _lib.check(lib.mi_adamw_step_prescaled(
+                    launch.rows.data_ptr(), launch.chunks.data_ptr(), launch.n_chunks,
+                    self.chunk_elems, harr, len(hs), coef.data_ptr(), pre, state_code, lflags,
+                    self.max_blocks, stream), "mi_adamw_step_prescaled")
                 continue
             _lib.check(lib.mi_adamw_step(
                 launch.rows.data_ptr(), launch.chunks.data_ptr(), launch.n_chunks,
