@@ -8,18 +8,25 @@ runs at main.py:209.  Gradients are generated once before the timed region;
 the step only reads them (the clip scale is applied in registers), so every
 timed step does the full work.
 
-Default workload (one GPU): gpt-125m, fp32 params/grads/moments, global
-grad-norm clip at 1.0 fused ahead of AdamW, optimizer state mid-training
-(step 1000), lr 3e-4, betas (0.9, 0.95), eps 1e-8, weight decay 0.1.
+Default run (one GPU).  Headline: gpt-6.7b (6,863,077,376 params, 261 tensors)
+in the flat-buffer layout, fp32 params/grads/moments, global grad-norm clip at
+1.0 fused ahead of AdamW, bf16 model copy written by the step, optimizer state
+mid-training (step 1000), lr 3e-4, betas (0.9, 0.95), eps 1e-8, weight decay 0.1.
+The other configurations of the workload list (125M, 350M, 1.3B with bf16
+moments, in the layouts the optimizer offers) are timed in the same run as rows
+of ``sweep``, each with its own ``roofline``.
 
 Output: one JSON line.  ``value`` is the achieved HBM bandwidth of the whole
 step in GB/s, from algorithmic bytes (every byte the step must read or write,
 counted once) over the measured step time.  ``roofline`` reports the update
-kernel against MI355X's 8 TB/s, timed with HIP events on the launch stream.
+kernel against MI355X's 8 TB/s, timed with HIP events on the launch stream,
+with its memory-only twin on the same tensors (``mix_probe``) and the HBM bytes
+per launch that rocprofv3's counters measured (``traffic``, profiles/).
 ``cpu_baseline`` times the reference's own CPU path (torch.optim.AdamW with
-foreach=False, after clip_grad_norm_) on the host's cores.
+foreach=False, after clip_grad_norm_) over the same parameter set on the host's
+physical cores.
 
-    python bench.py [--steps K] [--warmup W] [--config NAME | --config all]
+    python bench.py [--steps K] [--warmup W] [--config NAME] [--sweep A,B|all|none]
 """
 from __future__ import annotations
 
@@ -46,9 +53,17 @@ CONFIGS = {
     "350m-master-clip-copy": ("gpt-350m", True, "fp32", True, False, 1000, 1e-3),
     "1.3b-bf16state-copy": ("gpt-1.3b", False, "bf16", True, False, 1000, 1e-3),
     "1.3b-bf16state-copy-clip": ("gpt-1.3b", True, "bf16", True, False, 1000, 1e-3),
+    "1.3b-bf16state-copy-clip-flat": ("gpt-1.3b", True, "bf16", True, True, 1000, 1e-3),
     "6.7b-flat-clip-copy": ("gpt-6.7b", True, "fp32", True, True, 1000, 1e-3),
 }
-DEFAULT_CONFIG = "125m-clip"
+# The headline is the largest configuration that fits one GPU, the 6.7B flat clip + copy
+# step; the other configurations are timed in the same run, as rows of `sweep`.
+DEFAULT_CONFIG = "6.7b-flat-clip-copy"
+DEFAULT_SWEEP = ("1.3b-bf16state-copy-clip-flat", "1.3b-bf16state-copy-clip",
+                 "1.3b-bf16state-copy", "350m-master-clip-copy", "125m-clip", "125m-step1")
+# CPU baselines: the clip configurations of the workload list (125M, 350M, 1.3B, 6.7B)
+DEFAULT_CPU = ("6.7b-flat-clip-copy", "1.3b-bf16state-copy-clip-flat", "350m-master-clip-copy",
+               "125m-clip")
 HP = dict(lr=3e-4, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.1)
 
 
@@ -139,18 +154,33 @@ def _pct(xs, q):
 
 
 def host_cpu() -> dict:
-    """CPU model and counts of this host, for the baseline's context."""
-    model = None
+    """CPU model, logical and physical core counts of the CPUs this process may run on
+    (lscpu's view, read from /proc/cpuinfo), host memory, and torch's thread count."""
+    allowed = sorted(os.sched_getaffinity(0))
+    model, cores = None, set()
     try:
         with open("/proc/cpuinfo") as f:
-            for line in f:
-                if line.startswith("model name"):
-                    model = line.split(":", 1)[1].strip()
-                    break
+            for line in f.read().split("\n\n"):
+                fields = dict(l.split(":", 1) for l in line.splitlines() if ":" in l)
+                fields = {k.strip(): v.strip() for k, v in fields.items()}
+                if "processor" not in fields or int(fields["processor"]) not in allowed:
+                    continue
+                model = model or fields.get("model name")
+                cores.add((fields.get("physical id", "0"), fields.get("core id",
+                                                                        fields["processor"])))
     except OSError:
         pass
-    return {"model": model, "logical_cpus": os.cpu_count(),
-            "affinity_cpus": len(os.sched_getaffinity(0)), "torch_threads": torch.get_num_threads()}
+    ram = None
+    try:
+        with open("/proc/meminfo") as f:
+            for line in f:
+                if line.startswith("MemTotal:"):
+                    ram = round(int(line.split()[1]) / 2**20, 1)
+    except OSError:
+        pass
+    return {"model": model, "logical_cpus": os.cpu_count(), "affinity_cpus": len(allowed),
+            "physical_cores": len(cores) or None, "ram_gib": ram,
+            "torch_threads": torch.get_num_threads()}
 
 
 def torch_gpu_rows(name: str, device, steps: int = 10, warmup: int = 3) -> dict:
@@ -198,56 +228,88 @@ def torch_gpu_rows(name: str, device, steps: int = 10, warmup: int = 3) -> dict:
     return out
 
 
-def cpu_baseline(name: str, budget_s: float = 20.0) -> dict:
-    """The reference's CPU path: torch.optim.AdamW(foreach=False) (+ clip_grad_norm_),
-    on CPU tensors of the same set, bounded to about `budget_s` seconds of work."""
+def cpu_baseline(name: str, batch_params: int = 1 << 29, warmup: int = 2,
+                 reps: int = 5) -> dict:
+    """The reference's CPU path on the configuration's whole tensor set:
+    ``clip_grad_norm_`` (the clip configurations) and ``torch.optim.AdamW(foreach=False)``,
+    with torch's intra-op threads set to the host's physical cores.
+
+    The set is streamed through one host pool of at most `batch_params` parameters
+    (p, grad, exp_avg, exp_avg_sq in fp32: 16 B each; 8 GiB by default), so that a
+    6.7B set runs on a host with far less than its 110 GB: the tensors are taken in
+    model order in batches that fit the pool, every batch's tensors are views of the
+    pool at their real shapes, and the step time is the sum over batches of the
+    per-batch medians (`warmup` untimed, then `reps` timed repetitions).  Per batch and
+    repetition the clip is timed as its two halves: ``get_total_norm`` of the batch's
+    gradients (clip_grad.py:50-117) and ``clip_grads_with_norm_`` (:121-183), given a
+    total norm below max_norm so the coefficient is exactly 1: the multiply costs the
+    same as with a real coefficient, and the reused gradients keep their size instead
+    of shrinking towards denormals (which would slow the CPU).  The CPU path keeps
+    fp32 moments and writes no bf16 copy: it moves 32 B per parameter with the clip,
+    28 without, and ``value`` counts those bytes."""
     from mi_adamw.workloads import SHAPES
     shape_name, clip, state, copy, flat, start_step, gstd = CONFIGS[name]
-    tensors = SHAPES[shape_name].tensors()
-    # Bounded sample: whole tensors in model order up to ~170M parameters.
-    limit = 170_000_000
-    chosen, n = [], 0
-    for _, s in tensors:
-        k = 1
-        for d in s:
-            k *= d
-        if n + k > limit and chosen:
-            continue
-        chosen.append(s)
-        n += k
-    threads = torch.get_num_threads()
+    tensors = [s for _, s in SHAPES[shape_name].tensors()]
+    numels = [math.prod(s) for s in tensors]
+    info = host_cpu()
+    threads = info["physical_cores"] or info["affinity_cpus"]
+    torch.set_num_threads(threads)
+    batches, cur, n_cur = [], [], 0
+    for i, k in enumerate(numels):
+        if cur and n_cur + k > batch_params:
+            batches.append(cur)
+            cur, n_cur = [], 0
+        cur.append(i)
+        n_cur += k
+    batches.append(cur)
+    pool_n = max(sum(numels[i] for i in b) for b in batches)
     gen = torch.Generator().manual_seed(0)
-    params = [torch.nn.Parameter(torch.randn(s, generator=gen).mul_(0.02)) for s in chosen]
-    for p in params:
-        p.grad = torch.randn(p.shape, generator=gen).mul_(gstd)
-    opt = torch.optim.AdamW(params, **HP, foreach=False)
-    if start_step:
-        for p in params:
-            opt.state[p]["step"] = torch.tensor(float(start_step))
-            opt.state[p]["exp_avg"] = torch.randn(p.shape, generator=gen).mul_(1e-3)
-            opt.state[p]["exp_avg_sq"] = torch.randn(p.shape, generator=gen).mul_(1e-6).abs_()
-
-    def one():
-        if clip:
-            torch.nn.utils.clip_grad_norm_(params, 1.0)
-        opt.step()
-    for _ in range(2):
-        one()
-    times = []
-    t_start = time.perf_counter()
-    while len(times) < 5 or (time.perf_counter() - t_start < budget_s and len(times) < 200):
-        t0 = time.perf_counter()
-        one()
-        times.append(time.perf_counter() - t0)
-    ms = statistics.median(times) * 1e3
+    pool = {"p": torch.randn(pool_n, generator=gen).mul_(0.02),
+            "g": torch.randn(pool_n, generator=gen).mul_(gstd),
+            "m": torch.randn(pool_n, generator=gen).mul_(1e-3),
+            "v": torch.randn(pool_n, generator=gen).mul_(1e-6).abs_()}
+    below = torch.tensor(0.5)            # a total norm under max_norm 1.0: coefficient 1
+    total_ms, reps_done = 0.0, 0
+    for b in batches:
+        params, off = [], 0
+        for i in b:
+            k = numels[i]
+            p = torch.nn.Parameter(pool["p"][off:off + k].view(tensors[i]))
+            p.grad = pool["g"][off:off + k].view(tensors[i])
+            params.append((p, off, k))
+            off += k
+        opt = torch.optim.AdamW([p for p, _, _ in params], **HP, foreach=False)
+        for p, o, k in params:
+            opt.state[p] = {"step": torch.tensor(float(start_step)),
+                            "exp_avg": pool["m"][o:o + k].view(p.shape),
+                            "exp_avg_sq": pool["v"][o:o + k].view(p.shape)}
+        ps = [p for p, _, _ in params]
+        times = []
+        for r in range(warmup + reps):
+            t0 = time.perf_counter()
+            if clip:
+                torch.nn.utils.get_total_norm([p.grad for p in ps])
+                torch.nn.utils.clip_grads_with_norm_(ps, 1.0, below)
+            opt.step()
+            times.append(time.perf_counter() - t0)
+        total_ms += statistics.median(times[warmup:]) * 1e3
+        reps_done = reps
+        del opt, params, ps
+    del pool
+    n = sum(numels)
     total_b, _ = bytes_per_param(clip, "fp32", False)
+    info["torch_threads"] = torch.get_num_threads()
     return {
-        "value": round(total_b * n / ms / 1e6, 2), "unit": "GB/s", "cores": threads,
-        "kind": "reference", "ms_per_step": round(ms, 2), "params_per_s": round(n / ms * 1e3, 1),
-        "host": host_cpu(),
-        "sample": f"torch.optim.AdamW(foreach=False){' after clip_grad_norm_' if clip else ''} "
-                  f"on CPU, {len(params)} tensors / {n} params of {shape_name} (fp32 state), "
-                  f"median of {len(times)} steps after 2 warm-up",
+        "value": round(total_b * n / total_ms / 1e6, 2), "unit": "GB/s", "cores": threads,
+        "kind": "reference", "ms_per_step": round(total_ms, 4),
+        "params_per_s": round(n / total_ms * 1e3, 1), "host": info,
+        "sample": f"torch.optim.AdamW(foreach=False)"
+                  f"{' after clip_grad_norm_ (get_total_norm + clip_grads_with_norm_)' if clip else ''}"
+                  f" on the CPU over the whole {shape_name} set ({len(tensors)} tensors, {n} "
+                  f"params), fp32 moments, no bf16 copy ({total_b} B/param); "
+                  f"{'streamed in ' + str(len(batches)) + ' batches of whole tensors through one ' if len(batches) > 1 else 'one '}"
+                  f"{pool_n * 16 / 2**30:.1f} GiB host pool; per batch {warmup} warm-up + median of "
+                  f"{reps_done} repetitions, summed over batches",
     }
 
 
@@ -352,6 +414,15 @@ def load_traffic(name: str):
     return None if entry is None else entry.get("bytes_per_launch")
 
 
+def describe(name: str) -> str:
+    shape_name, clip, state, copy, flat, start_step, gstd = CONFIGS[name]
+    parts = [f"{shape_name}", "flat buffer" if flat else "per-tensor tables",
+             "bf16 moments" if state == "bf16" else "fp32 moments"]
+    if copy:
+        parts.append("bf16 copy")
+    return ", ".join(parts) + (": fused clip + AdamW step" if clip else ": AdamW step")
+
+
 def run_config(name: str, steps: int, warmup: int, device, with_context: bool,
                capturable: bool = False, write_grads: bool = False) -> dict:
     shape_name, clip, state, copy, flat, start_step, gstd = CONFIGS[name]
@@ -368,29 +439,75 @@ def run_config(name: str, steps: int, warmup: int, device, with_context: bool,
     norm_avg = statistics.mean(norm_ms) if clip else 0.0
     step_bytes = total_b * n
     achieved_upd = upd_b * n / upd_avg / 1e6
+    probe_gbs = None if probe_ms is None else upd_b * n / probe_ms / 1e6
+    # the PMC figures in profiles/ are for the default chain's update kernel, without
+    # the clipped-gradient store
+    traffic = None if capturable or write_grads else load_traffic(name)
     res = {
-        "config": name, "params": n, "tensors": n_tensors, "ms_per_step": gpu_ms,
-        "wall_ms_per_step": wall_ms, "bytes_per_step": step_bytes,
-        "gbs": step_bytes / gpu_ms / 1e6, "params_per_s": n / gpu_ms * 1e3,
+        "config": name, "workload": describe(name), "params": n, "tensors": n_tensors,
+        "state": state, "bf16_copy": copy, "flat_buffer": flat, "clip": clip,
+        "dtype": "f32", "ms_per_step": gpu_ms, "wall_ms_per_step": wall_ms,
+        "bytes_per_param": total_b, "bytes_per_step": step_bytes,
+        "gbs": step_bytes / gpu_ms / 1e6, "pct_of_peak": 100 * step_bytes / gpu_ms / 1e6 / PEAK_HBM_GBS,
+        "params_per_s": n / gpu_ms * 1e3,
         "norm_kernel_ms": norm_avg, "update_kernel_ms": upd_avg,
         "update_kernel_ms_p90": _pct(upd_ms, 0.9),
         "step_ms_median": statistics.median(step_ms), "step_ms_p90": _pct(step_ms, 0.9),
-        "update_bytes_per_launch": upd_b * n, "update_gbs": achieved_upd,
-        "probe_ms": probe_ms,
-        "probe_gbs": None if probe_ms is None else upd_b * n / probe_ms / 1e6,
-        "dtype": "f32" if state == "fp32" else "f32 math, bf16 moments",
+        "roofline": {
+            "bound": "hbm", "achieved": achieved_upd, "peak": PEAK_HBM_GBS, "unit": "GB/s",
+            "frac": achieved_upd / PEAK_HBM_GBS, "traffic": traffic,
+            "kernel": "mi_adamw_update_kernel", "bytes_per_launch": upd_b * n,
+            # the same launch with the arithmetic left out, on the same tensors, right
+            # after the timed region: the bandwidth this read/write mix gets here
+            "mix_probe": None if probe_ms is None else {
+                "achieved": probe_gbs, "frac": probe_gbs / PEAK_HBM_GBS,
+                "update_vs_probe": achieved_upd / probe_gbs,
+                "step_vs_probe_ceiling": (norm_avg + probe_ms) / gpu_ms,
+            },
+        },
     }
     log(f"[bench] {name}: {gpu_ms:.4f} ms/step, {res['gbs']:.1f} GB/s "
-        f"({100 * res['gbs'] / PEAK_HBM_GBS:.1f}% of peak); update {upd_avg:.4f} ms "
+        f"({res['pct_of_peak']:.1f}% of peak); update {upd_avg:.4f} ms "
         f"({achieved_upd:.1f} GB/s), norm {norm_avg:.4f} ms"
         + ("" if probe_ms is None else
-           f"; memory-only probe {probe_ms:.4f} ms ({res['probe_gbs']:.1f} GB/s)"))
+           f"; memory-only probe {probe_ms:.4f} ms ({probe_gbs:.1f} GB/s)"))
     del params, opt
     torch.cuda.empty_cache()
     if with_context:
-        res["torch_gpu"] = torch_gpu_rows(name, device)
-        log(f"[bench] {name}: torch GPU context {res['torch_gpu']}")
+        res["torch_gpu_ms"] = torch_gpu_rows(name, device)
+        log(f"[bench] {name}: torch GPU context {res['torch_gpu_ms']}")
     return res
+
+
+def host_step_us(device, n_tensors: int, steps: int = 300) -> dict:
+    """Host time of FusedAdamW.step() (enqueue only) with gradients that move every step,
+    as after mini-megatron's zero_grad() (main.py:204): n_tensors small fp32 tensors, the
+    clip on, three gradient sets in rotation.  Median and p90 in microseconds."""
+    import mi_adamw
+    params = [torch.nn.Parameter(torch.randn(4096, device=device)) for _ in range(n_tensors)]
+    sets = [[torch.randn_like(p) for p in params] for _ in range(3)]
+    opt = mi_adamw.FusedAdamW(params, **HP, max_grad_norm=1.0)
+    ts = []
+    for k in range(steps + 30):
+        for p, g in zip(params, sets[k % 3]):
+            p.grad = g
+        t0 = time.perf_counter()
+        opt.step()
+        ts.append(time.perf_counter() - t0)
+        if k % 50 == 49:
+            torch.cuda.synchronize()
+    torch.cuda.synchronize()
+    ts = sorted(ts[30:])
+    return {"tensors": n_tensors, "median_us": round(ts[len(ts) // 2] * 1e6, 1),
+            "p90_us": round(_pct(ts, 0.9) * 1e6, 1)}
+
+
+def _rounded(x):
+    if isinstance(x, float):
+        return round(x, 5)
+    if isinstance(x, dict):
+        return {k: _rounded(v) for k, v in x.items()}
+    return x
 
 
 def main() -> int:
@@ -399,9 +516,16 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--config", default=DEFAULT_CONFIG,
-                    help="one of %s, or 'all'" % ", ".join(CONFIGS))
-    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+                    help="headline configuration, one of %s" % ", ".join(CONFIGS))
+    ap.add_argument("--sweep", default=",".join(DEFAULT_SWEEP),
+                    help="comma-separated configurations timed in the same run as rows of "
+                         "`sweep` ('all' for every other configuration, 'none' for none)")
+    ap.add_argument("--cpu", default=",".join(DEFAULT_CPU),
+                    help="configurations whose CPU baseline is timed (the headline's goes to "
+                         "`cpu_baseline`, the others to their sweep rows)")
+    ap.add_argument("--no-cpu", action="store_true", help="skip every CPU baseline")
     ap.add_argument("--no-context", action="store_true", help="skip torch's GPU rows")
+    ap.add_argument("--no-host", action="store_true", help="skip the step() host-time rows")
     ap.add_argument("--training", action="store_true",
                     help="also time gpt-125m training iterations (bf16 autocast) with torch's "
                          "per-tensor and fused AdamW, FusedAdamW, and FusedAdamW + bf16_weights")
@@ -425,23 +549,33 @@ def main() -> int:
     if not torch.cuda.is_available():
         print("bench.py needs a ROCm GPU", file=sys.stderr)
         return 2
+    if args.config not in CONFIGS:
+        print(f"unknown configuration {args.config!r}", file=sys.stderr)
+        return 2
     device = torch.device("cuda", 0)
     import mi_adamw
     log(f"[bench] {mi_adamw.version()} on {torch.cuda.get_device_name(0)}")
 
-    names = list(CONFIGS) if args.config == "all" else [args.config]
+    sweep = {"all": [nm for nm in CONFIGS if nm != args.config], "none": []}.get(
+        args.sweep, [nm for nm in args.sweep.split(",") if nm and nm != args.config])
+    for nm in sweep:
+        if nm not in CONFIGS:
+            print(f"unknown configuration {nm!r}", file=sys.stderr)
+            return 2
+    names = [args.config] + sweep
     if args.clip_write_grads:
         names = [nm for nm in names if CONFIGS[nm][1]]
-        if not names:
-            print("--clip-write-grads needs a configuration with the clip", file=sys.stderr)
+        if args.config not in names:
+            print("--clip-write-grads needs a headline configuration with the clip",
+                  file=sys.stderr)
             return 2
     if args.capturable:
         import warnings
         warnings.filterwarnings("ignore", message="This instance was constructed with capturable")
-    results = [run_config(nm, args.steps, args.warmup, device,
-                          with_context=not args.no_context and nm == names[0],
-                          capturable=args.capturable, write_grads=args.clip_write_grads)
-               for nm in names]
+    results = {nm: run_config(nm, args.steps, args.warmup, device,
+                              with_context=not args.no_context and nm == args.config,
+                              capturable=args.capturable, write_grads=args.clip_write_grads)
+               for nm in names}
     if args.calibrate_copy:
         src = torch.ones(1 << 28, device=device)
         dst = torch.empty_like(src)
@@ -449,11 +583,8 @@ def main() -> int:
             dst.copy_(src)
         torch.cuda.synchronize()
         del src, dst
-    head = results[0]
-    shape_name, clip, state, copy, flat, start_step, gstd = CONFIGS[head["config"]]
-    # the PMC figures in profiles/ are for the default chain's update kernel, without
-    # the clipped-gradient store
-    traffic = None if args.capturable or args.clip_write_grads else load_traffic(head["config"])
+    head = results[args.config]
+    shape_name, clip, state, copy, flat, start_step, gstd = CONFIGS[args.config]
     line = {
         "metric": METRIC,
         "value": round(head["gbs"], 2),
@@ -465,49 +596,36 @@ def main() -> int:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f32",
+        "dtype": head["dtype"],
         "data": "synthetic: seeded N(0, 0.02) params (LayerNorm 1/0), resident seeded grads, "
                 "mid-training moments",
         "config": {
-            "workload": f"{shape_name} fused clip+AdamW step" if clip else f"{shape_name} AdamW step",
+            "workload": head["workload"],
             "params": head["params"], "tensors": head["tensors"],
-            "state": state, "bf16_copy": copy, "flat_buffer": flat, "clip_max_norm": 1.0 if clip else None,
+            "state": state, "bf16_copy": copy, "flat_buffer": flat,
+            "clip_max_norm": 1.0 if clip else None,
             "stored_step": start_step, "lr": HP["lr"], "betas": list(HP["betas"]),
             "eps": HP["eps"], "weight_decay": HP["weight_decay"],
-            "bytes_per_step": head["bytes_per_step"],
+            "bytes_per_param": head["bytes_per_param"], "bytes_per_step": head["bytes_per_step"],
             **({"capturable": True} if args.capturable else {}),
             **({"clip_write_grads": True} if args.clip_write_grads else {}),
         },
-        "pct_of_peak": round(100 * head["gbs"] / PEAK_HBM_GBS, 2),
+        "pct_of_peak": round(head["pct_of_peak"], 2),
         "params_per_s": round(head["params_per_s"], 1),
         "wall_ms_per_step": round(head["wall_ms_per_step"], 5),
         "kernels_ms": {"grad_norm": round(head["norm_kernel_ms"], 5),
                        "update": round(head["update_kernel_ms"], 5)},
         "step_ms_median": round(head["step_ms_median"], 5),
         "step_ms_p90": round(head["step_ms_p90"], 5),
-        "roofline": {
-            "bound": "hbm",
-            "achieved": round(head["update_gbs"], 2),
-            "peak": PEAK_HBM_GBS,
-            "unit": "GB/s",
-            "frac": round(head["update_gbs"] / PEAK_HBM_GBS, 4),
-            "traffic": traffic,
-            "kernel": "mi_adamw_update_kernel",
-            "bytes_per_launch": head["update_bytes_per_launch"],
-            # the same launch with the arithmetic left out, on the same tensors, right
-            # after the timed region: the bandwidth this read/write mix gets here
-            "mix_probe": None if head["probe_ms"] is None else {
-                "achieved": round(head["probe_gbs"], 2),
-                "frac": round(head["probe_gbs"] / PEAK_HBM_GBS, 4),
-                "update_vs_probe": round(head["update_gbs"] / head["probe_gbs"], 4),
-            },
-        },
+        "roofline": _rounded(head["roofline"]),
     }
-    if "torch_gpu" in head:
-        line["torch_gpu_ms"] = head["torch_gpu"]
-    if len(results) > 1:
-        line["sweep"] = [{k: (round(v, 5) if isinstance(v, float) else v) for k, v in r.items()
-                          if k != "torch_gpu"} for r in results]
+    if "torch_gpu_ms" in head:
+        line["torch_gpu_ms"] = head["torch_gpu_ms"]
+    if sweep:
+        line["sweep"] = [_rounded(results[nm]) for nm in names if nm != args.config]
+    if not args.no_host:
+        line["host_step_us_moving_grads"] = [host_step_us(device, n) for n in (101, 261)]
+        log(f"[bench] step() host time {line['host_step_us_moving_grads']}")
     if args.training:
         log("[bench] gpt-125m training iterations by optimizer")
         # the reference's micro-batch (config.py:9) with every optimizer, then a GPU-bound
@@ -521,9 +639,16 @@ def main() -> int:
         for row in line["training"]:
             log(f"[bench] {row}")
     if not args.no_cpu:
-        log("[bench] CPU baseline (torch.optim.AdamW foreach=False on host cores)")
-        line["cpu_baseline"] = cpu_baseline(head["config"])
-        log(f"[bench] CPU baseline {line['cpu_baseline']}")
+        for nm in [nm for nm in args.cpu.split(",") if nm in results]:
+            log(f"[bench] CPU baseline of {nm} (torch.optim.AdamW foreach=False on host cores)")
+            cb = cpu_baseline(nm)
+            log(f"[bench] CPU baseline of {nm}: {cb}")
+            if nm == args.config:
+                line["cpu_baseline"] = cb
+            else:
+                for row in line.get("sweep", []):
+                    if row["config"] == nm:
+                        row["cpu_baseline"] = cb
     print(json.dumps(line), flush=True)
     return 0
 

@@ -471,14 +471,45 @@ def test_bench_bytes_per_parameter():
     spec.loader.exec_module(bench)
     expected = {"125m-step1": 28, "125m-clip": 32, "350m-master-clip-copy": 34,
                 "1.3b-bf16state-copy": 22, "1.3b-bf16state-copy-clip": 26,
-                "6.7b-flat-clip-copy": 34}
+                "1.3b-bf16state-copy-clip-flat": 26, "6.7b-flat-clip-copy": 34}
     assert set(expected) == set(bench.CONFIGS)
+    # the headline is the largest configuration, and every other one is in the default sweep
+    assert bench.DEFAULT_CONFIG == "6.7b-flat-clip-copy"
+    assert set(bench.DEFAULT_SWEEP) | {bench.DEFAULT_CONFIG} == set(bench.CONFIGS)
+    assert set(bench.DEFAULT_CPU) <= set(bench.CONFIGS)
     for name, total in expected.items():
         _, clip, state, copy, *_ = bench.CONFIGS[name]
         step, update = bench.bytes_per_param(clip, state, copy)
         assert step == total and update == total - (4 if clip else 0), name
         step_w, update_w = bench.bytes_per_param(clip, state, copy, write_grads=True)
         assert (step_w, update_w) == (step + 4, update + 4), name
+
+
+def test_bench_cpu_host_record_and_streamed_baseline():
+    """The CPU baseline's host record (physical and logical cores from /proc/cpuinfo) and
+    the streamed full-set timing on a small set, with a pool smaller than the set."""
+    import importlib.util
+    spec = importlib.util.spec_from_file_location("bench_under_test", os.path.join(ROOT, "bench.py"))
+    bench = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(bench)
+    info = bench.host_cpu()
+    assert info["affinity_cpus"] >= 1 and info["logical_cpus"] >= info["physical_cores"] >= 1
+    from mi_adamw.workloads import GPTShape, SHAPES
+    threads = torch.get_num_threads()
+    try:
+        SHAPES["gpt-tiny"] = GPTShape("gpt-tiny", layers=2, hidden=64, heads=2, ffn=256,
+                                      vocab=1000, positions=128)
+        bench.CONFIGS["tiny-clip"] = ("gpt-tiny", True, "fp32", False, False, 1000, 1e-2)
+        n = SHAPES["gpt-tiny"].numel()
+        cb = bench.cpu_baseline("tiny-clip", batch_params=70_000, warmup=1, reps=2)
+    finally:
+        SHAPES.pop("gpt-tiny", None)
+        bench.CONFIGS.pop("tiny-clip", None)
+        torch.set_num_threads(threads)
+    assert cb["kind"] == "reference" and cb["unit"] == "GB/s" and cb["value"] > 0
+    assert cb["cores"] == (info["physical_cores"] or info["affinity_cpus"])
+    assert f"{n} params" in cb["sample"] and "streamed in" in cb["sample"]
+    assert abs(cb["params_per_s"] - n / cb["ms_per_step"] * 1e3) <= 1e-3 * cb["params_per_s"]
 
 
 def test_step_hooks_and_scheduler_see_step():
