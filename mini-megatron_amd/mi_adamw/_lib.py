@@ -3,8 +3,10 @@
 The library is loaded after torch has initialised HIP, so that its
 libamdhip64 dependency resolves to the HIP runtime torch already mapped and
 the device pointers and stream handles torch hands out are valid in it.
-There is no CPU fallback: if the library is missing or was built for another
-ABI, loading raises.
+The host extension ``_host`` (csrc/host.cpp: FusedAdamW.step()'s steady-state
+bookkeeping in C++) is imported with it and bound to the same library's entry
+points.  There is no CPU fallback: if either is missing or was built for
+another ABI, loading raises.
 """
 from __future__ import annotations
 
@@ -156,6 +158,12 @@ _SIGNATURES = {
 }
 
 _lib = None
+_host = None
+
+# The entry points the host extension calls, in the order _host.bind takes them.
+HOST_BINDINGS = ("mi_adamw_set_grads", "mi_adamw_grad_norm", "mi_adamw_grad_norm_flat",
+                 "mi_adamw_grad_sumsq", "mi_adamw_grad_sumsq_flat", "mi_adamw_norm_from_sumsq",
+                 "mi_adamw_step_prescaled", "mi_adamw_step_flat_prescaled")
 
 
 class MiAdamwError(RuntimeError):
@@ -183,8 +191,24 @@ def load(path: str = LIB_PATH) -> ctypes.CDLL:
     version = lib.mi_adamw_version().decode()
     if not version.startswith(f"mi_adamw {ABI_VERSION} "):
         raise MiAdamwError(f"libmi_adamw ABI mismatch: library reports {version!r}")
+    global _host
+    try:
+        from . import _host as host
+    except ImportError as e:
+        raise MiAdamwError(
+            f"mi_adamw's host extension (_host) is not built or does not load ({e}); build it "
+            "with `python -m mi_adamw.build` against the installed torch") from e
+    host.bind(*(ctypes.cast(getattr(lib, name), ctypes.c_void_p).value
+                for name in HOST_BINDINGS))
+    _host = host
     _lib = lib
     return lib
+
+
+def host():
+    """The bound host extension (loads the library first)."""
+    load()
+    return _host
 
 
 def strerror(code: int) -> str:

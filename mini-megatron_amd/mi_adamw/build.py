@@ -1,8 +1,10 @@
-"""Compile libmi_adamw.so for gfx950 from csrc/ with hipcc, in place.
+"""Compile libmi_adamw.so for gfx950 from csrc/ with hipcc, and the host
+extension _host from csrc/host.cpp with g++, in place.
 
 Run as ``python -m mi_adamw.build`` (with ``mini-megatron_amd`` on sys.path)
-or through ``__graft_entry__.build()``.  The library lands next to this file,
-where ``mi_adamw._lib`` loads it from.
+or through ``__graft_entry__.build()``.  Both land next to this file, where
+``mi_adamw._lib`` loads them from.  The host extension is built against the
+installed torch (its headers and libtorch_python), whose C++ ABI it must match.
 """
 from __future__ import annotations
 
@@ -10,12 +12,15 @@ import os
 import shutil
 import subprocess
 import sys
+import sysconfig
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 REPO = os.path.dirname(os.path.dirname(HERE))
 SOURCES = [os.path.join(HERE, "csrc", "mi_adamw.hip")]
 INCLUDE = os.path.join(REPO, "include")
 OUTPUT = os.path.join(HERE, "libmi_adamw.so")
+HOST_SOURCE = os.path.join(HERE, "csrc", "host.cpp")
+HOST_OUTPUT = os.path.join(HERE, "_host" + sysconfig.get_config_var("EXT_SUFFIX"))
 
 # -ffp-contract=off: the kernels spell out every fused multiply-add themselves,
 #   in the places torch-ROCm's kernels fuse, so the compiler must not add more.
@@ -40,16 +45,40 @@ def hipcc() -> str:
     return path
 
 
-def build(verbose: bool = False) -> str:
-    """Compile every source into libmi_adamw.so; returns the library path."""
-    tmp = OUTPUT + ".tmp"
-    cmd = [hipcc(), *HIPCC_FLAGS, "-I", INCLUDE, *SOURCES, "-o", tmp]
+def _run(cmd: list[str], verbose: bool, what: str) -> None:
     if verbose:
         print(" ".join(cmd), flush=True)
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
-        raise RuntimeError(f"hipcc failed ({res.returncode}):\n{res.stdout}\n{res.stderr}")
+        raise RuntimeError(f"{what} failed ({res.returncode}):\n{res.stdout}\n{res.stderr}")
+
+
+def host_command(output: str) -> list[str]:
+    """g++ line of the host extension: torch's headers and C++ ABI, Python's headers."""
+    import torch
+    tdir = os.path.dirname(torch.__file__)
+    tlib = os.path.join(tdir, "lib")
+    abi = int(torch._C._GLIBCXX_USE_CXX11_ABI)
+    gxx = shutil.which("g++") or "g++"
+    return [gxx, "-O2", "-std=c++17", "-fPIC", "-shared", "-Wall", "-Wno-unused-function",
+            f"-D_GLIBCXX_USE_CXX11_ABI={abi}",
+            "-I", os.path.join(tdir, "include"),
+            "-I", os.path.join(tdir, "include", "torch", "csrc", "api", "include"),
+            "-I", sysconfig.get_paths()["include"], "-I", INCLUDE,
+            HOST_SOURCE, "-o", output,
+            "-L", tlib, "-ltorch_python", "-ltorch", "-ltorch_cpu", "-lc10",
+            f"-Wl,-rpath,{tlib}"]
+
+
+def build(verbose: bool = False) -> str:
+    """Compile the kernels into libmi_adamw.so and the host extension; returns the
+    library path."""
+    tmp = OUTPUT + ".tmp"
+    _run([hipcc(), *HIPCC_FLAGS, "-I", INCLUDE, *SOURCES, "-o", tmp], verbose, "hipcc")
     os.replace(tmp, OUTPUT)
+    tmp = HOST_OUTPUT + ".tmp"
+    _run(host_command(tmp), verbose, "g++ (host extension)")
+    os.replace(tmp, HOST_OUTPUT)
     return OUTPUT
 
 

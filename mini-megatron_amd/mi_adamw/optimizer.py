@@ -223,6 +223,14 @@ class _Launch:
             self.rows = _upload(rows, device)
 
 
+class _Fast:
+    """What the native host path needs to take the next steps: the plan (_host.plan) and
+    the Python objects whose identity says the plan still describes this optimizer."""
+
+    __slots__ = ("plan", "cache", "steps", "state", "groups_key", "options", "hyper_group",
+                 "hyper_steps", "harr", "harr_addr", "clip", "device", "dev_index")
+
+
 class FusedAdamW(Optimizer):
     """AdamW with the whole step fused into one MI355X kernel launch (three with the
     global-norm clip: sum of squares, finalize, update).
@@ -376,6 +384,8 @@ class FusedAdamW(Optimizer):
         self._flat: FlatLayout | None = None
         self._copy_sync: dict[int, tuple[int, int]] | None = None
         self._step_idx: tuple[tuple, torch.Tensor] | None = None
+        self._fast: _Fast | None = None
+        self.native_steps = 0          # steps taken by the native host path
         self.timing_events = None
 
     # ------------------------------------------------------------------ torch API
@@ -687,10 +697,20 @@ class FusedAdamW(Optimizer):
             self._launch_cache = None
         return self._recs
 
-    @torch.no_grad()
     def step(self, closure=None):
-        """One optimizer step (adam.py:214-272), fused.  Returns closure's loss."""
+        """One optimizer step (adam.py:214-272), fused.  Returns closure's loss.
+
+        After a step that built the launch tables, the steps that follow go through the
+        native host path (``_host``) while nothing but the gradient addresses changes;
+        anything else takes the general path below, which rebuilds what changed."""
         self._cuda_graph_capture_health_check()
+        fast = self._fast
+        if closure is None and fast is not None and self._fast_step(fast):
+            return None
+        return self._step(closure)
+
+    @torch.no_grad()
+    def _step(self, closure):
         loss = None
         if closure is not None:
             with torch.enable_grad():
@@ -764,9 +784,11 @@ class FusedAdamW(Optimizer):
                     hyper_idx.append(h)
             hypers = [_hyper(self.param_groups[gi], step) for (gi, step) in keys]
             hyper_ams = [ams_g[gi] for (gi, _) in keys]
+            hyper_group = [gi for (gi, _) in keys]
 
         with torch.cuda.device(device):
-            self._launch(entries, hyper_idx, hypers, hyper_ams, device)
+            self._launch(entries, hyper_idx, hypers, hyper_ams, device,
+                         None if self.capturable else hyper_group)
         if self._copy_sync is not None:
             # the launch wrote these masters' copies
             for rec, _ in entries:
@@ -793,6 +815,123 @@ class FusedAdamW(Optimizer):
             self._steps[slot] = float(step.item()) if isinstance(step, torch.Tensor) else float(step)
         self._step_views[slot] = self._steps[slot]
         st["step"] = self._step_views[slot]
+
+    # ------------------------------------------------------------------ native path
+
+    def _options_key(self) -> tuple:
+        return (self.max_grad_norm, self.clip_write_grads, self.grad_prescale, self.max_blocks,
+                self.chunk_elems, self.bf16_copy, self.state_dtype)
+
+    def _groups_key(self) -> tuple:
+        return tuple((id(g["params"]), len(g["params"]), bool(g["amsgrad"]))
+                     for g in self.param_groups)
+
+    def _make_fast(self, entries, hyper_idx, hyper_group, ams, launch, device, stream, partials,
+                   coef, state_code, flags):
+        """The native path's plan for the steps after this one, when this step's launch is
+        one the native path can repeat: every parameter stepped, one launch that the norm
+        pass shares, one hyperparameter set per param group."""
+        if (len(set(hyper_group)) != len(hyper_group) or launch.n_chunks == 0
+                or len(entries) != len(self._records())
+                or not self._steps.is_contiguous() or self._steps.device.type != "cpu"):
+            return None
+        host = _lib.host()
+        n = len(entries)
+        if self._flat is not None:
+            rows = [-2] * n          # gradients are views of the flat buffer: they must stay
+            rest = [True] * n
+        else:
+            rows, rest = [-1] * n, [False] * n
+            for r, i in enumerate(launch.src.tolist()):
+                rows[i] = r
+                rest[i] = bool(launch.rest[r])
+        hyper_steps = np.zeros(len(hyper_group), dtype=np.float64)
+        flat_row = None if launch.tables else self._row_struct(launch)
+        if ams:
+            flags |= _lib.F_AMSGRAD
+        sumsq = self._sumsq_buf(device) if self.grad_prescale != 1.0 else None
+        clip = self.max_grad_norm is not None
+        if not clip:
+            flags &= ~_lib.F_WRITE_GRAD
+        try:
+            plan = host.plan(
+                [rec.p for rec, _ in entries], [rec.st for rec, _ in entries],
+                [rec.slot for rec, _ in entries], [int(h) for h in hyper_idx], rows, rest,
+                [g.data_ptr() for _, g in entries], bool(ams),
+                (self._steps.data_ptr(), self._steps.numel()),
+                (hyper_steps.ctypes.data, len(hyper_group)),
+                (bool(launch.tables), 0 if launch.rows is None else launch.rows.data_ptr(),
+                 0 if launch.chunks is None else launch.chunks.data_ptr(), int(launch.n_chunks),
+                 int(launch.n_rows), launch.host_rows.ctypes.data,
+                 0 if flat_row is None else ctypes.addressof(flat_row),
+                 0 if launch.tables else int(launch.host_rows[0]["hyper"])),
+                (int(self.chunk_elems), int(self.max_blocks), int(state_code), int(flags), clip,
+                 float(self.max_grad_norm or 0.0), float(self.grad_prescale),
+                 partials.data_ptr(), coef.data_ptr(), 0 if sumsq is None else sumsq.data_ptr(),
+                 int(stream)),
+                (launch.rows, launch.chunks, launch.host_rows, self._steps, hyper_steps,
+                 partials, coef, sumsq))
+        except (TypeError, ValueError):
+            return None     # a state entry the plan cannot check (not a tensor): general path
+        fast = _Fast()
+        fast.plan = plan
+        fast.cache = self._launch_cache
+        fast.steps = self._steps
+        fast.state = self.state
+        fast.groups_key = self._groups_key()
+        fast.options = self._options_key()
+        fast.hyper_group = list(hyper_group)
+        fast.hyper_steps = hyper_steps
+        fast.harr = (_lib.Hyper * len(hyper_group))()
+        fast.harr_addr = ctypes.addressof(fast.harr)
+        fast.clip = clip
+        fast.device = device
+        fast.dev_index = device.index if device.index is not None else torch.cuda.current_device()
+        return fast
+
+    def _fast_step(self, fast: _Fast) -> bool:
+        """One step through the native host path; False (nothing done) when it does not
+        apply, and the general path takes the step."""
+        if (self._launch_cache is not fast.cache or self._steps is not fast.steps
+                or self.state is not fast.state or self._options_key() != fast.options
+                or self._groups_key() != fast.groups_key):
+            return False
+        host = _lib._host
+        dev = fast.dev_index
+        if torch._C._cuda_getDevice() != dev:
+            with torch.cuda.device(dev):
+                return self._fast_launch(fast, host)
+        return self._fast_launch(fast, host)
+
+    def _fast_launch(self, fast: _Fast, host) -> bool:
+        stream = torch._C._cuda_getCurrentRawStream(fast.dev_index)
+        rc = host.prepare(fast.plan, stream)
+        if rc == host.FALLBACK:
+            return False
+        self.native_steps += 1
+        if rc == host.READY_MOVED:
+            fast.cache[4] = None      # the general path's record of the gradients is stale
+        elif rc != host.READY:
+            _lib.check(rc, "mi_adamw_set_grads")
+        groups = self.param_groups
+        harr = fast.harr
+        for h, gi in enumerate(fast.hyper_group):
+            harr[h] = _hyper(groups[gi], float(fast.hyper_steps[h]))
+        ev = self.timing_events
+        if ev is not None:
+            ev[0].record()
+        if fast.clip:
+            norm = torch.empty((), dtype=torch.float32, device=fast.device)
+            _lib.check(host.norm(fast.plan, stream, norm.data_ptr()), "mi_adamw_grad_norm")
+            self.last_grad_norm = norm
+        if ev is not None:
+            ev[1].record()
+        _lib.check(host.update(fast.plan, stream, fast.harr_addr, len(harr)), "mi_adamw_step")
+        if ev is not None:
+            ev[2].record()
+        if self._copy_sync is not None:
+            host.sync_versions(fast.plan, self._copy_sync)
+        return True
 
     # ------------------------------------------------------------------ launches
 
@@ -898,14 +1037,16 @@ class FusedAdamW(Optimizer):
         return self._copies[id(p)]
 
     @staticmethod
-    def _signature(entries, hyper_idx) -> tuple[list, list]:
-        """What a launch's tables encode, in two parts: the hyperparameter assignment
-        and the parameter and state pointers, which rarely change; and the gradient
-        pointers, which change whenever zero_grad() frees the gradients and backward
-        allocates them elsewhere."""
+    def _signature(entries, hyper_idx, hyper_ams) -> tuple[list, list]:
+        """What a launch's tables encode, in two parts: the hyperparameter assignment,
+        the amsgrad setting of each hyperparameter set (which decides how the entries
+        are split into launches), and the parameter and state pointers, which rarely
+        change; and the gradient pointers, which change whenever zero_grad() frees the
+        gradients and backward allocates them elsewhere."""
         sig = [(rec.p.data_ptr(), rec.st["exp_avg"].data_ptr(), rec.st["exp_avg_sq"].data_ptr(),
                 _ptr(rec.st.get("max_exp_avg_sq"))) for rec, _ in entries]
         sig.append(tuple(hyper_idx))
+        sig.append(tuple(bool(a) for a in hyper_ams))
         return sig, [g.data_ptr() for _, g in entries]
 
     @staticmethod
@@ -917,8 +1058,10 @@ class FusedAdamW(Optimizer):
                               max_exp_avg_sq=int(r["max_exp_avg_sq"]), numel=int(r["numel"]),
                               hyper=0, flags=int(r["flags"]))
 
-    def _launch(self, entries, hyper_idx, hypers, hyper_ams, device) -> None:
+    def _launch(self, entries, hyper_idx, hypers, hyper_ams, device,
+                hyper_group: list | None = None) -> None:
         lib = _lib.load()
+        self._fast = None
         stream = torch.cuda.current_stream(device).cuda_stream
         partials, coef = self._ws(device)
         flags = 0
@@ -947,7 +1090,7 @@ class FusedAdamW(Optimizer):
         # Tables: reused while the pointers and the hyperparameter assignment are
         # unchanged; when only the gradients moved, the rows are rewritten and the
         # chunk tables kept.
-        sig, grads = self._signature(entries, hyper_idx)
+        sig, grads = self._signature(entries, hyper_idx, hyper_ams)
         cache = self._launch_cache
         if cache is not None and cache[0] == sig and cache[1] == device:
             launches, norm_launch = cache[2], cache[3]
@@ -963,7 +1106,8 @@ class FusedAdamW(Optimizer):
                     launch.patch_grads(garr if part[4] is None else garr[part[4]], device)
                 if norm_launch is not launches[0]:
                     norm_launch.patch_grads(garr, device)
-                self._launch_cache = (sig, device, launches, norm_launch, grads)
+                # a list: the native path marks the gradients it moved (cache[4] = None)
+                self._launch_cache = [sig, device, launches, norm_launch, grads]
         else:
             _refuse_under_capture("the parameters, state or hyperparameter grouping changed")
             for rec, g in entries:
@@ -975,7 +1119,7 @@ class FusedAdamW(Optimizer):
                 norm_launch = launches[0]
             else:
                 norm_launch = self._new_launch(entries, [0] * len(entries), False, device)
-            self._launch_cache = (sig, device, launches, norm_launch, grads)
+            self._launch_cache = [sig, device, launches, norm_launch, grads]
 
         ev = self.timing_events
         if ev is not None:
@@ -1059,3 +1203,7 @@ class FusedAdamW(Optimizer):
                 self.max_blocks, stream), "mi_adamw_step")
         if ev is not None:
             ev[2].record()
+        if len(parts) == 1 and hyper_group is not None:
+            self._fast = self._make_fast(entries, hyper_idx, hyper_group, hyper_ams[0],
+                                         launches[0], device, stream, partials, coef,
+                                         state_code, flags & ~_lib.F_CLIP)
