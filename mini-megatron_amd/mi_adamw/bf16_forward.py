@@ -59,7 +59,10 @@ def _widen_on_gpu(srcs: list[torch.Tensor], device: torch.device) -> list[torch.
     rows = rows[rows["numel"] > 0]
     if len(rows) == 0:
         return dsts
-    key = (device, tuple(int(n) for n in rows["numel"]))
+    # Per stream: the tables are then allocated on the stream whose launches read them,
+    # so a replaced or dropped table returns to that stream's pool, ordered after them.
+    stream = torch.cuda.current_stream(device).cuda_stream
+    key = (device, stream, tuple(int(n) for n in rows["numel"]))
     launch = _widen_tables.get(key)
     if launch is None:
         if len(_widen_tables) > 8:
@@ -71,7 +74,7 @@ def _widen_on_gpu(srcs: list[torch.Tensor], device: torch.device) -> list[torch.
     with torch.cuda.device(device):
         _lib.check(lib.mi_adamw_widen_bf16(
             launch.rows.data_ptr(), launch.chunks.data_ptr(), launch.n_chunks, _WIDEN_CHUNK,
-            torch.cuda.current_stream(device).cuda_stream), "mi_adamw_widen_bf16")
+            stream), "mi_adamw_widen_bf16")
     return dsts
 
 

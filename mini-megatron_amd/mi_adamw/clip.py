@@ -39,10 +39,12 @@ def _ws(device, stream: int):
     return ws
 
 
-def _tables(grads, device):
+def _tables(grads, device, stream: int):
     """The tables of one gradient list.  The chunk table depends on the sizes only and is
-    cached by them; when the gradients moved (zero_grad freed them and backward allocated
-    them elsewhere) only the rows are rewritten."""
+    cached by them, per stream (so the tables are allocated on the stream whose launches
+    read them, and a replaced or dropped table returns to that stream's pool, ordered
+    after those launches); when the gradients moved (zero_grad freed them and backward
+    allocated them elsewhere) only the rows are rewritten."""
     from .optimizer import _ROW_DTYPE, _Launch
     rows = np.zeros(len(grads), dtype=_ROW_DTYPE)
     ptrs = np.array([g.data_ptr() for g in grads], dtype=np.uint64)
@@ -52,7 +54,7 @@ def _tables(grads, device):
     rows["numel"] = [g.numel() * (2 if torch.is_complex(g) else 1) for g in grads]
     rows["flags"] = np.where(ptrs % 16 == 0, _lib.T_VEC, 0)
     rows = rows[rows["numel"] > 0]
-    key = (device, tuple(int(n) for n in rows["numel"]))
+    key = (device, stream, tuple(int(n) for n in rows["numel"]))
     launch = _cache.get(key)
     if launch is not None:
         if not np.array_equal(launch.host_rows["grad"], rows["grad"]):
@@ -86,8 +88,8 @@ def clip_grad_norm_(parameters, max_norm: float, norm_type: float = 2.0,
     lib = _lib.load()
     norm = torch.empty((), dtype=torch.float32, device=device)
     with torch.cuda.device(device):
-        launch = _tables(grads, device)
         stream = torch.cuda.current_stream(device).cuda_stream
+        launch = _tables(grads, device, stream)
         partials, coef = _ws(device, stream)
         if launch.n_chunks == 0:
             norm.zero_()

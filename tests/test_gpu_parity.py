@@ -241,6 +241,32 @@ def test_clip_grad_norm_on_two_streams(dev):
             assert close_rel(q.grad, p.grad, 1e-6, 1e-12) <= 1.0
 
 
+def test_clip_grad_norm_same_sizes_on_two_streams(dev):
+    """Gradient lists of the same sizes, clipped on two streams with no ordering between
+    them, twice (the second round rewrites the rows): each stream has its own tables, so
+    neither call reads or frees rows the other is using."""
+    import mi_adamw
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    for rnd in range(2):
+        sets = []
+        for k in range(2):
+            ref = make_params(MINI_SHAPES, dev, seed=1000 + 100 * k + 10 * rnd)
+            set_grads(ref, 3 * rnd + k, 1e-2 * (k + 1))
+            sets.append((ref, clone_params(ref)))
+        for s_ in streams:
+            s_.wait_stream(torch.cuda.current_stream())
+        norms = []
+        for (ref, ours), s_ in zip(sets, streams):
+            with torch.cuda.stream(s_):
+                norms.append(mi_adamw.clip_grad_norm_(ours, 1.0))
+        torch.cuda.synchronize()
+        for (ref, ours), on in zip(sets, norms):
+            tn = torch.nn.utils.clip_grad_norm_(ref, 1.0)
+            assert rel_err(on, tn) <= 1e-6
+            for p, q in zip(ref, ours):
+                assert close_rel(q.grad, p.grad, 1e-6, 1e-12) <= 1.0
+
+
 def test_bf16_copy_and_state(dev):
     import mi_adamw
     params = make_params(MINI_SHAPES, dev)

@@ -243,7 +243,7 @@ def test_table_rows_are_built_field_by_field_on_cpu():
     assert _ROW_DTYPE.names == tuple(f for f, _ in _lib.TensorRow._fields_)
     assert _ROW_DTYPE.itemsize == ctypes.sizeof(_lib.TensorRow)
     grads = [torch.zeros(10), torch.zeros(4097), torch.zeros(0)]
-    launch = C._tables(grads, torch.device("cpu"))
+    launch = C._tables(grads, torch.device("cpu"), 0)
     rows = launch.host_rows
     assert len(rows) == 2
     assert list(rows["grad"]) == [grads[0].data_ptr(), grads[1].data_ptr()]
