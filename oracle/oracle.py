@@ -97,7 +97,7 @@ OPMODEL_TORCH_CPU = OpModel(lerp_fma=1, addcmul_mode=2, addcdiv_mode=2, div_reci
 # (fma(s, m/d, p)) are fused multiply-adds; sqrt and division are correctly
 # rounded; a tensor divided by a Python scalar c runs as a multiply by
 # f32(1.0 / c) with the reciprocal taken in float64.  Pinned bit-for-bit by the
-# GPU test tests/test_gpu_torch_opmodel.py.
+# GPU test tests/test_gpu_parity.py::test_torch_rocm_matches_oracle_opmodel.
 OPMODEL_TORCH_ROCM = OpModel(lerp_fma=1, addcmul_mode=1, addcdiv_mode=1, div_recip=1)
 
 

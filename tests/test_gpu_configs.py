@@ -6,22 +6,24 @@
    norm rel 1e-6 vs clip_grad_norm_.
 3. gpt-350m fp32 master + clip + bf16 model copy, step 1000: bit-exact, copy ==
    RNE(p).
-4. gpt-1.3b bf16 moments + bf16 copy (with and without clip): bit-exact vs the
-   oracle's bf16-state model on sampled tensors; within the bf16 rounding bound
+4. gpt-1.3b bf16 moments + bf16 copy (with and without clip): all 197 tensors
+   bit-exact vs the oracle's bf16-state model; within the bf16 rounding bound
    of the fp32-state torch reference everywhere.
 5. gpt-6.7b flat buffer + clip + bf16 copy, step 1000: norm vs float64 and
-   torch; sampled tensors bit-exact vs torch stepped with the same norm.
+   torch; all 261 tensors bit-exact vs torch stepped with the same norm, each
+   tensor's seeded inputs regenerated after the step.
 """
 from __future__ import annotations
 
 import gc
+from concurrent.futures import ThreadPoolExecutor
 
 import numpy as np
 import pytest
 import torch
 
-from _helpers import (clone_params, close_rel, gpt_params, load_states, max_ulp, max_ulp_all,
-                      midtrain_state, rel_err, rms, set_grads, to_np)
+from _helpers import (clone_params, close_rel, gen, gpt_params, load_states, make_params, max_ulp,
+                      max_ulp_all, midtrain_state, rel_err, rms, set_grads, to_np)
 from oracle import oracle as O
 
 pytestmark = pytest.mark.gpu
@@ -109,6 +111,40 @@ def test_config2_125m_clip_100_chained(dev):
     print(f"config2 vs torch clip_grad_norm_ path, worst |d|/tol: p {wp:.3g} m {wm:.3g} v {wv:.3g}",
           flush=True)
     assert max(wp, wm, wv) <= 1
+    # The pure relative error |d| / |torch| of the north star (rel <= 1e-5 after 100
+    # chained steps), per tensor kind: the largest over elements with |torch| >= floor x
+    # rms(tensor) for several floors, and how many elements exceed 1e-5 with no floor.
+    # Given the same norms the results are bit-identical (above); the differences come
+    # from torch's fp32 norm-of-norms landing 1 ulp away from this float64 norm at some
+    # steps.  The coefficient then differs by ~6e-8 relative, and the update by an
+    # absolute amount of that order times the gradient; values of p and m that pass
+    # near zero carry it as a large relative error.  Asserted: rel <= 1e-5 for every
+    # element at or above 0.1 x the tensor's rms.
+    stats = {}
+    for kind in ("p", "m", "v"):
+        worst = {f: 0.0 for f in (0.0, 1e-6, 1e-4, 1e-2, 1e-1)}
+        over, total = 0, 0
+        for p, q in zip(ref_a, ours):
+            if kind == "p":
+                a, b = q.detach().double().reshape(-1), p.detach().double().reshape(-1)
+            else:
+                key = "exp_avg" if kind == "m" else "exp_avg_sq"
+                a = oo.state[q][key].double().reshape(-1)
+                b = ta.state[p][key].double().reshape(-1)
+            nz = b != 0
+            rel = (a - b).abs()[nz] / b.abs()[nz]
+            over += int((rel > 1e-5).sum())
+            total += int(b.numel())
+            r = rms(b)
+            for f in worst:
+                sel = b.abs()[nz] >= f * r
+                if bool(sel.any()):
+                    worst[f] = max(worst[f], float(rel[sel].max()))
+        stats[kind] = (worst, over, total)
+        print(f"config2 pure rel, {kind}: max over |torch| >= floor x rms: "
+              + ", ".join(f"floor {f:g}: {w:.3g}" for f, w in worst.items())
+              + f"; {over} of {total} elements above 1e-5", flush=True)
+    assert all(st[0][1e-1] <= 1e-5 for st in stats.values()), stats
 
 
 def test_config3_350m_master_clip_bf16_copy(dev):
@@ -139,10 +175,24 @@ def test_config3_350m_master_clip_bf16_copy(dev):
         assert torch.equal(oopt.bf16_param(q), q.detach().to(torch.bfloat16))
 
 
+def _bf16_bits(t: torch.Tensor) -> np.ndarray:
+    return to_np(t.contiguous().view(torch.int16)).view(np.uint16).reshape(-1)
+
+
+def _seeded(shape, dev, i, names=None):
+    """Tensor i's seeded parameter, exp_avg and exp_avg_sq, regenerated as gpt_params and
+    midtrain_state made them."""
+    p0 = make_params([shape], dev, names=names, seed=1000 + i)[0].detach()
+    m0 = torch.randn(shape, device=dev, generator=gen(dev, 2000 + i)) * 1e-3
+    v0 = (torch.randn(shape, device=dev, generator=gen(dev, 3000 + i)) * 1e-6).abs()
+    return p0, m0, v0
+
+
 @pytest.mark.parametrize("clip", [False, True])
 def test_config4_1p3b_bf16_state(dev, clip):
     import mi_adamw
     from mi_adamw.workloads import GPT_1P3B
+    named = GPT_1P3B.tensors()
     ref = gpt_params(GPT_1P3B, dev)
     ours = clone_params(ref)
     topt = torch.optim.AdamW(ref, foreach=False, **HP)
@@ -151,10 +201,6 @@ def test_config4_1p3b_bf16_state(dev, clip):
     states = midtrain_state(ref, 1000.0)
     load_states(topt, ref, states)
     load_states(oopt, ours, states)
-    sample = [0, 2, 3, 4, 98, len(ref) - 3, len(ref) - 1]
-    before = {i: (to_np(ref[i]).reshape(-1).copy(),
-                  O.to_bf16_bits(to_np(states[i]["exp_avg"]).reshape(-1)),
-                  O.to_bf16_bits(to_np(states[i]["exp_avg_sq"]).reshape(-1))) for i in sample}
     m_old = [st["exp_avg"] for st in states]
     del states
     set_grads(ref, 0, 1e-3)
@@ -167,15 +213,36 @@ def test_config4_1p3b_bf16_state(dev, clip):
     topt.step()
     torch.cuda.synchronize()
     coef = O.clip_coef(np.float32(oopt.last_grad_norm.item()), 1.0) if clip else None
-    # Bit-exact against the oracle's bf16-state model on sampled tensors.
-    for i in sample:
-        pn, mb, vb = before[i]
-        g = to_np(ours[i].grad).reshape(-1)
+
+    # Every tensor bit-exact against the oracle's bf16-state model: each tensor's inputs
+    # are regenerated from their seeds (the moments rounded to bf16 as load_state_dict
+    # stored them) and stepped by the C oracle in a thread pool.
+    def check(i, pn, g, mb, vb, got_p, got_m, got_v, got_c):
         O.adamw_step_bf16state(pn, g, mb, vb, step=1001.0, grad_scale=coef, **HP)
-        q = ours[i]
-        assert O.max_ulp(pn, to_np(q).reshape(-1))[0] == 0
-        assert np.array_equal(mb, to_np(oopt.state[q]["exp_avg"].view(torch.int16)).view(np.uint16).reshape(-1))
-        assert np.array_equal(vb, to_np(oopt.state[q]["exp_avg_sq"].view(torch.int16)).view(np.uint16).reshape(-1))
+        return (i, O.max_ulp(pn, got_p)[0], int(np.count_nonzero(mb != got_m)),
+                int(np.count_nonzero(vb != got_v)),
+                int(np.count_nonzero(O.to_bf16_bits(pn) != got_c)))
+
+    bad = []
+    n_checked = 0
+    with ThreadPoolExecutor(max_workers=16) as pool:
+        pending = []
+        for i, ((name, shape), q) in enumerate(zip(named, ours)):
+            p0, m0, v0 = _seeded(shape, dev, i, names=[name])
+            pending.append(pool.submit(
+                check, i, to_np(p0).reshape(-1).copy(), to_np(q.grad).reshape(-1).copy(),
+                _bf16_bits(m0.to(torch.bfloat16)).copy(), _bf16_bits(v0.to(torch.bfloat16)).copy(),
+                to_np(q).reshape(-1), _bf16_bits(oopt.state[q]["exp_avg"]),
+                _bf16_bits(oopt.state[q]["exp_avg_sq"]), _bf16_bits(oopt.bf16_param(q))))
+            del p0, m0, v0
+            while len(pending) >= 16 or (pending and i == len(ours) - 1):
+                r = pending.pop(0).result()
+                n_checked += 1
+                if max(r[1:]) != 0:
+                    bad.append(r)
+    print(f"config4 clip={clip}: {n_checked} of {len(ours)} tensors checked against the "
+          f"oracle, differing: {bad[:5]}", flush=True)
+    assert n_checked == len(ours) and not bad
     # Against the fp32-state torch reference, bounds from bf16 rounding: bf16
     # keeps 8 significant bits, so round-to-nearest-even is off by at most 2^-8
     # relative.  The old moments were rounded when stored, the new ones are
@@ -200,7 +267,6 @@ def test_config4_1p3b_bf16_state(dev, clip):
         bound = (HP["lr"] * (mo.abs() + mr.abs()) * 2 ** -7 / d + u * 2 ** -7
                  + 2 * p.detach().double().abs() * 2 ** -23 + 1e-30)
         worst_p = max(worst_p, float(((q.detach().double() - p.detach().double()).abs() / bound).max()))
-        assert torch.equal(oopt.bf16_param(q), q.detach().to(torch.bfloat16))
     print(f"config4 clip={clip}: worst/bound m {worst_m:.3g} v {worst_v:.3g} p {worst_p:.3g}",
           flush=True)
     assert worst_m <= 1 and worst_v <= 1 and worst_p <= 1
@@ -209,44 +275,45 @@ def test_config4_1p3b_bf16_state(dev, clip):
 def test_config5_6p7b_flat_clip_bf16_copy(dev):
     import mi_adamw
     from mi_adamw.workloads import GPT_6P7B
+    named = GPT_6P7B.tensors()
     params = gpt_params(GPT_6P7B, dev)
-    sample = [0, 2, 4, 7, 250, len(params) - 3, len(params) - 1]
-    ref = [torch.nn.Parameter(params[i].detach().clone()) for i in sample]
     opt = mi_adamw.FusedAdamW(params, max_grad_norm=1.0, bf16_copy=True, flat_buffer=True, **HP)
     print("flat buffer elements", opt._flat.total, flush=True)
     assert opt._flat.total == GPT_6P7B.numel()  # 128-byte alignment adds no padding here
-    for i, p in enumerate(params):
-        st = midtrain_state([p], 1000.0)[0]
-        st["exp_avg"] = st["exp_avg"]
-        opt.state[p]["step"] = st["step"]
-        m, v = opt._flat.state_views(p)
-        m.copy_(st["exp_avg"])
-        v.copy_(st["exp_avg_sq"])
-        opt.state[p]["exp_avg"], opt.state[p]["exp_avg_sq"] = m, v
-    tref = torch.optim.AdamW(ref, foreach=False, **HP)
-    load_states(tref, ref, [{"step": torch.tensor(1000.0),
-                             "exp_avg": opt.state[params[i]]["exp_avg"].clone(),
-                             "exp_avg_sq": opt.state[params[i]]["exp_avg_sq"].clone()} for i in sample])
+    for i, ((name, shape), p) in enumerate(zip(named, params)):
+        _, m0, v0 = _seeded(shape, dev, i, names=[name])
+        opt.set_state(p, 1000.0, m0, v0)
+        del m0, v0
     set_grads(params, 0, 1e-3)   # writes into the flat gradient views
-    for j, i in enumerate(sample):
-        ref[j].grad = params[i].grad.clone()
     tn = torch.nn.utils.get_total_norm([p.grad for p in params])
     exact = float(sum(float((p.grad.double() ** 2).sum().item()) for p in params)) ** 0.5
     opt.step()
-    torch.nn.utils.clip_grads_with_norm_(ref, 1.0, opt.last_grad_norm.clone())
-    tref.step()
     torch.cuda.synchronize()
-    on = opt.last_grad_norm.item()
+    norm = opt.last_grad_norm.clone()
+    on = norm.item()
     print(f"config5 norm ours={on:.9g} torch={tn.item():.9g} float64={exact:.12g}", flush=True)
     assert abs(on - exact) <= 1e-7 * exact
     assert rel_err(opt.last_grad_norm, tn) <= 1e-6
-    for j, i in enumerate(sample):
-        q, p = params[i], ref[j]
-        assert max_ulp(q, p) == 0
-        assert max_ulp(opt.state[q]["exp_avg"], tref.state[p]["exp_avg"]) == 0
-        assert max_ulp(opt.state[q]["exp_avg_sq"], tref.state[p]["exp_avg_sq"]) == 0
-        assert float(opt.state[q]["step"]) == 1001.0
-        assert torch.equal(opt.bf16_param(q), q.detach().to(torch.bfloat16))
+    # Every tensor bit-exact against torch.optim.AdamW(foreach=False) stepped with the same
+    # norm, one tensor at a time: its inputs are regenerated from their seeds.
+    bad = []
+    for i, ((name, shape), q) in enumerate(zip(named, params)):
+        p0, m0, v0 = _seeded(shape, dev, i, names=[name])
+        p = torch.nn.Parameter(p0)
+        p.grad = torch.randn(shape, device=dev, generator=gen(dev, 4000 + i)) * 1e-3
+        tref = torch.optim.AdamW([p], foreach=False, **HP)
+        load_states(tref, [p], [{"step": torch.tensor(1000.0), "exp_avg": m0, "exp_avg_sq": v0}])
+        torch.nn.utils.clip_grads_with_norm_([p], 1.0, norm)
+        tref.step()
+        d = (max_ulp(q, p), max_ulp(opt.state[q]["exp_avg"], tref.state[p]["exp_avg"]),
+             max_ulp(opt.state[q]["exp_avg_sq"], tref.state[p]["exp_avg_sq"]))
+        same_copy = torch.equal(opt.bf16_param(q), q.detach().to(torch.bfloat16))
+        if max(d) != 0 or not same_copy or float(opt.state[q]["step"]) != 1001.0:
+            bad.append((i, name, d, same_copy))
+        del p, p0, m0, v0, tref
+    print(f"config5: {len(named)} of {len(named)} tensors checked against torch, differing: "
+          f"{bad[:5]}", flush=True)
+    assert not bad
 
 
 @pytest.mark.filterwarnings("ignore:This instance was constructed with capturable=True")
