@@ -3,8 +3,9 @@
 // Kernels (all HBM-streaming, no MFMA: the step is ~15 fp32 ops per 22-34 bytes):
 //   mi_adamw_sumsq_kernel  pass 1 of the clip: float64 sum of g*g over every
 //                          gradient, reduced wave (shuffle) -> LDS -> one
-//                          partial per workgroup; the last 256 MB it reads stay
-//                          in the Infinity Cache for pass 2;
+//                          partial per workgroup; it walks the chunks last to
+//                          first, and the last 256 MB it reads (the first the
+//                          update reads) stay in the Infinity Cache for pass 2;
 //   mi_adamw_norm_finalize_kernel  one workgroup reduces the partials in a fixed
 //                          order and writes the norm and the clip coefficient
 //                          to device memory (no host sync).
@@ -473,18 +474,34 @@ __device__ __forceinline__ int64_t sumsq_chunks(const Src& src, int64_t c, int64
     return c;
 }
 
-// Workgroup b sums chunks b, b + grid, b + 2*grid, ...: streaming loads below
-// keep_from, ordinary loads from keep_from on (the last chunks the pass reads, the
-// ones still in the memory-side cache when the update reaches them).  Two loops,
-// not one with a per-chunk choice: the compiler would fold the two loads into one.
+// The chunks of a work source in reverse order: the norm pass walks the gradients from the
+// last chunk to the first, so the chunks it reads last (kept in the memory-side cache) are
+// the ones the update, which walks them from the first, reads first.
+template <class Src>
+struct ReverseSource {
+    Src src;
+    int64_t n_chunks;
+    __device__ __forceinline__ void get(int64_t c, int64_t chunk_elems, mi_adamw_tensor& t,
+                                        int64_t& begin, int64_t& end, int32_t& row) const {
+        src.get(n_chunks - 1 - c, chunk_elems, t, begin, end, row);
+    }
+};
+
+// Workgroup b sums chunks b, b + grid, b + 2*grid, ... of the reversed order: streaming
+// loads below keep_from, ordinary loads from keep_from on (the last chunks the pass reads,
+// the first ones the update reads, which then come from the memory-side cache: measured
+// 0.2-0.6% off the update against keeping the chunks the update reads last, which its own
+// traffic evicts first).  Two loops, not one with a per-chunk choice: the compiler would
+// fold the two loads into one.
 template <class Src>
 __global__ __launch_bounds__(kNormThreads) void mi_adamw_sumsq_kernel(
     Src src, int64_t n_chunks, int64_t chunk_elems, double* __restrict__ partials,
     int64_t keep_from, float pre) {
     double acc0 = 0.0, acc1 = 0.0;
     int64_t c = blockIdx.x;
-    c = sumsq_chunks<false>(src, c, keep_from, gridDim.x, chunk_elems, pre, acc0, acc1);
-    sumsq_chunks<true>(src, c, n_chunks, gridDim.x, chunk_elems, pre, acc0, acc1);
+    const ReverseSource<Src> rev{src, n_chunks};
+    c = sumsq_chunks<false>(rev, c, keep_from, gridDim.x, chunk_elems, pre, acc0, acc1);
+    sumsq_chunks<true>(rev, c, n_chunks, gridDim.x, chunk_elems, pre, acc0, acc1);
     const double total = block_sum<kNormThreads>(acc0 + acc1);
     if (threadIdx.x == 0) partials[blockIdx.x] = total;
 }
