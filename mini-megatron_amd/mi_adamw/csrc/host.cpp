@@ -20,7 +20,7 @@
 //
 // Module _host (CPython extension, built against the installed torch):
 //   bind(addresses)                     function pointers of libmi_adamw (ctypes)
-//   plan(...) -> capsule                one launch's bookkeeping (see py_plan)
+//   plan(...) -> capsule                one launch's bookkeeping (see plan_new)
 //   prepare(plan, stream) -> int        steps 1-3: READY, READY_MOVED or FALLBACK
 //   norm(plan, stream, d_norm) -> int   mi_adamw_grad_norm* (or sumsq + finalize)
 //   update(plan, stream, hypers, n) -> int   mi_adamw_step*_prescaled
@@ -33,6 +33,7 @@
 
 #include <cstdint>
 #include <cstring>
+#include <exception>
 #include <vector>
 
 #include "mi_adamw.h"
@@ -179,7 +180,18 @@ PyObject* py_bind(PyObject*, PyObject* const* args, Py_ssize_t nargs) {
 //   options:         (chunk_elems, max_blocks, state_code, flags, clip, max_norm, prescale,
 //                     partials, coef, sumsq, stream)
 //   keep:            objects to keep alive while the plan exists
+PyObject* plan_new(PyObject* args);
+
 PyObject* py_plan(PyObject*, PyObject* args) {
+    try {
+        return plan_new(args);
+    } catch (const std::exception& ex) {
+        PyErr_SetString(PyExc_ValueError, ex.what());
+        return nullptr;
+    }
+}
+
+PyObject* plan_new(PyObject* args) {
     PyObject *params, *states, *slots, *hypers, *rows, *rest, *grads, *steps_t, *hsteps_t,
         *launch_t, *opts_t, *keep;
     int amsgrad = 0;
@@ -398,7 +410,16 @@ PyObject* py_prepare(PyObject*, PyObject* const* args, Py_ssize_t nargs) {
         PyErr_SetString(PyExc_RuntimeError, "mi_adamw._host: bind() was not called");
         return nullptr;
     }
-    return PyLong_FromLong(prepare(pl, stream));
+    int rc;
+    try {
+        rc = prepare(pl, stream);
+    } catch (const std::exception& ex) {
+        // an at::Tensor accessor refused a tensor (no storage, ...): let the general path
+        // take the step and report it
+        (void)ex;
+        rc = kFallback;
+    }
+    return PyLong_FromLong(rc);
 }
 
 PyObject* py_norm(PyObject*, PyObject* const* args, Py_ssize_t nargs) {
@@ -456,6 +477,8 @@ PyObject* py_update(PyObject*, PyObject* const* args, Py_ssize_t nargs) {
     return PyLong_FromLong(rc);
 }
 
+PyObject* sync_versions(Plan* pl, PyObject* dict);
+
 PyObject* py_sync_versions(PyObject*, PyObject* const* args, Py_ssize_t nargs) {
     if (nargs != 2 || !PyDict_Check(args[1])) {
         PyErr_SetString(PyExc_TypeError, "sync_versions(plan, dict)");
@@ -463,13 +486,22 @@ PyObject* py_sync_versions(PyObject*, PyObject* const* args, Py_ssize_t nargs) {
     }
     Plan* pl = get_plan(args[0]);
     if (!pl) return nullptr;
+    try {
+        return sync_versions(pl, args[1]);
+    } catch (const std::exception& ex) {
+        PyErr_SetString(PyExc_RuntimeError, ex.what());
+        return nullptr;
+    }
+}
+
+PyObject* sync_versions(Plan* pl, PyObject* dict) {
     for (const Entry& en : pl->e) {
         const at::Tensor& p = THPVariable_Unpack(en.p);
         PyObject* key = PyLong_FromVoidPtr(en.p);
         PyObject* val = Py_BuildValue("(KK)", static_cast<unsigned long long>(p._version()),
                                       static_cast<unsigned long long>(
                                           reinterpret_cast<uint64_t>(p.data_ptr())));
-        const int rc = (key && val) ? PyDict_SetItem(args[1], key, val) : -1;
+        const int rc = (key && val) ? PyDict_SetItem(dict, key, val) : -1;
         Py_XDECREF(key);
         Py_XDECREF(val);
         if (rc < 0) return nullptr;
