@@ -688,9 +688,12 @@ class FusedAdamW(Optimizer):
             raise NotImplementedError("FusedAdamW: parameters and gradients must be contiguous")
 
     def _records(self) -> list:
-        """Per-parameter bookkeeping in param_groups order, rebuilt when the groups change."""
-        key = tuple((id(g["params"]), len(g["params"])) for g in self.param_groups)
+        """Per-parameter bookkeeping in param_groups order, rebuilt when the groups' parameters
+        change (compared by identity, so a parameter swapped into a list in place counts)."""
+        key = tuple(tuple(map(id, g["params"])) for g in self.param_groups)
         if self._recs is None or self._recs_key != key:
+            # a parameter put into a group's list directly gets its step slot (and bf16 copy)
+            self._register_params([p for g in self.param_groups for p in g["params"]])
             self._recs = [_Rec(gi, p, self._slots[id(p)])
                           for gi, g in enumerate(self.param_groups) for p in g["params"]]
             self._recs_key = key
@@ -823,8 +826,9 @@ class FusedAdamW(Optimizer):
                 self.chunk_elems, self.bf16_copy, self.state_dtype)
 
     def _groups_key(self) -> tuple:
-        return tuple((id(g["params"]), len(g["params"]), bool(g["amsgrad"]))
-                     for g in self.param_groups)
+        """The groups' parameters (by identity, so a parameter swapped into a group's list
+        in place is seen) and amsgrad settings."""
+        return tuple((tuple(map(id, g["params"])), bool(g["amsgrad"])) for g in self.param_groups)
 
     def _make_fast(self, entries, hyper_idx, hyper_group, ams, launch, device, stream, partials,
                    coef, state_code, flags):

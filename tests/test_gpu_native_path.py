@@ -296,3 +296,36 @@ def test_amsgrad_switched_off_for_one_group(dev):
         # one launch while both groups agree (native from the second such step); two
         # launches while they differ, which only the general path makes
         assert oopt.native_steps == before + (1 if k in (1, 2, 7) else 0)
+
+
+def test_parameter_swapped_into_a_group_in_place(dev):
+    """A parameter replaced inside a group's list (same list object, same length): both
+    paths notice it, and the new parameter starts from fresh state, as torch's does."""
+    import mi_adamw
+    ref = make_params(SHAPES, dev)
+    ours = clone_params(ref)
+    topt = torch.optim.AdamW(ref, foreach=False, **HP)
+    oopt = mi_adamw.FusedAdamW(ours, **HP, max_grad_norm=1.0)
+    spacer = []
+    for k in range(3):
+        _assign(ref, ours, _fresh_grads(ref, k), spacer)
+        oopt.step()
+        torch.nn.utils.clip_grads_with_norm_(ref, 1.0, oopt.last_grad_norm.clone())
+        topt.step()
+    new_ref = torch.nn.Parameter(torch.randn(SHAPES[4], device=dev))
+    new_ours = torch.nn.Parameter(new_ref.detach().clone())
+    topt.param_groups[0]["params"][4] = new_ref
+    oopt.param_groups[0]["params"][4] = new_ours
+    ref[4], ours[4] = new_ref, new_ours
+    before = oopt.native_steps
+    for k in range(3, 6):
+        _assign(ref, ours, _fresh_grads(ref, k), spacer)
+        oopt.step()
+        torch.nn.utils.clip_grads_with_norm_(ref, 1.0, oopt.last_grad_norm.clone())
+        topt.step()
+    torch.cuda.synchronize()
+    assert _same(ref, ours, topt, oopt) == 0
+    assert float(oopt.state[new_ours]["step"]) == 3.0
+    # the new parameter's step count differs from the others: two hyperparameter sets in
+    # one group, which only the general path launches
+    assert oopt.native_steps == before
