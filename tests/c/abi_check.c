@@ -189,6 +189,38 @@ static int cpu_checks(void)
           "flat probe without a range");
     CHECK(mi_adamw_probe_flat(&t, 1000, MI_ADAMW_STATE_F32, 0, 0, NULL) == MI_ADAMW_E_INVALID,
           "flat probe chunk size");
+    /* the clip split at the all-reduce, the pre-scaled steps, the gradient patch, the no-alloc
+       norm: argument checks */
+    double *fake_d = (double *)(uintptr_t)4096;
+    float *fake_f = (float *)(uintptr_t)4096;
+    CHECK(mi_adamw_grad_sumsq_flat(NULL, 10, 4096, 1.0f, fake_d, fake_d, NULL) ==
+              MI_ADAMW_E_INVALID, "sumsq without a gradient");
+    CHECK(mi_adamw_grad_sumsq_flat(fake_f, 0, 4096, 1.0f, fake_d, fake_d, NULL) ==
+              MI_ADAMW_E_INVALID, "sumsq of nothing");
+    CHECK(mi_adamw_grad_sumsq_flat(fake_f, 10, 4096, INFINITY, fake_d, fake_d, NULL) ==
+              MI_ADAMW_E_INVALID, "sumsq with a non-finite pre-scale");
+    CHECK(mi_adamw_grad_sumsq(NULL, fake, 1, 4096, 1.0f, fake_d, fake_d, NULL) ==
+              MI_ADAMW_E_INVALID, "sumsq without tables");
+    CHECK(mi_adamw_norm_from_sumsq(NULL, 1, 1.0f, fake_f, fake_f, NULL) == MI_ADAMW_E_INVALID,
+          "finalize without sums");
+    CHECK(mi_adamw_norm_from_sumsq(fake_d, 0, 1.0f, fake_f, fake_f, NULL) == MI_ADAMW_E_INVALID,
+          "finalize of no sums");
+    CHECK(mi_adamw_norm_from_sumsq(fake_d, MI_ADAMW_MAX_NORM_BLOCKS + 1, 1.0f, fake_f, fake_f,
+                                   NULL) == MI_ADAMW_E_INVALID, "finalize of too many sums");
+    CHECK(mi_adamw_step_flat_prescaled(&t, h, NULL, NAN, 4096, MI_ADAMW_STATE_F32, 0, 0, NULL) ==
+              MI_ADAMW_E_INVALID, "flat step with a NaN pre-scale");
+    CHECK(mi_adamw_step_prescaled(fake, fake, 1, 4096, h, 1, NULL, INFINITY, 0, 0, 0, NULL) ==
+              MI_ADAMW_E_INVALID, "table step with an infinite pre-scale");
+    const int32_t bad_row[1] = {2};
+    const uint64_t some_grad[1] = {4096};
+    const uint8_t vec0[1] = {0};
+    CHECK(mi_adamw_set_grads((mi_adamw_tensor *)fake, 2, 1, bad_row, some_grad, vec0, NULL) ==
+              MI_ADAMW_E_INVALID, "gradient patch of a row outside the table");
+    CHECK(mi_adamw_set_grads(NULL, 2, 1, bad_row, some_grad, vec0, NULL) == MI_ADAMW_E_INVALID,
+          "gradient patch without a table");
+    CHECK(mi_adamw_grad_norm_flat_noalloc(NULL, 10, 4096, 1.0f, fake_f, fake_f, NULL) ==
+              MI_ADAMW_E_INVALID, "no-alloc norm without a gradient");
+    CHECK(strstr(mi_adamw_strerror(MI_ADAMW_E_SCRATCH), "scratch") != NULL, "scratch error text");
     printf("abi_check cpu: ok (%s)\n", mi_adamw_version());
     return 0;
 }
@@ -449,6 +481,178 @@ static void capt_case(void)
     printf("abi_check gpu: capturable tables, steps 3 and 1, float then device lr: bit-exact\n");
 }
 
+/* The clip split at the all-reduce over `world` slices of one flat range, with the
+ * data-parallel pre-scale f32(1/world): each slice's float64 sum, the finalize over the
+ * sums, each slice's pre-scaled update; against the oracle stepping the pre-scaled
+ * gradients.  Then the no-alloc norm against the workspace one. */
+static void split_case(int64_t n, int world)
+{
+    const size_t fb = (size_t)n * sizeof(float);
+    float *p = malloc(fb), *g = malloc(fb), *m = malloc(fb), *v = malloc(fb), *gp = malloc(fb);
+    float *pr = malloc(fb), *mr = malloc(fb), *vr = malloc(fb);
+    CHECK(p && g && m && v && gp && pr && mr && vr, "host allocation");
+    fill(p, n, 0.02f, 0);
+    fill(g, n, 3e-2f, 0);
+    fill(m, n, 1e-3f, 0);
+    fill(v, n, 1e-6f, 1);
+    const float pre = (float)(1.0 / world);
+    for (int64_t i = 0; i < n; ++i) gp[i] = g[i] * pre; /* what grad.div_(world) stores */
+    memcpy(pr, p, fb);
+    memcpy(mr, m, fb);
+    memcpy(vr, v, fb);
+    float *dp = dev_copy(p, fb), *dg = dev_copy(g, fb), *dm = dev_copy(m, fb);
+    float *dv = dev_copy(v, fb);
+    double *dpart = NULL, *dsum = NULL;
+    float *dnorm = NULL, *dcoef = NULL;
+    HIP(hipMalloc((void **)&dpart, MI_ADAMW_MAX_NORM_BLOCKS * sizeof(double)));
+    HIP(hipMalloc((void **)&dsum, world * sizeof(double)));
+    HIP(hipMalloc((void **)&dnorm, 4 * sizeof(float)));
+    HIP(hipMalloc((void **)&dcoef, 4 * sizeof(float)));
+    mi_adamw_hyper h;
+    oracle_hyper oh;
+    scalars(3e-4, 0.9, 0.95, 1e-8, 0.1, 1001.0, 0, &h, &oh);
+    const int64_t units = n / 32;
+    int rc;
+    for (int r = 0; r < world; ++r) {
+        const int64_t lo = (r * units / world) * 32;
+        const int64_t hi = r + 1 == world ? n : ((r + 1) * units / world) * 32;
+        rc = mi_adamw_grad_sumsq_flat(dg + lo, hi - lo, 4096, pre, dpart, dsum + r, NULL);
+        CHECK(rc == 0, "mi_adamw_grad_sumsq_flat: %s", mi_adamw_strerror(rc));
+    }
+    rc = mi_adamw_norm_from_sumsq(dsum, world, 1.0f, dnorm, dcoef, NULL);
+    CHECK(rc == 0, "mi_adamw_norm_from_sumsq: %s", mi_adamw_strerror(rc));
+    for (int r = 0; r < world; ++r) {
+        const int64_t lo = (r * units / world) * 32;
+        const int64_t hi = r + 1 == world ? n : ((r + 1) * units / world) * 32;
+        mi_adamw_tensor t;
+        memset(&t, 0, sizeof t);
+        t.param = dp + lo;
+        t.grad = dg + lo;
+        t.exp_avg = dm + lo;
+        t.exp_avg_sq = dv + lo;
+        t.numel = hi - lo;
+        t.flags = MI_ADAMW_T_VEC; /* 32-element (128-byte) slice boundaries */
+        rc = mi_adamw_step_flat_prescaled(&t, &h, dcoef, pre, 4096, MI_ADAMW_STATE_F32,
+                                          MI_ADAMW_F_CLIP, 0, NULL);
+        CHECK(rc == 0, "mi_adamw_step_flat_prescaled: %s", mi_adamw_strerror(rc));
+    }
+    /* the no-alloc norm against the workspace norm, on the raw gradients */
+    rc = mi_adamw_grad_norm_flat(dg, n, 4096, 1.0f, dpart, dnorm + 1, dcoef + 1, NULL);
+    CHECK(rc == 0, "mi_adamw_grad_norm_flat: %s", mi_adamw_strerror(rc));
+    rc = mi_adamw_grad_norm_flat_noalloc(dg, n, 4096, 1.0f, dnorm + 2, dcoef + 2, NULL);
+    CHECK(rc == 0, "mi_adamw_grad_norm_flat_noalloc: %s", mi_adamw_strerror(rc));
+    HIP(hipDeviceSynchronize());
+    float norm[4], coef[4];
+    back(norm, dnorm, sizeof norm);
+    back(coef, dcoef, sizeof coef);
+    const double ref = sqrt(oracle_sumsq_f64(gp, n));
+    CHECK(fabs((double)norm[0] - ref) <= 1e-6 * ref, "split norm %.9g vs %.9g", norm[0], ref);
+    const float coef_ref = oracle_clip_coef(norm[0], 1.0);
+    CHECK(memcmp(&coef[0], &coef_ref, sizeof coef_ref) == 0 && coef[0] < 1.0f,
+          "split coef %.9g vs %.9g", coef[0], coef_ref);
+    CHECK(memcmp(&norm[1], &norm[2], 4) == 0 && memcmp(&coef[1], &coef[2], 4) == 0,
+          "no-alloc norm %.9g / %.9g vs workspace %.9g / %.9g", norm[2], coef[2], norm[1], coef[1]);
+    oracle_adamw_f32(pr, gp, mr, vr, NULL, n, &oh, &ROCM_OPS, coef[0], 1);
+    back(p, dp, fb);
+    back(m, dm, fb);
+    back(v, dv, fb);
+    same_f32(p, pr, n, "param (split clip)");
+    same_f32(m, mr, n, "exp_avg (split clip)");
+    same_f32(v, vr, n, "exp_avg_sq (split clip)");
+    printf("abi_check gpu: split clip over %d slices, pre-scale 1/%d, n=%lld: norm %.7g, "
+           "no-alloc norm equal, bit-exact\n", world, world, (long long)n, norm[0]);
+    HIP(hipFree(dp)); HIP(hipFree(dg)); HIP(hipFree(dm)); HIP(hipFree(dv));
+    HIP(hipFree(dpart)); HIP(hipFree(dsum)); HIP(hipFree(dnorm)); HIP(hipFree(dcoef));
+    free(p); free(g); free(m); free(v); free(gp); free(pr); free(mr); free(vr);
+}
+
+/* Tables of two tensors, two chained steps: the second step's gradients are new
+ * buffers written into the device table by mi_adamw_set_grads (one of them misaligned,
+ * so its row leaves the vector path). */
+static void set_grads_case(void)
+{
+    enum { NT = 2 };
+    const int64_t numel[NT] = {70001, 4099};
+    float *p[NT], *pr[NT], *m[NT], *mr[NT], *v[NT], *vr[NT], *g1[NT], *g2[NT];
+    void *dp[NT], *dm[NT], *dv[NT], *dg1[NT], *dg2[NT];
+    mi_adamw_tensor rows[NT];
+    for (int k = 0; k < NT; ++k) {
+        const int64_t n = numel[k];
+        p[k] = malloc(n * 4); pr[k] = malloc(n * 4); m[k] = malloc(n * 4); mr[k] = malloc(n * 4);
+        v[k] = malloc(n * 4); vr[k] = malloc(n * 4); g1[k] = malloc(n * 4); g2[k] = malloc(n * 4);
+        CHECK(p[k] && pr[k] && m[k] && mr[k] && v[k] && vr[k] && g1[k] && g2[k], "host allocation");
+        fill(p[k], n, 0.02f, 0);
+        fill(m[k], n, 1e-3f, 0);
+        fill(v[k], n, 1e-6f, 1);
+        fill(g1[k], n, 1e-3f, 0);
+        fill(g2[k], n, 1e-3f, 0);
+        memcpy(pr[k], p[k], n * 4);
+        memcpy(mr[k], m[k], n * 4);
+        memcpy(vr[k], v[k], n * 4);
+        dp[k] = dev_copy(p[k], n * 4);
+        dm[k] = dev_copy(m[k], n * 4);
+        dv[k] = dev_copy(v[k], n * 4);
+        dg1[k] = dev_copy(g1[k], n * 4);
+        /* the second gradient of tensor 1 sits one element into its buffer: misaligned */
+        HIP(hipMalloc(&dg2[k], (n + 1) * 4));
+        HIP(hipMemcpy((float *)dg2[k] + k, g2[k], n * 4, hipMemcpyHostToDevice));
+        memset(&rows[k], 0, sizeof rows[k]);
+        rows[k].param = dp[k];
+        rows[k].grad = dg1[k];
+        rows[k].exp_avg = dm[k];
+        rows[k].exp_avg_sq = dv[k];
+        rows[k].numel = n;
+        rows[k].hyper = 0;
+        rows[k].flags = MI_ADAMW_T_VEC;
+    }
+    const int64_t nc = mi_adamw_build_chunks(numel, NT, 4096, NULL, 0);
+    mi_adamw_chunk *chunks = malloc(nc * sizeof *chunks);
+    CHECK(chunks && mi_adamw_build_chunks(numel, NT, 4096, chunks, nc) == nc, "chunks");
+    void *d_rows = dev_copy(rows, sizeof rows), *d_chunks = dev_copy(chunks, nc * sizeof *chunks);
+    for (int step = 1; step <= 2; ++step) {
+        if (step == 2) {
+            const int32_t which[NT] = {0, 1};
+            const uint64_t ptrs[NT] = {(uint64_t)(uintptr_t)dg2[0],
+                                       (uint64_t)(uintptr_t)((float *)dg2[1] + 1)};
+            const uint8_t vec[NT] = {1, 0};
+            const int rc = mi_adamw_set_grads((mi_adamw_tensor *)d_rows, NT, NT, which, ptrs, vec,
+                                              NULL);
+            CHECK(rc == 0, "mi_adamw_set_grads: %s", mi_adamw_strerror(rc));
+        }
+        mi_adamw_hyper h;
+        oracle_hyper oh;
+        scalars(3e-4, 0.9, 0.95, 1e-8, 0.1, 10.0 + step, 0, &h, &oh);
+        const int rc = mi_adamw_step(d_rows, d_chunks, nc, 4096, &h, 1, NULL, MI_ADAMW_STATE_F32,
+                                     0, 0, NULL);
+        CHECK(rc == 0, "mi_adamw_step: %s", mi_adamw_strerror(rc));
+        for (int k = 0; k < NT; ++k)
+            oracle_adamw_f32(pr[k], step == 1 ? g1[k] : g2[k], mr[k], vr[k], NULL, numel[k], &oh,
+                             &ROCM_OPS, 1.0f, 0);
+    }
+    HIP(hipDeviceSynchronize());
+    mi_adamw_tensor after[NT];
+    back(after, d_rows, sizeof after);
+    CHECK(after[0].grad == dg2[0] && (after[0].flags & MI_ADAMW_T_VEC), "row 0 after the patch");
+    CHECK(after[1].grad == (float *)dg2[1] + 1 && !(after[1].flags & MI_ADAMW_T_VEC),
+          "row 1 after the patch");
+    for (int k = 0; k < NT; ++k) {
+        back(p[k], dp[k], numel[k] * 4);
+        back(m[k], dm[k], numel[k] * 4);
+        back(v[k], dv[k], numel[k] * 4);
+        same_f32(p[k], pr[k], numel[k], "param (patched gradients)");
+        same_f32(m[k], mr[k], numel[k], "exp_avg (patched gradients)");
+        same_f32(v[k], vr[k], numel[k], "exp_avg_sq (patched gradients)");
+        HIP(hipFree(dp[k])); HIP(hipFree(dm[k])); HIP(hipFree(dv[k]));
+        HIP(hipFree(dg1[k])); HIP(hipFree(dg2[k]));
+        free(p[k]); free(pr[k]); free(m[k]); free(mr[k]); free(v[k]); free(vr[k]);
+        free(g1[k]); free(g2[k]);
+    }
+    HIP(hipFree(d_rows)); HIP(hipFree(d_chunks));
+    free(chunks);
+    printf("abi_check gpu: gradients moved between two table steps (one misaligned), patched by "
+           "mi_adamw_set_grads: bit-exact\n");
+}
+
 static int gpu_checks(void)
 {
     int count = 0;
@@ -459,6 +663,8 @@ static int gpu_checks(void)
     table_case();
     flat_case(262147, 1);
     capt_case();
+    split_case(3000000 + 96, 3);
+    set_grads_case();
     printf("abi_check gpu: ok (%s)\n", mi_adamw_version());
     return 0;
 }

@@ -2,7 +2,9 @@
 
 CPU: version, error text, the chunk-table helper and the argument rejections
 that return before any launch.  GPU: flat clip, tensor/chunk tables with bf16
-state and copy, and amsgrad, each bit-exact against the C oracle.
+state and copy, amsgrad, the capturable chain, the clip split over slices with
+the data-parallel pre-scale (and the no-alloc norm), and gradient pointers
+patched into a table, each bit-exact against the C oracle.
 """
 from __future__ import annotations
 
@@ -30,4 +32,4 @@ def test_c_host_cpu_checks():
 @pytest.mark.gpu
 def test_c_host_gpu_parity_against_oracle():
     out = _run("gpu")
-    assert out.count("bit-exact") == 4 and "abi_check gpu: ok" in out
+    assert out.count("bit-exact") == 6 and "abi_check gpu: ok" in out
