@@ -78,6 +78,7 @@ struct Entry {
     PyObject* obj[4] = {};      // state["step"], exp_avg, exp_avg_sq, max_exp_avg_sq (owned)
     uint64_t ptr[4] = {};       // data pointers of p, exp_avg, exp_avg_sq, max_exp_avg_sq
     uint64_t grad = 0;          // gradient pointer the device table holds
+    int64_t numel = 0;          // the parameter's element count when the row was built
     int32_t row = kNoRow;       // table row to patch, or kNoRow / kFixed
     int32_t slot = 0;           // index into the step buffer
     int32_t hyper = 0;          // hyperparameter set (one per param group)
@@ -288,6 +289,7 @@ PyObject* plan_new(PyObject* args) {
         Py_INCREF(st);
         en.st = st;
         en.ptr[0] = tensor_ptr(p);
+        en.numel = THPVariable_Unpack(p).numel();
         for (int k = 0; k < pl->n_state; ++k) {
             PyObject* o = PyDict_GetItemWithError(st, pl->keys[k]);
             if (!is_tensor(o)) {
@@ -333,10 +335,14 @@ int prepare(Plan* pl, uint64_t stream) {
     for (size_t i = 0; i < n; ++i) {
         Entry& en = pl->e[i];
         const at::Tensor& p = THPVariable_Unpack(en.p);
-        if (reinterpret_cast<uint64_t>(p.data_ptr()) != en.ptr[0]) return kFallback;
+        // the row covers en.numel elements of p, its gradient and its state: a parameter
+        // narrowed in place through .data keeps its address but not its size
+        if (reinterpret_cast<uint64_t>(p.data_ptr()) != en.ptr[0] || p.numel() != en.numel)
+            return kFallback;
         const at::Tensor& g = p.grad();
         if (!g.defined() || g.layout() != c10::kStrided || !g.is_contiguous() ||
-            g.scalar_type() != p.scalar_type() || g.device() != p.device())
+            g.scalar_type() != p.scalar_type() || g.device() != p.device() ||
+            g.numel() != en.numel)
             return kFallback;
         for (int k = 0; k < pl->n_state; ++k) {
             PyObject* o = PyDict_GetItem(en.st, pl->keys[k]);
@@ -375,7 +381,8 @@ int prepare(Plan* pl, uint64_t stream) {
         } else {
             // the single row of a table-free launch lives on the host
             pl->flat_row.grad = reinterpret_cast<float*>(pl->pgrad[0]);
-            pl->flat_row.flags = pl->pvec[0] ? MI_ADAMW_T_VEC : 0;
+            pl->flat_row.flags =
+                (pl->flat_row.flags & ~MI_ADAMW_T_VEC) | (pl->pvec[0] ? MI_ADAMW_T_VEC : 0);
         }
         for (int32_t j = 0; j < m; ++j) {
             // keep the host copy of the rows equal to the device table

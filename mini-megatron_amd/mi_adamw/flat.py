@@ -15,7 +15,12 @@ backward accumulates straight into it.  Consequence: every parameter whose
 ``p.grad`` is a view is stepped every step, exactly as torch.optim.AdamW does
 after ``zero_grad(set_to_none=False)``.  A parameter whose grad was set to
 None is skipped (torch semantics); a gradient tensor that autograd allocated
-elsewhere is copied into the buffer at the next step.
+elsewhere is copied into the buffer at the next step.  So are new values given
+through ``p.data = t`` and moments put into the state dict directly: the step
+copies them into the tensor's slice and points ``p.data`` (or the state entry)
+back at the slice, so the results equal torch's for p while t itself is no
+longer p's storage.  A tensor whose element count changed cannot be taken back
+into its slice and is refused.
 """
 from __future__ import annotations
 
@@ -43,12 +48,14 @@ class FlatLayout:
             raise RuntimeError("flat_buffer=True needs parameters on a ROCm GPU")
         self.device = device
         self.offsets: dict[int, int] = {}
+        self.numels: dict[int, int] = {}
         self.group_ranges: list[tuple[int, int]] = []
         off = 0
         for g in param_groups:
             start = off
             for p in g["params"]:
                 self.offsets[id(p)] = off
+                self.numels[id(p)] = p.numel()
                 off = _align(off + p.numel())
             self.group_ranges.append((start, off))
         self.total = off
@@ -72,8 +79,10 @@ class FlatLayout:
                 self.copy.copy_(self.param)
 
     def _view(self, buf: torch.Tensor, p: torch.Tensor) -> torch.Tensor:
+        # the slice has the element count p had when the buffer was laid out; a p since
+        # resized through .data no longer fits and view() raises
         off = self.offsets[id(p)]
-        return buf[off:off + p.numel()].view(p.shape)
+        return buf[off:off + self.numels[id(p)]].view(p.shape)
 
     def grad_view(self, p: torch.Tensor) -> torch.Tensor:
         return self._view(self.grad, p)
@@ -89,6 +98,43 @@ class FlatLayout:
         p.grad = view
         return view
 
+    def _check_size(self, p: torch.Tensor, t: torch.Tensor, what: str) -> None:
+        n = self.numels[id(p)]
+        if t.numel() != n:
+            raise RuntimeError(f"flat_buffer=True: {what} has {t.numel()} elements but the "
+                               f"buffer holds {n} for this parameter")
+
+    def is_param_view(self, p: torch.Tensor) -> bool:
+        return (p.data_ptr() == self.param.data_ptr() + 4 * self.offsets[id(p)]
+                and p.numel() == self.numels[id(p)] and p.is_contiguous())
+
+    def absorb_param(self, p: torch.Tensor) -> None:
+        """Values given to p through ``p.data = t`` are copied into its slice of the
+        parameter buffer and p.data becomes the slice again (the step updates the slice,
+        as it does every other parameter; t itself is no longer p's storage)."""
+        self._check_size(p, p, "the parameter's new data")
+        if p.dtype != torch.float32 or p.device != self.device:
+            raise NotImplementedError("flat_buffer=True: a parameter's new data must be fp32 "
+                                      "on the buffer's device")
+        view = self._view(self.param, p)
+        view.copy_(p.detach())
+        p.data = view
+
+    def absorb_state(self, p: torch.Tensor, st: dict) -> None:
+        """State tensors put into p's state dict directly (not through load_state_dict)
+        are copied into p's slices of the moment buffers, which the step updates."""
+        off = self.offsets[id(p)]
+        for key in ("exp_avg", "exp_avg_sq", "max_exp_avg_sq"):
+            t = st.get(key)
+            if t is None:
+                continue
+            buf = (self.exp_avg if key == "exp_avg" else self.exp_avg_sq
+                   if key == "exp_avg_sq" else self.max_exp_avg_sq)
+            if (buf is not None and t.data_ptr() == buf.data_ptr() + buf.element_size() * off
+                    and t.numel() == self.numels[id(p)]):
+                continue
+            st[key] = self.adopt_state(p, key, t)
+
     def state_views(self, p: torch.Tensor):
         return self._view(self.exp_avg, p), self._view(self.exp_avg_sq, p)
 
@@ -103,7 +149,8 @@ class FlatLayout:
             view = self.vmax_view(p)
         else:
             view = self._view(self.exp_avg if key == "exp_avg" else self.exp_avg_sq, p)
-        view.copy_(t)
+        self._check_size(p, t, f"state[{key!r}]")
+        view.copy_(t.reshape(view.shape))
         return view
 
     def copy_view(self, p: torch.Tensor) -> torch.Tensor:

@@ -730,10 +730,13 @@ class FusedAdamW(Optimizer):
             self._steps_for(device)
         views = self._step_views
         for i, (rec, g) in enumerate(entries):
-            if flat is not None and not flat.is_grad_view(rec.p, g):
-                self._check_param(rec.p, g)
-                g = flat.absorb_grad(rec.p)
-                entries[i] = (rec, g)
+            if flat is not None:
+                if not flat.is_param_view(rec.p):
+                    flat.absorb_param(rec.p)      # p.data was replaced
+                if not flat.is_grad_view(rec.p, g):
+                    self._check_param(rec.p, g)
+                    g = flat.absorb_grad(rec.p)
+                    entries[i] = (rec, g)
             if g.is_sparse:
                 raise RuntimeError("Adam does not support sparse gradients, please consider "
                                    "SparseAdam instead")
@@ -744,8 +747,11 @@ class FusedAdamW(Optimizer):
             if len(st) == 0:
                 self._check_param(rec.p, g)
                 self._init_state(rec.p, st, ams_g[rec.gi])
-            elif st["step"] is not views[rec.slot]:
-                self._adopt_step(rec.p, st, rec.slot)
+            else:
+                if st["step"] is not views[rec.slot]:
+                    self._adopt_step(rec.p, st, rec.slot)
+                if flat is not None:
+                    flat.absorb_state(rec.p, st)   # moments put into the dict directly
             if ams_g[rec.gi] and "max_exp_avg_sq" not in st:
                 # amsgrad switched on for a group after its state was created
                 self._init_vmax(rec.p, st)
@@ -1047,8 +1053,10 @@ class FusedAdamW(Optimizer):
         are split into launches), and the parameter and state pointers, which rarely
         change; and the gradient pointers, which change whenever zero_grad() frees the
         gradients and backward allocates them elsewhere."""
-        sig = [(rec.p.data_ptr(), rec.st["exp_avg"].data_ptr(), rec.st["exp_avg_sq"].data_ptr(),
-                _ptr(rec.st.get("max_exp_avg_sq"))) for rec, _ in entries]
+        # the element count too: a parameter narrowed in place through .data keeps its address
+        sig = [(rec.p.data_ptr(), rec.p.numel(), rec.st["exp_avg"].data_ptr(),
+                rec.st["exp_avg_sq"].data_ptr(), _ptr(rec.st.get("max_exp_avg_sq")))
+               for rec, _ in entries]
         sig.append(tuple(hyper_idx))
         sig.append(tuple(bool(a) for a in hyper_ams))
         return sig, [g.data_ptr() for _, g in entries]
@@ -1101,9 +1109,9 @@ class FusedAdamW(Optimizer):
             if cache[4] != grads:
                 _refuse_under_capture("gradient tensors moved")
                 # torch checks shape, dtype and device when .grad is assigned; the
-                # kernels also need dense storage
+                # kernels also need dense storage of the row's size
                 for rec, g in entries:
-                    if not g.is_contiguous():
+                    if not g.is_contiguous() or g.numel() != rec.p.numel():
                         self._check_param(rec.p, g)
                 garr = np.asarray(grads, dtype=np.uint64)
                 for launch, part in zip(launches, parts):

@@ -329,3 +329,36 @@ def test_parameter_swapped_into_a_group_in_place(dev):
     # the new parameter's step count differs from the others: two hyperparameter sets in
     # one group, which only the general path launches
     assert oopt.native_steps == before
+
+
+@pytest.mark.parametrize("layout", ["tables", "single"])
+def test_parameter_narrowed_in_place_is_refused(dev, layout):
+    """p.data narrowed to a view at the same address, then a gradient of the new size:
+    torch's AdamW raises at the size mismatch with exp_avg, and so must both step paths,
+    before any kernel reads the old row size from the smaller gradient."""
+    import mi_adamw
+    shapes = [(4099,)] if layout == "single" else SHAPES
+    ref = make_params(shapes, dev)
+    ours = clone_params(ref)
+    topt = torch.optim.AdamW(ref, foreach=False, **HP)
+    oopt = mi_adamw.FusedAdamW(ours, **HP, max_grad_norm=1.0)
+    spacer = []
+    for k in range(3):
+        _assign(ref, ours, _fresh_grads(ref, k), spacer)
+        oopt.step()
+        torch.nn.utils.clip_grads_with_norm_(ref, 1.0, oopt.last_grad_norm.clone())
+        topt.step()
+    assert oopt.native_steps == 2
+    j = 0 if layout == "single" else 4
+    for p in (ref[j], ours[j]):
+        ptr = p.data_ptr()
+        with torch.no_grad():
+            p.data = p.data[:1000]
+        assert p.data_ptr() == ptr
+    _assign(ref, ours, _fresh_grads(ref, 3), spacer)
+    with pytest.raises(RuntimeError):
+        topt.step()
+    with pytest.raises(RuntimeError, match="elements"):
+        oopt.step()
+    torch.cuda.synchronize()
+    assert oopt.native_steps == 2

@@ -47,8 +47,12 @@ def _state_diff(ref, ours, topt, oopt):
     return d
 
 
+@pytest.mark.parametrize("layout", ["tables", "flat"])
 @pytest.mark.parametrize("seed", range(6))
-def test_random_step_sequences(dev, seed):
+def test_random_step_sequences(dev, seed, layout):
+    """In the flat layout the parameters, gradients and moments are views of its buffers:
+    a replaced p.data, gradient or state tensor is copied into its slice at the next step,
+    and the results must still equal torch's."""
     import mi_adamw
     rng = random.Random(seed)
     clip = seed % 2 == 0
@@ -58,7 +62,8 @@ def test_random_step_sequences(dev, seed):
                          {"params": ps[4:], "lr": 1e-3, "weight_decay": 0.0, "amsgrad": True}]
     hp = dict(lr=3e-4, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.1)
     topt = torch.optim.AdamW(groups(ref), foreach=False, **hp)
-    oopt = mi_adamw.FusedAdamW(groups(ours), **hp, max_grad_norm=1.0 if clip else None)
+    oopt = mi_adamw.FusedAdamW(groups(ours), **hp, max_grad_norm=1.0 if clip else None,
+                               flat_buffer=layout == "flat")
     side = torch.cuda.Stream()
     spacer = []
     log = []
@@ -129,6 +134,15 @@ def test_random_step_sequences(dev, seed):
         log.append((k, action, oopt.native_steps - before, d))
         assert d == 0, log[-5:]
     native = sum(n for _, _, n, _ in log)
-    print(f"seed {seed} clip {clip}: {native} of 40 steps on the native path; actions "
+    if layout == "flat":
+        # every parameter, gradient and moment is a view of the buffers again
+        fl = oopt._flat
+        for q in ours:
+            assert fl.is_param_view(q) and (q.grad is None or fl.is_grad_view(q, q.grad))
+            st = oopt.state.get(q, {})
+            if "exp_avg" in st:
+                assert st["exp_avg"].data_ptr() == (fl.exp_avg.data_ptr()
+                                                    + 4 * fl.offsets[id(q)])
+    print(f"seed {seed} {layout} clip {clip}: {native} of 40 steps on the native path; actions "
           f"{sorted(set(a for _, a, _, _ in log))}", flush=True)
     assert native >= 1

@@ -85,8 +85,8 @@ def _unchanged(s, before_steps):
 
 
 @pytest.mark.parametrize("change", ["grad None", "grad non-contiguous", "grad dtype", "p.data",
-                                    "state replaced", "state data", "step replaced",
-                                    "other stream"])
+                                    "p.data narrowed", "grad narrowed", "state replaced",
+                                    "state data", "step replaced", "other stream"])
 def test_every_other_change_falls_back_untouched(change):
     s = _Setup(n_params=2)
     assert s.prepare() == s.host.READY
@@ -108,6 +108,17 @@ def test_every_other_change_falls_back_untouched(change):
     elif change == "p.data":
         with torch.no_grad():
             p.data = p.data.clone()
+    elif change == "p.data narrowed":
+        # same address, fewer elements: the row (and the state) still cover the old size
+        ptr = p.data_ptr()
+        with torch.no_grad():
+            p.data = p.data[:p.numel() // 2]
+        assert p.data_ptr() == ptr
+        p.grad = torch.randn(p.shape)
+    elif change == "grad narrowed":
+        # a gradient whose storage is smaller than the row (torch checks shapes on
+        # assignment, .data of the gradient is not checked)
+        p.grad.data = torch.randn(p.numel() // 2)
     elif change == "state replaced":
         s.states[1]["exp_avg"] = s.states[1]["exp_avg"].clone()
     elif change == "state data":
