@@ -80,7 +80,7 @@ class ZeroRangeStep:
 
     def segments(self, rank: int) -> list[tuple[int, int, int]]:
         """(param group, lo, hi) pieces of rank's slice, one per group it overlaps."""
-        lo, hi = self.bounds[rank]
+        lo, hi = self._bounds(rank)
         out = []
         for gi, (a, b) in enumerate(self.flat.group_ranges):
             s, e = max(lo, a), min(hi, b)
@@ -107,12 +107,16 @@ class ZeroRangeStep:
         for group in opt.param_groups:
             slots = []
             for p in group["params"]:
+                if not self.flat.is_param_view(p):
+                    self.flat.absorb_param(p)          # p.data was replaced
                 slot = opt._slots[id(p)]
                 st = opt.state[p]
                 if len(st) == 0:
                     opt._init_state(p, st, False)
-                elif st["step"] is not opt._step_views[slot]:
-                    opt._adopt_step(p, st, slot)
+                else:
+                    if st["step"] is not opt._step_views[slot]:
+                        opt._adopt_step(p, st, slot)
+                    self.flat.absorb_state(p, st)      # moments put into the dict directly
                 slots.append(slot)
             group_slots.append(torch.as_tensor(slots, dtype=torch.long))
         for idx in group_slots:
@@ -131,15 +135,26 @@ class ZeroRangeStep:
     def _stream(self) -> int:
         return torch.cuda.current_stream(self.flat.device).cuda_stream
 
+    def _bounds(self, rank: int) -> tuple[int, int]:
+        if not 0 <= rank < self.world:
+            raise ValueError(f"rank must be in [0, {self.world}), got {rank}")
+        return self.bounds[rank]
+
+    def _device_buffer(self, t: torch.Tensor, dtype: torch.dtype, what: str) -> None:
+        # the kernels read or write t's memory as `dtype` elements from its first one
+        if (not isinstance(t, torch.Tensor) or t.dtype != dtype or t.device != self.flat.device
+                or t.numel() < 1 or not t.is_contiguous()):
+            raise ValueError(f"{what} must be a contiguous {dtype} tensor of at least one "
+                             f"element on {self.flat.device}")
+
     def grad_sumsq(self, rank: int, out: torch.Tensor | None = None) -> torch.Tensor:
         """The float64 sum of squares of rank's pre-scaled gradients, written to out[0]
         (default: entry `rank` of this object's buffer of one sum per rank)."""
         lib = _lib.load()
-        lo, hi = self.bounds[rank]
+        lo, hi = self._bounds(rank)
         if out is None:
             out = self._sumsq[rank:rank + 1]
-        if out.dtype != torch.float64 or out.device != self.flat.device:
-            raise ValueError("grad_sumsq: out must be a float64 tensor on the buffers' device")
+        self._device_buffer(out, torch.float64, "grad_sumsq: out")
         partials, _ = self.opt._ws(self.flat.device)
         with torch.cuda.device(self.flat.device):
             if hi <= lo:
@@ -155,7 +170,10 @@ class ZeroRangeStep:
         """(norm, coefficient) as 0-d / 1-element device tensors from the ranks' sums,
         added in rank order."""
         lib = _lib.load()
+        self._device_buffer(sumsq, torch.float64, "finalize: sumsq")
         max_norm = self.opt.max_grad_norm if max_norm is None else max_norm
+        if max_norm is None:
+            raise ValueError("finalize: no max_norm (the optimizer has max_grad_norm=None)")
         norm = torch.empty((), dtype=torch.float32, device=self.flat.device)
         with torch.cuda.device(self.flat.device):
             _lib.check(lib.mi_adamw_norm_from_sumsq(
@@ -171,6 +189,7 @@ class ZeroRangeStep:
         if opt.bf16_copy:
             flags |= _lib.F_BF16_COPY
         if coef is not None:
+            self._device_buffer(coef, torch.float32, "update: coef")
             flags |= _lib.F_CLIP
             if opt.clip_write_grads:
                 flags |= _lib.F_WRITE_GRAD

@@ -186,6 +186,61 @@ def test_range_step_split_calls_match_step(dev):
         assert torch.equal(x, y), key
 
 
+
+def test_range_step_takes_back_replaced_tensors(dev):
+    """p.data and a moment replaced between steps (new tensors, same sizes): the range
+    step copies them into their slices as the flat step does, and both stay bit-identical."""
+    import mi_adamw
+    a, b, oa, ob = _flat_pair(dev, SHAPES, torch.float32, 2, 1.0)
+    zs = mi_adamw.ZeroRangeStep(ob, 3)
+    for step in range(3):
+        set_grads(a, step, 3e-2)
+        for p, q in zip(a, b):
+            q.grad.copy_(p.grad)
+        if step == 1:
+            with torch.no_grad():
+                for ps, opt in ((a, oa), (b, ob)):
+                    ps[3].data = ps[3].data.clone() * 0.5
+                    opt.state[ps[7]]["exp_avg"] = opt.state[ps[7]]["exp_avg"].clone() * 0.25
+        oa.step()
+        zs.step()
+    torch.cuda.synchronize()
+    for key in ("param", "exp_avg", "exp_avg_sq", "copy"):
+        assert torch.equal(getattr(oa._flat, key), getattr(ob._flat, key)), key
+    for ps, opt in ((a, oa), (b, ob)):
+        assert opt._flat.is_param_view(ps[3])
+        assert opt.state[ps[7]]["exp_avg"].data_ptr() == (opt._flat.exp_avg.data_ptr()
+                                                          + 4 * opt._flat.offsets[id(ps[7])])
+    assert torch.equal(a[3], b[3])
+
+
+def test_range_step_rejects_bad_arguments(dev):
+    """Ranks out of range and device buffers of the wrong type are refused on the host,
+    before any launch (the kernels would read 8-byte sums from a 4-byte buffer)."""
+    import mi_adamw
+    _, b, _, ob = _flat_pair(dev, SHAPES, torch.float32, 1, 1.0)
+    zs = mi_adamw.ZeroRangeStep(ob, 2)
+    set_grads(b, 0, 3e-2)
+    for bad in (-1, 2):
+        with pytest.raises(ValueError):
+            zs.grad_sumsq(bad)
+        with pytest.raises(ValueError):
+            zs.segments(bad)
+    for bad in (torch.zeros(1, dtype=torch.float32, device=dev),
+                torch.zeros(0, dtype=torch.float64, device=dev),
+                torch.zeros(1, dtype=torch.float64),
+                torch.zeros(4, dtype=torch.float64, device=dev)[::2]):
+        with pytest.raises(ValueError):
+            zs.grad_sumsq(0, bad)
+        with pytest.raises(ValueError):
+            zs.finalize(bad)
+    hypers = zs.begin()
+    with pytest.raises(ValueError):
+        zs.update(0, hypers, torch.ones(1, dtype=torch.float64, device=dev))
+    with pytest.raises(ValueError):
+        zs.update(5, hypers, None)
+    torch.cuda.synchronize()
+
 def _fill_6p7b(params, opt, step: float) -> None:
     """Seeded parameters, gradients and moments (per-tensor seeds) in the flat buffers."""
     from mi_adamw.workloads import GPT_6P7B, init_kind
