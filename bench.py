@@ -423,8 +423,70 @@ def describe(name: str) -> str:
     return ", ".join(parts) + (": fused clip + AdamW step" if clip else ": AdamW step")
 
 
+def range_shard_rows(opt, world: int, steps: int = 10, warmup: int = 3) -> dict:
+    """The step as `world` ZeRO-1 ranks would take it, each rank's kernels on its own
+    contiguous slice of the flat buffers (mi_adamw.ZeroRangeStep, gradients pre-scaled by
+    f32(1/world) as allreduce_grads' div_ would leave them): per rank the sum of squares
+    of its slice, the finalize from the ranks' sums (which arrive by an 8-byte all-reduce
+    across GPUs) and the update of its slice.  Every rank's kernels run in turn on this
+    GPU; each is timed with HIP events on the launch stream."""
+    import mi_adamw
+    zs = mi_adamw.ZeroRangeStep(opt, world, grad_prescale=mi_adamw.dp_prescale(world))
+    clip = opt.max_grad_norm is not None
+    sizes = [hi - lo for lo, hi in zs.bounds]
+    per = {"sumsq": [[] for _ in range(world)], "finalize": [], "update": [[] for _ in range(world)]}
+    ev = lambda: torch.cuda.Event(enable_timing=True)    # noqa: E731
+    for k in range(warmup + steps):
+        hypers = zs.begin()
+        marks = []
+        coef = None
+        if clip:
+            for r in range(world):
+                a, b = ev(), ev()
+                a.record()
+                zs.grad_sumsq(r)
+                b.record()
+                marks.append(("sumsq", r, a, b))
+            a, b = ev(), ev()
+            a.record()
+            _, coef = zs.finalize(zs._sumsq[:world])
+            b.record()
+            marks.append(("finalize", 0, a, b))
+        for r in range(world):
+            a, b = ev(), ev()
+            a.record()
+            zs.update(r, hypers, coef)
+            b.record()
+            marks.append(("update", r, a, b))
+        torch.cuda.synchronize()
+        if k >= warmup:
+            for kind, r, a, b in marks:
+                (per[kind] if kind == "finalize" else per[kind][r]).append(a.elapsed_time(b))
+    shape_bytes = bytes_per_param(clip, "fp32" if opt.state_dtype == torch.float32 else "bf16",
+                                  opt.bf16_copy)
+    upd_ms = [statistics.mean(x) for x in per["update"]]
+    sq_ms = [statistics.mean(x) for x in per["sumsq"]] if clip else [0.0] * world
+    fin_ms = statistics.mean(per["finalize"]) if clip else 0.0
+    rank_ms = [s + fin_ms + u for s, u in zip(sq_ms, upd_ms)]
+    upd_gbs = [shape_bytes[1] * n / t / 1e6 for n, t in zip(sizes, upd_ms)]
+    rank_gbs = [shape_bytes[0] * n / t / 1e6 for n, t in zip(sizes, rank_ms)]
+    return {
+        "world": world, "slice_params": sizes[0], "grad_prescale": zs.grad_prescale,
+        "rank_ms_mean": statistics.mean(rank_ms), "rank_ms_max": max(rank_ms),
+        "rank_gbs_mean": statistics.mean(rank_gbs),
+        "rank_pct_of_peak_mean": 100 * statistics.mean(rank_gbs) / PEAK_HBM_GBS,
+        "sumsq_ms_mean": statistics.mean(sq_ms), "finalize_ms": fin_ms,
+        "update_ms_mean": statistics.mean(upd_ms), "update_ms_max": max(upd_ms),
+        "update_gbs_mean": statistics.mean(upd_gbs),
+        "update_frac_mean": statistics.mean(upd_gbs) / PEAK_HBM_GBS,
+        "note": "every rank's kernels in turn on one GPU; the reduce-scatter, the 8-byte "
+                "all-reduce of the sums and the all-gather need more than one GPU",
+    }
+
+
 def run_config(name: str, steps: int, warmup: int, device, with_context: bool,
-               capturable: bool = False, write_grads: bool = False) -> dict:
+               capturable: bool = False, write_grads: bool = False,
+               range_world: int = 0) -> dict:
     shape_name, clip, state, copy, flat, start_step, gstd = CONFIGS[name]
     log(f"[bench] {name}: building {shape_name} set" + (" (capturable)" if capturable else "")
         + (" (clipped grads written back)" if write_grads else ""))
@@ -471,6 +533,12 @@ def run_config(name: str, steps: int, warmup: int, device, with_context: bool,
         f"({achieved_upd:.1f} GB/s), norm {norm_avg:.4f} ms"
         + ("" if probe_ms is None else
            f"; memory-only probe {probe_ms:.4f} ms ({probe_gbs:.1f} GB/s)"))
+    if range_world > 1 and flat and not capturable and not write_grads:
+        res["range_shard"] = range_shard_rows(opt, range_world)
+        rs = res["range_shard"]
+        log(f"[bench] {name}: as {range_world} ZeRO-1 ranks, {rs['slice_params']} params each: "
+            f"{rs['rank_ms_mean']:.4f} ms per rank ({rs['rank_pct_of_peak_mean']:.1f}% of peak), "
+            f"update {rs['update_ms_mean']:.4f} ms ({rs['update_gbs_mean']:.1f} GB/s)")
     del params, opt
     torch.cuda.empty_cache()
     if with_context:
@@ -526,6 +594,9 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true", help="skip every CPU baseline")
     ap.add_argument("--no-context", action="store_true", help="skip torch's GPU rows")
     ap.add_argument("--no-host", action="store_true", help="skip the step() host-time rows")
+    ap.add_argument("--range-world", type=int, default=8,
+                    help="after the headline's timed steps (flat layout), time its step as this "
+                         "many ZeRO-1 ranks' slices, every rank's kernels in turn (0: skip)")
     ap.add_argument("--training", action="store_true",
                     help="also time gpt-125m training iterations (bf16 autocast) with torch's "
                          "per-tensor and fused AdamW, FusedAdamW, and FusedAdamW + bf16_weights")
@@ -574,7 +645,8 @@ def main() -> int:
         warnings.filterwarnings("ignore", message="This instance was constructed with capturable")
     results = {nm: run_config(nm, args.steps, args.warmup, device,
                               with_context=not args.no_context and nm == args.config,
-                              capturable=args.capturable, write_grads=args.clip_write_grads)
+                              capturable=args.capturable, write_grads=args.clip_write_grads,
+                              range_world=args.range_world if nm == args.config else 0)
                for nm in names}
     if args.calibrate_copy:
         src = torch.ones(1 << 28, device=device)
@@ -621,6 +693,8 @@ def main() -> int:
     }
     if "torch_gpu_ms" in head:
         line["torch_gpu_ms"] = head["torch_gpu_ms"]
+    if "range_shard" in head:
+        line["range_shard"] = _rounded(head["range_shard"])
     if sweep:
         line["sweep"] = [_rounded(results[nm]) for nm in names if nm != args.config]
     if not args.no_host:

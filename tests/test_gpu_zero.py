@@ -299,3 +299,31 @@ def test_range_step_6p7b_equals_flat_step(dev):
         assert same_norm
         assert all(v == 0 for v in diff.values())
         assert all(float(opt.state[p]["step"]) == 1001.0 for p in params)
+
+
+def test_bench_range_shard_rows_step_as_the_flat_step(dev):
+    """bench.py's range_shard row steps the flat buffers as `world` ranks: after its steps
+    the buffers equal an unsharded flat optimizer's after as many steps, bit for bit."""
+    import importlib.util
+    import os
+    import mi_adamw
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    spec = importlib.util.spec_from_file_location("bench_under_test", os.path.join(root, "bench.py"))
+    bench = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(bench)
+    world = 4
+    a, b, oa, ob = _flat_pair(dev, SHAPES, torch.float32, 2, mi_adamw.dp_prescale(world))
+    set_grads(a, 0, 3e-2)
+    for p, q in zip(a, b):
+        q.grad.copy_(p.grad)
+    rs = bench.range_shard_rows(ob, world, steps=2, warmup=1)
+    for _ in range(3):
+        oa.step()
+    torch.cuda.synchronize()
+    lo, hi = mi_adamw.shard_bounds(ob._flat.total, world)[0]
+    assert rs["world"] == world and rs["slice_params"] == hi - lo
+    assert rs["rank_ms_mean"] > 0 and rs["update_gbs_mean"] > 0
+    for key in ("param", "exp_avg", "exp_avg_sq", "copy"):
+        assert torch.equal(getattr(oa._flat, key), getattr(ob._flat, key)), key
+    assert all(float(oa.state[p]["step"]) == float(ob.state[q]["step"]) == 1003.0
+               for p, q in zip(a, b))
