@@ -77,6 +77,52 @@ class ZeroRangeStep:
         self.bounds = shard_bounds(flat.total, self.world)
         self._sumsq = torch.zeros(max(self.world, 1), dtype=torch.float64, device=flat.device)
         self._coef = torch.ones(1, dtype=torch.float32, device=flat.device)
+        self._plan = None       # the native checks of begin(), made by a begin() in Python
+        self.native_begins = 0
+
+    def _make_plan(self, stream: int) -> None:
+        """The native host path's plan for the checks and the step counting of begin():
+        every parameter's storage, gradient view (which must stay where it is) and state
+        entries, one step count per param group.  Its launch fields are unused (begin()
+        launches nothing)."""
+        opt = self.opt
+        self._plan = None
+        steps = opt._steps
+        if not steps.is_contiguous() or steps.device.type != "cpu":
+            return
+        entries = [(gi, p) for gi, g in enumerate(opt.param_groups) for p in g["params"]]
+        n = len(entries)
+        hyper_steps = np.zeros(max(len(opt.param_groups), 1), dtype=np.float64)
+        row = _lib.TensorRow()
+        try:
+            plan = _lib.host().plan(
+                [p for _, p in entries], [opt.state[p] for _, p in entries],
+                [opt._slots[id(p)] for _, p in entries], [gi for gi, _ in entries],
+                [-2] * n, [True] * n, [p.grad.data_ptr() for _, p in entries], False,
+                (steps.data_ptr(), steps.numel()), (hyper_steps.ctypes.data, len(hyper_steps)),
+                (False, 0, 0, 0, 0, 0, ctypes.addressof(row), 0),
+                (0, 0, 0, 0, False, 0.0, 1.0, 0, 0, 0, int(stream)),
+                (steps, hyper_steps, row))
+        except (TypeError, ValueError):
+            return
+        self._plan = (plan, steps, opt.state, opt._groups_key(), hyper_steps, row,
+                      [bool(g["params"]) for g in opt.param_groups])
+
+    def _native_begin(self):
+        """begin() through the native checks, or None when the Python begin() must run."""
+        opt = self.opt
+        pl = self._plan
+        if (pl is None or pl[1] is not opt._steps or pl[2] is not opt.state
+                or pl[3] != opt._groups_key()):
+            return None
+        host = _lib._host
+        if host.prepare(pl[0], self._stream()) != host.READY:
+            return None
+        from .optimizer import _hyper
+        self.native_begins += 1
+        hs = pl[4]
+        return [_hyper(g, float(hs[gi])) if nonempty else None
+                for gi, (g, nonempty) in enumerate(zip(opt.param_groups, pl[6]))]
 
     def segments(self, rank: int) -> list[tuple[int, int, int]]:
         """(param group, lo, hi) pieces of rank's slice, one per group it overlaps."""
@@ -92,7 +138,13 @@ class ZeroRangeStep:
     def begin(self) -> list[_lib.Hyper]:
         """Advance every parameter's step count by one (each rank keeps the same count) and
         return one hyperparameter set per param group.  Every parameter must have its
-        gradient view and all parameters of a group one step count, as in the flat step."""
+        gradient view and all parameters of a group one step count, as in the flat step.
+        After the first call, the checks and the counting run natively while nothing they
+        cover changed; any change (a replaced tensor, a moved gradient, a new group, a loaded
+        checkpoint) takes this Python body, which handles it and makes a new plan."""
+        hypers = self._native_begin()
+        if hypers is not None:
+            return hypers
         opt = self.opt
         from .optimizer import _hyper
         steps = opt._steps_for(self.flat.device)
@@ -130,6 +182,7 @@ class ZeroRangeStep:
                 continue
             steps[idx] += 1
             hypers.append(_hyper(group, float(steps[idx[0]])))
+        self._make_plan(self._stream())
         return hypers
 
     def _stream(self) -> int:

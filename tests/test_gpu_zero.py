@@ -153,6 +153,7 @@ def test_range_step_equals_flat_step(dev, state_dtype, groups):
                                y.view(torch.int32)), (world, key)
         assert all(float(oa.state[p]["step"]) == float(ob.state[q]["step"]) == 1003.0
                    for p, q in zip(a, b))
+        assert zs.native_begins == 2          # the first begin() makes the native plan
         print(f"world {world} groups {groups} {state_dtype}: bit-identical, {cuts_inside} "
               f"slice boundaries inside tensors", flush=True)
         del a, b, oa, ob, zs
@@ -212,6 +213,44 @@ def test_range_step_takes_back_replaced_tensors(dev):
         assert opt.state[ps[7]]["exp_avg"].data_ptr() == (opt._flat.exp_avg.data_ptr()
                                                           + 4 * opt._flat.offsets[id(ps[7])])
     assert torch.equal(a[3], b[3])
+    # step 0 made the plan, step 1 saw the replaced tensors and took the Python begin()
+    assert zs.native_begins == 1
+
+
+def test_range_step_native_begin_changes(dev):
+    """Between range steps: a learning-rate change (read from the group each step, natively),
+    a checkpoint loaded into the optimizer and a moved gradient.  The results stay the
+    unsharded flat step's; a gradient that is no longer the buffer's view is refused as
+    before, with the step counts unchanged."""
+    import copy
+    import mi_adamw
+    a, b, oa, ob = _flat_pair(dev, SHAPES, torch.float32, 2, 1.0)
+    zs = mi_adamw.ZeroRangeStep(ob, 4)
+    log = []
+    for step in range(6):
+        set_grads(a, step, 3e-2)
+        for p, q in zip(a, b):
+            q.grad.copy_(p.grad)
+        if step == 2:
+            for opt in (oa, ob):
+                opt.param_groups[1]["lr"] = 7e-4
+        if step == 4:
+            sd = copy.deepcopy(oa.state_dict())
+            ob.load_state_dict(sd)
+        before = zs.native_begins
+        oa.step()
+        zs.step()
+        log.append(zs.native_begins - before)
+    torch.cuda.synchronize()
+    for key in ("param", "exp_avg", "exp_avg_sq", "copy"):
+        assert torch.equal(getattr(oa._flat, key), getattr(ob._flat, key)), key
+    # native from the second step; the checkpoint load replaces the state dicts
+    assert log == [0, 1, 1, 1, 0, 1], log
+    counts = [float(ob.state[q]["step"]) for q in b]
+    b[2].grad = b[2].grad.clone()
+    with pytest.raises(RuntimeError, match="gradient view"):
+        zs.begin()
+    assert [float(ob.state[q]["step"]) for q in b] == counts
 
 
 def test_range_step_rejects_bad_arguments(dev):
