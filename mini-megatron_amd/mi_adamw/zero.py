@@ -47,6 +47,15 @@ def shard_bounds(total: int, world: int, align: int = ALIGN_ELEMS) -> list[tuple
     return [(cuts[r], cuts[r + 1]) for r in range(world)]
 
 
+class _BeginPlan:
+    """The native plan of ZeroRangeStep.begin() and what it was made from."""
+    __slots__ = ("plan", "steps", "state", "groups_key", "hyper_steps", "row", "nonempty")
+
+    def __init__(self, **kw):
+        for k, v in kw.items():
+            setattr(self, k, v)
+
+
 def dp_prescale(world: int) -> float:
     """The fp32 factor that ``grad.div_(world)`` multiplies by on the GPU: torch divides a
     tensor by a host scalar as a multiply by the reciprocal, rounded to fp32."""
@@ -105,24 +114,25 @@ class ZeroRangeStep:
                 (steps, hyper_steps, row))
         except (TypeError, ValueError):
             return
-        self._plan = (plan, steps, opt.state, opt._groups_key(), hyper_steps, row,
-                      [bool(g["params"]) for g in opt.param_groups])
+        self._plan = _BeginPlan(plan=plan, steps=steps, state=opt.state,
+                                groups_key=opt._groups_key(), hyper_steps=hyper_steps, row=row,
+                                nonempty=[bool(g["params"]) for g in opt.param_groups])
 
     def _native_begin(self):
         """begin() through the native checks, or None when the Python begin() must run."""
         opt = self.opt
         pl = self._plan
-        if (pl is None or pl[1] is not opt._steps or pl[2] is not opt.state
-                or pl[3] != opt._groups_key()):
+        # the plan points into the step buffer and holds the state dicts it was made from
+        if (pl is None or pl.steps is not opt._steps or pl.state is not opt.state
+                or pl.groups_key != opt._groups_key()):
             return None
         host = _lib._host
-        if host.prepare(pl[0], self._stream()) != host.READY:
+        if host.prepare(pl.plan, self._stream()) != host.READY:
             return None
         from .optimizer import _hyper
         self.native_begins += 1
-        hs = pl[4]
-        return [_hyper(g, float(hs[gi])) if nonempty else None
-                for gi, (g, nonempty) in enumerate(zip(opt.param_groups, pl[6]))]
+        return [_hyper(g, float(pl.hyper_steps[gi])) if nonempty else None
+                for gi, (g, nonempty) in enumerate(zip(opt.param_groups, pl.nonempty))]
 
     def segments(self, rank: int) -> list[tuple[int, int, int]]:
         """(param group, lo, hi) pieces of rank's slice, one per group it overlaps."""
