@@ -223,6 +223,20 @@ class _Launch:
             self.rows = _upload(rows, device)
 
 
+class _LaunchCache:
+    """The general path's launches, reused while `sig` (parameter and state pointers, the
+    hyperparameter grouping, the amsgrad settings) and the device are unchanged.  `grads`
+    are the gradient pointers the launch tables hold, or None after the native path
+    patched the tables itself.  A new object replaces it whenever the general path
+    rewrites the tables, so that a native plan made from the old one no longer applies."""
+
+    __slots__ = ("sig", "device", "launches", "norm_launch", "grads")
+
+    def __init__(self, sig, device, launches, norm_launch, grads):
+        self.sig, self.device, self.launches = sig, device, launches
+        self.norm_launch, self.grads = norm_launch, grads
+
+
 class _Fast:
     """What the native host path needs to take the next steps: the plan (_host.plan) and
     the Python objects whose identity says the plan still describes this optimizer."""
@@ -377,7 +391,7 @@ class FusedAdamW(Optimizer):
         self._steps = torch.zeros(0, dtype=torch.float32)
         self._step_views: list[torch.Tensor | None] = []
         self._copies: dict[int, torch.Tensor] = {}
-        self._launch_cache: tuple | None = None
+        self._launch_cache: _LaunchCache | None = None
         self._recs: list | None = None
         self._recs_key: tuple | None = None
         self._workspace: dict[torch.device, tuple] = {}
@@ -920,7 +934,7 @@ class FusedAdamW(Optimizer):
             return False
         self.native_steps += 1
         if rc == host.READY_MOVED:
-            fast.cache[4] = None      # the general path's record of the gradients is stale
+            fast.cache.grads = None   # the general path's record of the gradients is stale
         elif rc != host.READY:
             _lib.check(rc, "mi_adamw_set_grads")
         groups = self.param_groups
@@ -1104,9 +1118,9 @@ class FusedAdamW(Optimizer):
         # chunk tables kept.
         sig, grads = self._signature(entries, hyper_idx, hyper_ams)
         cache = self._launch_cache
-        if cache is not None and cache[0] == sig and cache[1] == device:
-            launches, norm_launch = cache[2], cache[3]
-            if cache[4] != grads:
+        if cache is not None and cache.sig == sig and cache.device == device:
+            launches, norm_launch = cache.launches, cache.norm_launch
+            if cache.grads != grads:
                 _refuse_under_capture("gradient tensors moved")
                 # torch checks shape, dtype and device when .grad is assigned; the
                 # kernels also need dense storage of the row's size
@@ -1118,8 +1132,7 @@ class FusedAdamW(Optimizer):
                     launch.patch_grads(garr if part[4] is None else garr[part[4]], device)
                 if norm_launch is not launches[0]:
                     norm_launch.patch_grads(garr, device)
-                # a list: the native path marks the gradients it moved (cache[4] = None)
-                self._launch_cache = [sig, device, launches, norm_launch, grads]
+                self._launch_cache = _LaunchCache(sig, device, launches, norm_launch, grads)
         else:
             _refuse_under_capture("the parameters, state or hyperparameter grouping changed")
             for rec, g in entries:
@@ -1131,7 +1144,7 @@ class FusedAdamW(Optimizer):
                 norm_launch = launches[0]
             else:
                 norm_launch = self._new_launch(entries, [0] * len(entries), False, device)
-            self._launch_cache = [sig, device, launches, norm_launch, grads]
+            self._launch_cache = _LaunchCache(sig, device, launches, norm_launch, grads)
 
         ev = self.timing_events
         if ev is not None:

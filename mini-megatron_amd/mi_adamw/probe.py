@@ -27,7 +27,7 @@ def time_probe(opt, launches: int = 20) -> float | None:
     cache = opt._launch_cache
     if cache is None:
         raise RuntimeError("time_probe: run one optimizer step first")
-    _, device, launches_, norm_launch, _ = cache
+    device, launches_, norm_launch = cache.device, cache.launches, cache.norm_launch
     if len(launches_) != 1 or launches_[0].n_chunks == 0:
         return None
     launch = launches_[0]

@@ -653,7 +653,7 @@ def test_thousands_of_ragged_tensors_with_clip(dev):
         torch.nn.utils.clip_grads_with_norm_(ref, 1.0, oopt.last_grad_norm.clone())
         topt.step()
     torch.cuda.synchronize()
-    launch = oopt._launch_cache[2][0]
+    launch = oopt._launch_cache.launches[0]
     assert launch.n_rows == len(shapes) and launch.tables
     exact = O.total_norm([to_np(p.grad) for p in ours])
     print("rows", launch.n_rows, "chunks", launch.n_chunks, "norm", oopt.last_grad_norm.item(),
