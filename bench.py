@@ -59,10 +59,10 @@ CONFIGS = {
 # The headline is the largest configuration that fits one GPU, the 6.7B flat clip + copy
 # step; the other configurations are timed in the same run, as rows of `sweep`.
 DEFAULT_CONFIG = "6.7b-flat-clip-copy"
-DEFAULT_SWEEP = ("1.3b-bf16state-copy-clip-flat", "1.3b-bf16state-copy-clip",
+DEFAULT_SWEEP = ("1.3b-bf16state-copy-clip", "1.3b-bf16state-copy-clip-flat",
                  "1.3b-bf16state-copy", "350m-master-clip-copy", "125m-clip", "125m-step1")
 # CPU baselines: the clip configurations of the workload list (125M, 350M, 1.3B, 6.7B)
-DEFAULT_CPU = ("6.7b-flat-clip-copy", "1.3b-bf16state-copy-clip-flat", "350m-master-clip-copy",
+DEFAULT_CPU = ("6.7b-flat-clip-copy", "1.3b-bf16state-copy-clip", "350m-master-clip-copy",
                "125m-clip")
 HP = dict(lr=3e-4, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.1)
 
