@@ -219,8 +219,10 @@ int mi_adamw_norm_from_sumsq(const double *d_sumsq, int32_t n, float max_norm, f
  * aligned for the vector path).  For the step after zero_grad() freed the gradients and
  * backward allocated new ones (main.py:204-209): only the gradient column of the table
  * changes.  rows, grads and vec are host arrays of n entries, carried to the device as
- * kernel arguments, so they may be reused as soon as the call returns.  Ordered on the
- * stream like every other call: launches queued earlier on it still see the old rows. */
+ * kernel arguments, so they may be reused as soon as the call returns.  Each row may
+ * appear at most once (MI_ADAMW_E_INVALID otherwise, as for a row outside [0, n_rows)).
+ * Ordered on the stream like every other call: launches queued earlier on it still see
+ * the old rows. */
 int mi_adamw_set_grads(mi_adamw_tensor *d_tensors, int32_t n_rows, int32_t n, const int32_t *rows,
                        const uint64_t *grads, const uint8_t *vec, void *stream);
 

@@ -38,6 +38,7 @@
 
 #include <atomic>
 #include <mutex>
+#include <vector>
 
 #include "mi_adamw.h"
 
@@ -1067,8 +1068,13 @@ int mi_adamw_set_grads(mi_adamw_tensor* d_tensors, int32_t n_rows, int32_t n,
                        void* stream) {
     if (!d_tensors || n_rows <= 0 || n < 0 || (n > 0 && (!rows || !grads || !vec)))
         return MI_ADAMW_E_INVALID;
-    for (int32_t i = 0; i < n; ++i)
-        if (rows[i] < 0 || rows[i] >= n_rows) return MI_ADAMW_E_INVALID;
+    // each row at most once: two patch lanes writing one row would race on its pointer
+    // and its alignment flag
+    std::vector<uint8_t> seen(static_cast<size_t>(n_rows), 0);
+    for (int32_t i = 0; i < n; ++i) {
+        if (rows[i] < 0 || rows[i] >= n_rows || seen[rows[i]]) return MI_ADAMW_E_INVALID;
+        seen[rows[i]] = 1;
+    }
     const hipStream_t s = static_cast<hipStream_t>(stream);
     for (int32_t base = 0; base < n; base += kPatchRows) {
         GradPatch patch;

@@ -218,6 +218,11 @@ static int cpu_checks(void)
               MI_ADAMW_E_INVALID, "gradient patch of a row outside the table");
     CHECK(mi_adamw_set_grads(NULL, 2, 1, bad_row, some_grad, vec0, NULL) == MI_ADAMW_E_INVALID,
           "gradient patch without a table");
+    const int32_t twice[3] = {0, 1, 0};
+    const uint64_t three_grads[3] = {4096, 8192, 12288};
+    const uint8_t vec3[3] = {1, 1, 0};
+    CHECK(mi_adamw_set_grads((mi_adamw_tensor *)fake, 2, 3, twice, three_grads, vec3, NULL) ==
+              MI_ADAMW_E_INVALID, "gradient patch naming one row twice");
     CHECK(mi_adamw_grad_norm_flat_noalloc(NULL, 10, 4096, 1.0f, fake_f, fake_f, NULL) ==
               MI_ADAMW_E_INVALID, "no-alloc norm without a gradient");
     CHECK(strstr(mi_adamw_strerror(MI_ADAMW_E_SCRATCH), "scratch") != NULL, "scratch error text");
