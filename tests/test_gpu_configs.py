@@ -111,8 +111,9 @@ def test_config2_125m_clip_100_chained(dev):
     print(f"config2 vs torch clip_grad_norm_ path, worst |d|/tol: p {wp:.3g} m {wm:.3g} v {wv:.3g}",
           flush=True)
     assert max(wp, wm, wv) <= 1
-    # The pure relative error |d| / |torch| of the north star (rel <= 1e-5 after 100
-    # chained steps), per tensor kind: the largest over elements with |torch| >= floor x
+    # The pure relative error |d| / |torch| of the parity target for this configuration
+    # (rel <= 1e-5 after 100 chained steps), per tensor kind: the largest over elements
+    # with |torch| >= floor x
     # rms(tensor) for several floors, and how many elements exceed 1e-5 with no floor.
     # Given the same norms the results are bit-identical (above); the differences come
     # from torch's fp32 norm-of-norms landing 1 ulp away from this float64 norm at some
