@@ -113,8 +113,8 @@ def test_config2_125m_clip_100_chained(dev):
     assert max(wp, wm, wv) <= 1
     # The pure relative error |d| / |torch| of the parity target for this configuration
     # (rel <= 1e-5 after 100 chained steps), per tensor kind: the largest over elements
-    # with |torch| >= floor x
-    # rms(tensor) for several floors, and how many elements exceed 1e-5 with no floor.
+    # with |torch| >= floor x rms(tensor) for several floors, and how many elements exceed
+    # 1e-5 with no floor.
     # Given the same norms the results are bit-identical (above); the differences come
     # from torch's fp32 norm-of-norms landing 1 ulp away from this float64 norm at some
     # steps.  The coefficient then differs by ~6e-8 relative, and the update by an
