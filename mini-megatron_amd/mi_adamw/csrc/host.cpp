@@ -21,7 +21,8 @@
 // Module _host (CPython extension, built against the installed torch):
 //   bind(addresses)                     function pointers of libmi_adamw (ctypes)
 //   plan(...) -> capsule                one launch's bookkeeping (see plan_new)
-//   prepare(plan, stream) -> int        steps 1-3: READY, READY_MOVED or FALLBACK
+//   prepare(plan, stream) -> int        steps 1-3: READY, READY_MOVED, FALLBACK or ERROR
+//   last_error(plan) -> int             the library's code behind the last ERROR
 //   norm(plan, stream, d_norm) -> int   mi_adamw_grad_norm* (or sumsq + finalize)
 //   update(plan, stream, hypers, n) -> int   mi_adamw_step*_prescaled
 //   sync_versions(plan, dict)           dict[id(p)] = (p._version, p.data_ptr())
@@ -40,9 +41,13 @@
 
 namespace {
 
+// prepare()'s statuses.  A library error is reported as kError, with the library's own
+// code (a negative MI_ADAMW_E_* or a positive hipError_t) kept in Plan::last_error, so
+// that no error code can read as one of the other statuses.
 constexpr int kReady = 0;
 constexpr int kFallback = 1;
 constexpr int kReadyMoved = 2;
+constexpr int kError = 3;
 
 // Entry points of libmi_adamw, bound once from the ctypes-loaded library so that both
 // paths call the same instance.
@@ -111,6 +116,7 @@ struct Plan {
     float* coef = nullptr;
     double* sumsq = nullptr;
     uint64_t stream = 0;             // the stream the tables were last used on
+    int last_error = 0;              // library code of prepare()'s last kError
     // scratch of prepare()
     std::vector<int32_t> prow;
     std::vector<uint64_t> pgrad;
@@ -325,7 +331,10 @@ fail:
 
 // The checks and the table update of one step.  Returns kReady / kReadyMoved after the
 // step counts were advanced (and moved gradients written to the table), kFallback with
-// nothing changed, or a positive library error code (raised by the caller).
+// nothing changed, or kError when mi_adamw_set_grads failed: then the step counts, the
+// host rows and the entries' gradient pointers are unchanged, while the device table may
+// hold part of the patch (its rows are patched 128 at a time), so the caller must drop
+// the tables and the plan before the next step.
 int prepare(Plan* pl, uint64_t stream) {
     if (stream != pl->stream) return kFallback;
     const size_t n = pl->e.size();
@@ -335,9 +344,11 @@ int prepare(Plan* pl, uint64_t stream) {
     for (size_t i = 0; i < n; ++i) {
         Entry& en = pl->e[i];
         const at::Tensor& p = THPVariable_Unpack(en.p);
-        // the row covers en.numel elements of p, its gradient and its state: a parameter
-        // narrowed in place through .data keeps its address but not its size
-        if (reinterpret_cast<uint64_t>(p.data_ptr()) != en.ptr[0] || p.numel() != en.numel)
+        // the row covers en.numel elements of p, its gradient and its state, stepped by
+        // memory position: a parameter narrowed or re-strided in place through .data keeps
+        // its address but no longer matches the row
+        if (reinterpret_cast<uint64_t>(p.data_ptr()) != en.ptr[0] || p.numel() != en.numel ||
+            !p.is_contiguous())
             return kFallback;
         const at::Tensor& g = p.grad();
         if (!g.defined() || g.layout() != c10::kStrided || !g.is_contiguous() ||
@@ -377,7 +388,10 @@ int prepare(Plan* pl, uint64_t stream) {
             const int rc = g_api.set_grads(pl->d_rows, pl->n_rows, m, pl->prow.data(),
                                            pl->pgrad.data(), pl->pvec.data(),
                                            reinterpret_cast<void*>(stream));
-            if (rc != MI_ADAMW_OK) return rc;
+            if (rc != MI_ADAMW_OK) {
+                pl->last_error = rc;
+                return kError;
+            }
         } else {
             // the single row of a table-free launch lives on the host
             pl->flat_row.grad = reinterpret_cast<float*>(pl->pgrad[0]);
@@ -427,6 +441,16 @@ PyObject* py_prepare(PyObject*, PyObject* const* args, Py_ssize_t nargs) {
         rc = kFallback;
     }
     return PyLong_FromLong(rc);
+}
+
+PyObject* py_last_error(PyObject*, PyObject* const* args, Py_ssize_t nargs) {
+    if (nargs != 1) {
+        PyErr_SetString(PyExc_TypeError, "last_error(plan)");
+        return nullptr;
+    }
+    Plan* pl = get_plan(args[0]);
+    if (!pl) return nullptr;
+    return PyLong_FromLong(pl->last_error);
 }
 
 PyObject* py_norm(PyObject*, PyObject* const* args, Py_ssize_t nargs) {
@@ -522,6 +546,8 @@ PyMethodDef kMethods[] = {
     {"plan", py_plan, METH_VARARGS, "the bookkeeping of one launch"},
     {"prepare", reinterpret_cast<PyCFunction>(reinterpret_cast<void (*)()>(py_prepare)),
      METH_FASTCALL, "checks, moved gradients, step counts"},
+    {"last_error", reinterpret_cast<PyCFunction>(reinterpret_cast<void (*)()>(py_last_error)),
+     METH_FASTCALL, "the library code behind prepare()'s last ERROR"},
     {"norm", reinterpret_cast<PyCFunction>(reinterpret_cast<void (*)()>(py_norm)), METH_FASTCALL,
      "enqueue the norm pass"},
     {"update", reinterpret_cast<PyCFunction>(reinterpret_cast<void (*)()>(py_update)),
@@ -542,7 +568,8 @@ PyMODINIT_FUNC PyInit__host(void) {
     if (!m) return nullptr;
     if (PyModule_AddIntConstant(m, "READY", kReady) < 0 ||
         PyModule_AddIntConstant(m, "READY_MOVED", kReadyMoved) < 0 ||
-        PyModule_AddIntConstant(m, "FALLBACK", kFallback) < 0) {
+        PyModule_AddIntConstant(m, "FALLBACK", kFallback) < 0 ||
+        PyModule_AddIntConstant(m, "ERROR", kError) < 0) {
         Py_DECREF(m);
         return nullptr;
     }

@@ -706,6 +706,11 @@ class FusedAdamW(Optimizer):
         change (compared by identity, so a parameter swapped into a list in place counts)."""
         key = tuple(tuple(map(id, g["params"])) for g in self.param_groups)
         if self._recs is None or self._recs_key != key:
+            if self._flat is not None and any(id(p) not in self._flat.offsets
+                                              for g in self.param_groups for p in g["params"]):
+                # the flat buffers were laid out at construction and have no slice for it
+                raise NotImplementedError("FusedAdamW(flat_buffer=True): a parameter put into "
+                                          "a param group after construction is not supported")
             # a parameter put into a group's list directly gets its step slot (and bf16 copy)
             self._register_params([p for g in self.param_groups for p in g["params"]])
             self._recs = [_Rec(gi, p, self._slots[id(p)])
@@ -927,16 +932,31 @@ class FusedAdamW(Optimizer):
                 return self._fast_launch(fast, host)
         return self._fast_launch(fast, host)
 
-    def _fast_launch(self, fast: _Fast, host) -> bool:
-        stream = torch._C._cuda_getCurrentRawStream(fast.dev_index)
+    def _fast_prepare(self, fast: _Fast, host, stream: int) -> bool:
+        """The native checks, gradient patch and step counting of one step: True when the
+        native path takes the step, False (nothing changed) when the general path must.
+        A failed gradient patch raises, after dropping the plan and the tables: the step
+        counts are unchanged, but the device table may hold part of the patch."""
         rc = host.prepare(fast.plan, stream)
         if rc == host.FALLBACK:
             return False
-        self.native_steps += 1
+        if rc == host.ERROR:
+            code = host.last_error(fast.plan)
+            self._fast = None
+            self._launch_cache = None
+            raise _lib.MiAdamwError(f"mi_adamw_set_grads failed: {_lib.strerror(code)} "
+                                    f"(code {code})")
         if rc == host.READY_MOVED:
             fast.cache.grads = None   # the general path's record of the gradients is stale
         elif rc != host.READY:
-            _lib.check(rc, "mi_adamw_set_grads")
+            raise RuntimeError(f"mi_adamw._host.prepare returned an unknown status {rc}")
+        self.native_steps += 1
+        return True
+
+    def _fast_launch(self, fast: _Fast, host) -> bool:
+        stream = torch._C._cuda_getCurrentRawStream(fast.dev_index)
+        if not self._fast_prepare(fast, host, stream):
+            return False
         groups = self.param_groups
         harr = fast.harr
         for h, gi in enumerate(fast.hyper_group):
@@ -1067,8 +1087,10 @@ class FusedAdamW(Optimizer):
         are split into launches), and the parameter and state pointers, which rarely
         change; and the gradient pointers, which change whenever zero_grad() frees the
         gradients and backward allocates them elsewhere."""
-        # the element count too: a parameter narrowed in place through .data keeps its address
-        sig = [(rec.p.data_ptr(), rec.p.numel(), rec.st["exp_avg"].data_ptr(),
+        # the element count and contiguity too: a parameter narrowed or re-strided in place
+        # through .data keeps its address (a rebuild then checks it)
+        sig = [(rec.p.data_ptr(), rec.p.numel(), rec.p.is_contiguous(),
+                rec.st["exp_avg"].data_ptr(),
                 rec.st["exp_avg_sq"].data_ptr(), _ptr(rec.st.get("max_exp_avg_sq")))
                for rec, _ in entries]
         sig.append(tuple(hyper_idx))

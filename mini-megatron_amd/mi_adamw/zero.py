@@ -71,14 +71,26 @@ class ZeroRangeStep:
       ``finalize(sumsq)``            norm and coefficient from the ranks' sums;
       ``update(rank, hypers, coef)`` the AdamW update of the rank's slice.
     ``step()`` runs them for every rank in turn on one GPU.
+
+    ``grad_prescale``: the factor every gradient is multiplied by in both kernels (the
+    world-size division of ``allreduce_grads``).  None takes the optimizer's own
+    ``grad_prescale``, so ``step()`` here and ``opt.step()`` see the same gradients.  An
+    explicit value that differs from a pre-scale the optimizer was built with raises;
+    over an optimizer without one (1) it applies to the ranks' kernels only.
     """
 
-    def __init__(self, opt, world: int, grad_prescale: float = 1.0):
+    def __init__(self, opt, world: int, grad_prescale: float | None = None):
         flat = getattr(opt, "_flat", None)
         if flat is None:
             raise ValueError("ZeroRangeStep needs FusedAdamW(flat_buffer=True)")
         if opt.capturable:
             raise NotImplementedError("ZeroRangeStep: capturable=True is not supported")
+        own = float(opt.grad_prescale)
+        if grad_prescale is None:
+            grad_prescale = own
+        elif own != 1.0 and float(np.float32(grad_prescale)) != own:
+            raise ValueError(f"ZeroRangeStep: grad_prescale={grad_prescale} differs from the "
+                             f"optimizer's grad_prescale={own}")
         self.opt = opt
         self.flat = flat
         self.world = int(world)

@@ -331,6 +331,55 @@ def test_parameter_swapped_into_a_group_in_place(dev):
     assert oopt.native_steps == before
 
 
+def test_parameter_swapped_into_a_flat_group_is_refused(dev):
+    """The flat layout's buffers have no slice for a parameter put into a group's list
+    after construction: the step refuses it before anything is launched or changed."""
+    import mi_adamw
+    ours = make_params(SHAPES, dev)
+    oopt = mi_adamw.FusedAdamW(ours, **HP, max_grad_norm=1.0, flat_buffer=True)
+    spacer = []
+    for k in range(2):
+        _assign(ours, ours, _fresh_grads(ours, k), spacer, inplace=True)
+        oopt.step()
+    before = oopt._flat.param.clone()
+    new = torch.nn.Parameter(torch.randn(SHAPES[4], device=dev))
+    new.grad = torch.randn_like(new)
+    oopt.param_groups[0]["params"][4] = new
+    with pytest.raises(NotImplementedError, match="after construction"):
+        oopt.step()
+    torch.cuda.synchronize()
+    assert torch.equal(oopt._flat.param, before)
+
+
+@pytest.mark.parametrize("layout", ["tables", "single"])
+def test_parameter_restrided_in_place_is_refused(dev, layout):
+    """p.data replaced by a transposed view of its own storage (same address and element
+    count, another element order) with a dense gradient of the new shape: the kernels
+    step by memory position, so both step paths must refuse it rather than pair p's
+    elements with the wrong gradients."""
+    import mi_adamw
+    shapes = [(65, 63)] if layout == "single" else SHAPES
+    ours = make_params(shapes, dev)
+    oopt = mi_adamw.FusedAdamW(ours, **HP, max_grad_norm=1.0)
+    spacer = []
+    for k in range(3):
+        _assign(ours, ours, _fresh_grads(ours, k), spacer)
+        oopt.step()
+    assert oopt.native_steps == 2
+    p = ours[0]
+    ptr = p.data_ptr()
+    with torch.no_grad():
+        p.data = p.data.t()
+    assert p.data_ptr() == ptr and not p.is_contiguous()
+    before = [q.detach().clone() for q in ours]
+    _assign(ours, ours, _fresh_grads(ours, 3), spacer)
+    with pytest.raises(NotImplementedError, match="contiguous"):
+        oopt.step()
+    torch.cuda.synchronize()
+    assert oopt.native_steps == 2
+    assert all(torch.equal(q, b) for q, b in zip(ours, before))
+
+
 @pytest.mark.parametrize("layout", ["tables", "single"])
 def test_parameter_narrowed_in_place_is_refused(dev, layout):
     """p.data narrowed to a view at the same address, then a gradient of the new size:

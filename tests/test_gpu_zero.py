@@ -159,6 +159,29 @@ def test_range_step_equals_flat_step(dev, state_dtype, groups):
         del a, b, oa, ob, zs
 
 
+def test_range_step_takes_the_optimizers_prescale(dev):
+    """An optimizer built with grad_prescale, driven by ZeroRangeStep without one: the
+    range step pre-scales as the optimizer's own step does, bit for bit."""
+    import mi_adamw
+    world = 4
+    prescale = mi_adamw.dp_prescale(world)
+    a, b, oa, ob = _flat_pair(dev, SHAPES, torch.float32, 2, prescale)
+    zs = mi_adamw.ZeroRangeStep(ob, world)
+    assert zs.grad_prescale == ob.grad_prescale == prescale
+    with pytest.raises(ValueError, match="differs"):
+        mi_adamw.ZeroRangeStep(ob, world, grad_prescale=1.0)
+    for step in range(2):
+        set_grads(a, step, 3e-2 * world)
+        for p, q in zip(a, b):
+            q.grad.copy_(p.grad)
+        oa.step()
+        nb = zs.step()
+        torch.cuda.synchronize()
+        assert torch.equal(oa.last_grad_norm.view(torch.int32), nb.view(torch.int32))
+    for key in ("param", "exp_avg", "exp_avg_sq", "copy"):
+        assert torch.equal(getattr(oa._flat, key), getattr(ob._flat, key)), key
+
+
 def test_range_step_split_calls_match_step(dev):
     """The per-rank calls in the order a multi-GPU rank makes them: each rank's sum into its
     own float64, the sums combined (the all-reduce), the finalize from the one total."""

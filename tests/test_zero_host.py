@@ -68,3 +68,20 @@ def test_range_step_needs_the_flat_layout():
     p = [torch.nn.Parameter(torch.zeros(4))]
     with pytest.raises(ValueError):
         ZeroRangeStep(mi_adamw.FusedAdamW(p), 2)
+
+
+def test_range_step_takes_the_optimizers_prescale():
+    """grad_prescale=None takes the optimizer's own pre-scale; an explicit value that
+    differs from one the optimizer was built with is refused; over an optimizer without a
+    pre-scale an explicit value applies to the ranks' kernels."""
+    import types
+    flat = types.SimpleNamespace(total=4096, device=torch.device("cpu"))
+    third = float(np.float32(1.0 / 3))
+    opt = types.SimpleNamespace(_flat=flat, capturable=False, grad_prescale=third)
+    assert ZeroRangeStep(opt, 2).grad_prescale == third
+    assert ZeroRangeStep(opt, 2, grad_prescale=1.0 / 3).grad_prescale == third
+    with pytest.raises(ValueError, match="differs"):
+        ZeroRangeStep(opt, 2, grad_prescale=0.5)
+    plain = types.SimpleNamespace(_flat=flat, capturable=False, grad_prescale=1.0)
+    assert ZeroRangeStep(plain, 2).grad_prescale == 1.0
+    assert ZeroRangeStep(plain, 4, grad_prescale=dp_prescale(4)).grad_prescale == 0.25
