@@ -7,16 +7,23 @@ The host extension ``_host`` (csrc/host.cpp: FusedAdamW.step()'s steady-state
 bookkeeping in C++) is imported with it and bound to the same library's entry
 points.  There is no CPU fallback: if either is missing or was built for
 another ABI, loading raises.
+
+Both load from this package's directory, or from the directory named by the
+environment variable MI_ADAMW_LIB_DIR (another build of the same sources, e.g.
+the sanitizer build of ``python -m mi_adamw.build --sanitize DIR``).
 """
 from __future__ import annotations
 
 import ctypes
+import importlib.util
 import os
+import sysconfig
 
 import torch
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(HERE, "libmi_adamw.so")
+LIB_DIR = os.environ.get("MI_ADAMW_LIB_DIR") or HERE
+LIB_PATH = os.path.join(LIB_DIR, "libmi_adamw.so")
 
 ABI_VERSION = 7
 MAX_HYPER = 16
@@ -193,7 +200,7 @@ def load(path: str = LIB_PATH) -> ctypes.CDLL:
         raise MiAdamwError(f"libmi_adamw ABI mismatch: library reports {version!r}")
     global _host
     try:
-        from . import _host as host
+        host = _import_host()
     except ImportError as e:
         raise MiAdamwError(
             f"mi_adamw's host extension (_host) is not built or does not load ({e}); build it "
@@ -203,6 +210,20 @@ def load(path: str = LIB_PATH) -> ctypes.CDLL:
     _host = host
     _lib = lib
     return lib
+
+
+def _import_host():
+    """The host extension: this package's ``_host``, or the one in MI_ADAMW_LIB_DIR."""
+    if LIB_DIR == HERE:
+        from . import _host as host
+        return host
+    path = os.path.join(LIB_DIR, "_host" + sysconfig.get_config_var("EXT_SUFFIX"))
+    spec = importlib.util.spec_from_file_location(__package__ + "._host", path)
+    if spec is None or not os.path.exists(path):
+        raise ImportError(f"no host extension at {path}")
+    host = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(host)
+    return host
 
 
 def host():

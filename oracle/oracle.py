@@ -53,7 +53,9 @@ from dataclasses import dataclass
 import numpy as np
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-_LIB_PATH = os.path.join(_HERE, "liboracle.so")
+# MI_ADAMW_ORACLE_LIB: another build of adamw_oracle.c (the sanitizer build, `make -C
+# oracle asan OUT=DIR`)
+_LIB_PATH = os.environ.get("MI_ADAMW_ORACLE_LIB") or os.path.join(_HERE, "liboracle.so")
 
 
 class OpModel(ctypes.Structure):
