@@ -484,14 +484,53 @@ def range_shard_rows(opt, world: int, steps: int = 10, warmup: int = 3) -> dict:
     }
 
 
+def placement_ab(opt, orig: dict, streams, steps: int, warmup: int, rounds: int = 4) -> dict:
+    """The step on the optimizer's original streams against the streams place_buffers
+    chose, alternating in this process (same parameters and gradients): `rounds` rounds of
+    `steps` timed steps on each, after `warmup` untimed ones at every switch."""
+    placed = streams.current()
+    res = {"original": [], "placed": []}
+    for r in range(rounds):
+        order = (("original", orig), ("placed", placed))
+        for label, bufs in (order if r % 2 == 0 else order[::-1]):
+            streams.adopt(bufs)
+            opt._launch_cache = None
+            opt._fast = None
+            gpu_ms, _, _, _, _ = time_fused(opt, steps, warmup)
+            res[label].append(round(gpu_ms, 5))
+    streams.adopt(placed)
+    opt._launch_cache = None
+    opt._fast = None
+    gain = statistics.mean(res["original"]) / statistics.mean(res["placed"]) - 1.0
+    return {"rounds": rounds, "steps_per_round": steps, "original_ms": res["original"],
+            "placed_ms": res["placed"], "gain": round(gain, 5)}
+
+
 def run_config(name: str, steps: int, warmup: int, device, with_context: bool,
                capturable: bool = False, write_grads: bool = False,
-               range_world: int = 0) -> dict:
+               range_world: int = 0, trials: int = 0, ab: bool = False) -> dict:
     shape_name, clip, state, copy, flat, start_step, gstd = CONFIGS[name]
     log(f"[bench] {name}: building {shape_name} set" + (" (capturable)" if capturable else "")
         + (" (clipped grads written back)" if write_grads else ""))
     params, opt, n, n_tensors = build_set(name, device, capturable, write_grads)
     total_b, upd_b = bytes_per_param(clip, state, copy, write_grads)
+    placement = None
+    if trials > 0 and not capturable:
+        # where the streams the update writes live: the fastest of `trials` more
+        # allocations by the update's memory-only twin (FusedAdamW.place_buffers)
+        from mi_adamw import placement as pl
+        opt.step()                      # the tables exist and every state entry is created
+        torch.cuda.synchronize()
+        streams = orig = None
+        if ab:
+            streams = pl._FlatStreams(opt, device) if flat else pl._TableStreams(opt, device)
+            orig = streams.current()    # kept alive for the A/B
+        placement = opt.place_buffers(trials=trials)
+        log(f"[bench] {name}: place_buffers {placement}")
+        if ab:
+            placement["ab"] = placement_ab(opt, orig, streams, steps, warmup)
+            log(f"[bench] {name}: placement A/B {placement['ab']}")
+        del orig, streams
     log(f"[bench] {name}: {n} params in {n_tensors} tensors; timing {steps} steps")
     gpu_ms, wall_ms, norm_ms, upd_ms, step_ms = time_fused(opt, steps, warmup)
     # after the timed region: the update's memory-only twin on the same tensors
@@ -512,6 +551,7 @@ def run_config(name: str, steps: int, warmup: int, device, with_context: bool,
         "bytes_per_param": total_b, "bytes_per_step": step_bytes,
         "gbs": step_bytes / gpu_ms / 1e6, "pct_of_peak": 100 * step_bytes / gpu_ms / 1e6 / PEAK_HBM_GBS,
         "params_per_s": n / gpu_ms * 1e3,
+        "placement": placement,
         "norm_kernel_ms": norm_avg, "update_kernel_ms": upd_avg,
         "update_kernel_ms_p90": _pct(upd_ms, 0.9),
         "step_ms_median": statistics.median(step_ms), "step_ms_p90": _pct(step_ms, 0.9),
@@ -608,6 +648,13 @@ def main() -> int:
                     help="FusedAdamW(clip_write_grads=True): the update also stores the clipped "
                          "gradients back, as torch's clip_grad_norm_ does (+4 B per parameter; "
                          "clip configurations only)")
+    ap.add_argument("--placement-trials", type=int, default=8,
+                    help="before each configuration's timed steps, FusedAdamW.place_buffers "
+                         "with this many candidate placements of the streams the update writes "
+                         "(0: keep the first allocation)")
+    ap.add_argument("--placement-ab", action="store_true",
+                    help="also time each configuration's step on its original streams against "
+                         "the placed ones, alternating rounds in this process")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="after the timed steps, run 3 plain 1 GiB device copies (torch copy_) "
                          "so a counter run (rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE) sees a "
@@ -646,7 +693,8 @@ def main() -> int:
     results = {nm: run_config(nm, args.steps, args.warmup, device,
                               with_context=not args.no_context and nm == args.config,
                               capturable=args.capturable, write_grads=args.clip_write_grads,
-                              range_world=args.range_world if nm == args.config else 0)
+                              range_world=args.range_world if nm == args.config else 0,
+                              trials=args.placement_trials, ab=args.placement_ab)
                for nm in names}
     if args.calibrate_copy:
         src = torch.ones(1 << 28, device=device)
@@ -690,6 +738,7 @@ def main() -> int:
         "step_ms_median": round(head["step_ms_median"], 5),
         "step_ms_p90": round(head["step_ms_p90"], 5),
         "roofline": _rounded(head["roofline"]),
+        "placement": head["placement"],
     }
     if "torch_gpu_ms" in head:
         line["torch_gpu_ms"] = head["torch_gpu_ms"]

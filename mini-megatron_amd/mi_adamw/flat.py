@@ -160,6 +160,42 @@ class FlatLayout:
             v = self._copy_views[id(p)] = self._view(self.copy, p)
         return v
 
+    def _holds(self, buf: torch.Tensor, p: torch.Tensor, t: torch.Tensor | None) -> bool:
+        """t is p's slice of buf (a view at p's offset with p's element count)."""
+        off = self.offsets[id(p)]
+        return (t is not None and t.data_ptr() == buf.data_ptr() + buf.element_size() * off
+                and t.numel() == self.numels[id(p)])
+
+    @torch.no_grad()
+    def adopt_buffers(self, bufs: dict, params, state) -> None:
+        """Move the values of the buffers named in `bufs` ("param", "exp_avg", "exp_avg_sq",
+        "copy") into the given tensors of the same size and dtype, and point everything
+        that was a view of an old buffer (parameters' .data, state entries) at the new
+        one.  A parameter or state entry that was not a view stays as it is; the next step
+        takes its values into the new slice, as it would have into the old one."""
+        old = {name: getattr(self, name) for name in bufs}
+        for name, new in bufs.items():
+            if new.shape != old[name].shape or new.dtype != old[name].dtype:
+                raise ValueError(f"adopt_buffers: {name} differs in size or dtype")
+        was = {}
+        for p in params:
+            st = state.get(p) or {}
+            was[id(p)] = {"param": "param" in bufs and self._holds(old["param"], p, p)}
+            for key in ("exp_avg", "exp_avg_sq"):
+                was[id(p)][key] = key in bufs and self._holds(old[key], p, st.get(key))
+        for name, new in bufs.items():
+            if new is not old[name]:
+                new.copy_(old[name])
+            setattr(self, name, new)
+        self._copy_views = {}
+        for p in params:
+            if was[id(p)]["param"]:
+                p.data = self._view(self.param, p)
+            st = state.get(p)
+            for key in ("exp_avg", "exp_avg_sq"):
+                if was[id(p)][key]:
+                    st[key] = self._view(getattr(self, key), p)
+
     def zero_grads(self, param_groups) -> None:
         self.grad.zero_()
         for g in param_groups:

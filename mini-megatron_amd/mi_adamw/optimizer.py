@@ -598,6 +598,22 @@ class FusedAdamW(Optimizer):
                 self._init_vmax(p, st)
             st["max_exp_avg_sq"].copy_(max_exp_avg_sq)
 
+    def place_buffers(self, trials: int = 8, launches: int = 3, rounds: int = 2,
+                      reserve_bytes: int | None = None) -> dict:
+        """Move the streams the update writes to the fastest of up to `trials` newly
+        allocated places, chosen by timing the update's memory-only twin on each against
+        the current parameters and gradients (so call it after a backward, or with the
+        gradients set).  Tables: exp_avg, exp_avg_sq and the bf16 copy become views of one
+        block per stream; flat: the parameter, moment and copy buffers move.  Values are
+        moved bit for bit.  Transient memory: one stream set per candidate, as many as fit
+        keeping `reserve_bytes` (default max(2 GiB, 2% of HBM)) free.  Returns a report
+        of the candidates' twin times and the choice.  No counterpart in torch: the
+        MI355X's bandwidth for the update's mix depends on the physical pages of its
+        written streams (10-13% between placements)."""
+        from .placement import place_buffers
+        return place_buffers(self, trials=trials, launches=launches, rounds=rounds,
+                             reserve_bytes=reserve_bytes)
+
     def _amsgrad_of(self, p: torch.Tensor) -> bool:
         for g in self.param_groups:
             if any(q is p for q in g["params"]):

@@ -1,0 +1,180 @@
+"""FusedAdamW.place_buffers on the GPU: moving the written streams changes no result.
+
+place_buffers times the update's memory-only twin on the optimizer's current streams and
+on newly allocated sets, and moves the values into the fastest set.  Which set wins
+depends on the box, so the move itself is also forced through the layout's stream
+classes.  Either way, the steps that follow must be bit-identical to those of the same
+optimizer left where it was (parameters, moments, bf16 copy, clip norm), the native host
+path must take the steps after the move, and a checkpoint must still interchange with
+torch.optim.AdamW.
+"""
+from __future__ import annotations
+
+import gc
+import io
+
+import pytest
+import torch
+
+from _helpers import clone_params, load_states, make_params, midtrain_state, set_grads
+
+pytestmark = pytest.mark.gpu
+
+HP = dict(lr=3e-4, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.1)
+SHAPES = [(64, 48), (48,), (48,), (144, 48), (4099,), (3,), (7, 5), (70001,), (0,),
+          (65536 + 12,), (1024,)]
+
+
+@pytest.fixture
+def dev():
+    if not torch.cuda.is_available():
+        pytest.fail("GPU test run without a ROCm GPU")
+    yield torch.device("cuda", 0)
+    gc.collect()
+    torch.cuda.empty_cache()
+
+
+def _pair(dev, state_dtype, flat, copy=True):
+    import mi_adamw
+    a = make_params(SHAPES, dev)
+    b = clone_params(a)
+    kw = dict(**HP, max_grad_norm=1.0, bf16_copy=copy, state_dtype=state_dtype,
+              flat_buffer=flat)
+    oa, ob = mi_adamw.FusedAdamW(a, **kw), mi_adamw.FusedAdamW(b, **kw)
+    states = midtrain_state(a, 1000.0)
+    load_states(oa, a, states)
+    load_states(ob, b, states)
+    return a, b, oa, ob
+
+
+def _bits(t):
+    t = t.detach()
+    return t.view(torch.int16) if t.dtype == torch.bfloat16 else t.view(torch.int32)
+
+
+def _assert_same(a, b, oa, ob):
+    for p, q in zip(a, b):
+        assert torch.equal(_bits(p), _bits(q))
+        for key in ("exp_avg", "exp_avg_sq"):
+            assert torch.equal(_bits(oa.state[p][key]), _bits(ob.state[q][key])), key
+        if oa.bf16_copy:
+            assert torch.equal(_bits(oa.bf16_param(p)), _bits(ob.bf16_param(q)))
+    assert torch.equal(_bits(oa.last_grad_norm), _bits(ob.last_grad_norm))
+
+
+def _steps(a, b, oa, ob, first, n):
+    for k in range(first, first + n):
+        set_grads(a, k, 3e-2)
+        for p, q in zip(a, b):
+            q.grad.copy_(p.grad) if q.grad is not None else setattr(q, "grad", p.grad.clone())
+        oa.step()
+        ob.step()
+    torch.cuda.synchronize()
+
+
+@pytest.mark.parametrize("flat", [False, True])
+@pytest.mark.parametrize("state_dtype", [torch.float32, torch.bfloat16])
+def test_forced_move_changes_no_result(dev, flat, state_dtype):
+    from mi_adamw import placement
+    a, b, oa, ob = _pair(dev, state_dtype, flat)
+    _steps(a, b, oa, ob, 0, 2)
+    streams = (placement._FlatStreams(oa, dev) if flat else placement._TableStreams(oa, dev))
+    def ptrs():
+        # an empty tensor reports data_ptr() 0 wherever it lives: only non-empty ones count
+        return {n: [t.data_ptr() for t in (v if isinstance(v, list) else [v]) if t.numel()]
+                for n, v in streams.current().items()}
+    before = ptrs()
+    cand = streams.allocate()
+    streams.adopt(cand)
+    oa._launch_cache = None
+    oa._fast = None
+    after = ptrs()
+    assert all(x != y for n in before for x, y in zip(before[n], after[n])), "nothing moved"
+    if flat:
+        assert all(oa._flat.is_param_view(p) for p in a if p.numel())
+        assert oa._flat.param.data_ptr() == cand["param"].data_ptr()
+    else:
+        # every state entry and copy is a view of its stream's block, in order
+        blk = oa.state[a[0]]["exp_avg"].untyped_storage().data_ptr()
+        assert all(oa.state[p]["exp_avg"].untyped_storage().data_ptr() == blk for p in a)
+    _assert_same(a, b, oa, ob)                     # the move itself changes no value
+    native = oa.native_steps
+    _steps(a, b, oa, ob, 2, 4)
+    _assert_same(a, b, oa, ob)
+    assert oa.native_steps >= native + 2           # rebuilt once, then native again
+
+
+@pytest.mark.parametrize("flat", [False, True])
+def test_place_buffers_report_and_parity(dev, flat):
+    a, b, oa, ob = _pair(dev, torch.bfloat16, flat)
+    _steps(a, b, oa, ob, 0, 1)
+    rep = oa.place_buffers(trials=3)
+    print(f"place_buffers ({'flat' if flat else 'tables'}): {rep}", flush=True)
+    assert rep["layout"] == ("flat" if flat else "tables")
+    assert rep["candidates"] == 4 and len(rep["twin_ms"]) == 4
+    assert 0 <= rep["chosen"] < 4 and rep["twin_ms"][rep["chosen"]] == min(rep["twin_ms"])
+    names = ["param", "exp_avg", "exp_avg_sq", "copy"] if flat else ["exp_avg", "exp_avg_sq",
+                                                                     "copy"]
+    assert rep["streams"] == names
+    assert rep["transient_bytes"] == 3 * rep["set_bytes"]
+    _assert_same(a, b, oa, ob)
+    _steps(a, b, oa, ob, 1, 3)
+    _assert_same(a, b, oa, ob)
+
+
+def test_checkpoint_after_a_move_interchanges_with_torch(dev):
+    """Tables, fp32 state: after a forced move the state entries are views of the blocks;
+    a state_dict taken then loads into torch.optim.AdamW and both step alike."""
+    import mi_adamw
+    from mi_adamw import placement
+    ref = make_params(SHAPES, dev)
+    ours = clone_params(ref)
+    oopt = mi_adamw.FusedAdamW(ours, **HP)
+    states = midtrain_state(ref, 1000.0)
+    load_states(oopt, ours, states)
+    set_grads(ours, 0, 3e-2)
+    oopt.step()
+    streams = placement._TableStreams(oopt, dev)
+    streams.adopt(streams.allocate())
+    oopt._launch_cache = None
+    oopt._fast = None
+    with torch.no_grad():
+        for p, q in zip(ref, ours):
+            p.copy_(q)
+    topt = torch.optim.AdamW(ref, foreach=False, **HP)
+    buf = io.BytesIO()
+    torch.save(oopt.state_dict(), buf)
+    buf.seek(0)
+    topt.load_state_dict(torch.load(buf, weights_only=True))
+    for k in range(1, 4):
+        set_grads(ref, k, 3e-2)
+        set_grads(ours, k, 3e-2)
+        topt.step()
+        oopt.step()
+    torch.cuda.synchronize()
+    for p, q in zip(ref, ours):
+        assert torch.equal(_bits(p), _bits(q))
+        for key in ("exp_avg", "exp_avg_sq"):
+            assert torch.equal(_bits(topt.state[p][key]), _bits(oopt.state[q][key]))
+
+
+def test_place_buffers_refusals(dev):
+    import mi_adamw
+    ps = make_params(SHAPES[:3], dev)
+    with pytest.raises(RuntimeError, match="no parameter has optimizer state"):
+        mi_adamw.FusedAdamW(ps, **HP).place_buffers(trials=1)
+    with pytest.raises(NotImplementedError, match="amsgrad"):
+        mi_adamw.FusedAdamW(ps, **HP, amsgrad=True).place_buffers(trials=1)
+    with pytest.raises(NotImplementedError, match="capturable"):
+        mi_adamw.FusedAdamW(ps, **HP, capturable=True).place_buffers(trials=1)
+    opt = mi_adamw.FusedAdamW(ps, **HP)
+    set_grads(ps, 0, 1e-2)
+    opt.step()
+    for p in ps:
+        p.grad = None
+    with pytest.raises(RuntimeError, match="gradient"):
+        opt.place_buffers(trials=1)
+    # no memory for a candidate: only the current set is timed, nothing moves
+    set_grads(ps, 1, 1e-2)
+    rep = opt.place_buffers(trials=4, reserve_bytes=1 << 50)
+    assert rep["candidates"] == 1 and rep["chosen"] == 0 and rep["transient_bytes"] == 0
