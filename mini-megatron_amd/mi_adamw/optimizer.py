@@ -280,9 +280,14 @@ class FusedAdamW(Optimizer):
                       a summing all-reduce.  ``p.grad`` is left as it was (with
                       clip_write_grads the stored gradient is the pre-scaled,
                       clipped one).
+    place_trials:     if > 0, run ``place_buffers(place_trials)`` once, after
+                      the first step that leaves every parameter with state:
+                      the streams the update writes move to the fastest of up
+                      to this many more allocations (report in ``placement``).
 
     Not supported (NotImplementedError at construction): differentiable, betas
-    as tensors, param groups with different capturable settings.
+    as tensors, param groups with different capturable settings, place_trials
+    with capturable or amsgrad.
     """
 
     def __init__(
@@ -306,6 +311,7 @@ class FusedAdamW(Optimizer):
         flat_buffer: bool = False,
         chunk_elems: int = DEFAULT_CHUNK_ELEMS,
         grad_prescale: float = 1.0,
+        place_trials: int = 0,
     ) -> None:
         # adam.py:58-86, in the same order and with the same messages.
         if isinstance(lr, torch.Tensor):
@@ -355,6 +361,11 @@ class FusedAdamW(Optimizer):
         if capturable and grad_prescale != 1.0:
             raise NotImplementedError("FusedAdamW: grad_prescale with capturable=True is not "
                                       "supported")
+        if not isinstance(place_trials, int) or place_trials < 0:
+            raise ValueError(f"Invalid place_trials: {place_trials}")
+        if place_trials and (capturable or amsgrad):
+            raise NotImplementedError("FusedAdamW: place_trials with capturable=True or "
+                                      "amsgrad=True is not supported")
 
         self.capturable = bool(capturable)
         self.max_grad_norm = None if max_grad_norm is None else float(max_grad_norm)
@@ -364,6 +375,7 @@ class FusedAdamW(Optimizer):
         self.flat_buffer = bool(flat_buffer)
         self.chunk_elems = int(chunk_elems)
         self.grad_prescale = grad_prescale
+        self.place_trials = place_trials
         self.max_blocks = 0
         self._reset_bookkeeping()
 
@@ -381,7 +393,7 @@ class FusedAdamW(Optimizer):
             self._flat = FlatLayout(self.param_groups, self.state_dtype, self.bf16_copy)
 
     _OPTIONS = ("capturable", "max_grad_norm", "clip_write_grads", "state_dtype", "bf16_copy",
-                "flat_buffer", "chunk_elems", "grad_prescale", "max_blocks")
+                "flat_buffer", "chunk_elems", "grad_prescale", "max_blocks", "place_trials")
 
     def _reset_bookkeeping(self) -> None:
         """The state this class keeps beside torch's: step slots, the packed step buffer,
@@ -401,6 +413,8 @@ class FusedAdamW(Optimizer):
         self._fast: _Fast | None = None
         self.native_steps = 0          # steps taken by the native host path
         self.timing_events = None
+        # place_trials: place_buffers' report once it has run (None until then)
+        self.placement: dict | None = None
 
     # ------------------------------------------------------------------ torch API
 
@@ -837,6 +851,11 @@ class FusedAdamW(Optimizer):
             # the launch wrote these masters' copies
             for rec, _ in entries:
                 self._copy_sync[id(rec.p)] = (rec.p._version, rec.p.data_ptr())
+        if (getattr(self, "place_trials", 0) and self.placement is None
+                and all("exp_avg" in self.state.get(rec.p, {}) for rec in self._records())):
+            # the first step that left every parameter with state: place the written
+            # streams once, against this step's gradients
+            self.placement = self.place_buffers(trials=self.place_trials)
         return loss
 
     def _step_increment(self, entries, device):

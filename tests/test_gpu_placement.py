@@ -178,3 +178,24 @@ def test_place_buffers_refusals(dev):
     set_grads(ps, 1, 1e-2)
     rep = opt.place_buffers(trials=4, reserve_bytes=1 << 50)
     assert rep["candidates"] == 1 and rep["chosen"] == 0 and rep["transient_bytes"] == 0
+
+
+@pytest.mark.parametrize("flat", [False, True])
+def test_place_trials_option_places_once_after_the_first_step(dev, flat):
+    """FusedAdamW(place_trials=K) runs place_buffers(K) once, after the first step (the
+    one that creates every parameter's state): results equal an optimizer without it."""
+    import mi_adamw
+    a = make_params(SHAPES, dev)
+    b = clone_params(a)
+    kw = dict(**HP, max_grad_norm=1.0, bf16_copy=True, state_dtype=torch.bfloat16,
+              flat_buffer=flat)
+    oa = mi_adamw.FusedAdamW(a, **kw, place_trials=2)
+    ob = mi_adamw.FusedAdamW(b, **kw)
+    assert oa.placement is None
+    _steps(a, b, oa, ob, 0, 1)
+    rep = oa.placement
+    assert rep is not None and rep["candidates"] == 3
+    assert rep["layout"] == ("flat" if flat else "tables")
+    _steps(a, b, oa, ob, 1, 3)
+    assert oa.placement is rep                     # once only
+    _assert_same(a, b, oa, ob)

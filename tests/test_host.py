@@ -102,6 +102,15 @@ def test_extra_options_are_validated():
         mi_adamw.FusedAdamW(_params(), state_dtype=torch.float16)
     with pytest.raises(ValueError):
         mi_adamw.FusedAdamW(_params(), chunk_elems=1000)
+    for bad in (-1, 1.5, "4"):
+        with pytest.raises(ValueError, match="place_trials"):
+            mi_adamw.FusedAdamW(_params(), place_trials=bad)
+    with pytest.raises(NotImplementedError, match="place_trials"):
+        mi_adamw.FusedAdamW(_params(), place_trials=2, capturable=True)
+    with pytest.raises(NotImplementedError, match="place_trials"):
+        mi_adamw.FusedAdamW(_params(), place_trials=2, amsgrad=True)
+    opt = mi_adamw.FusedAdamW(_params(), place_trials=4)
+    assert opt.place_trials == 4 and opt.placement is None
 
 
 def test_step_on_cpu_params_raises_before_touching_state():
