@@ -11,7 +11,9 @@ them: ``place_buffers`` allocates up to ``trials`` more sets of the streams the
 optimizer owns and writes, times the update's memory-only twin (``mi_adamw_probe``,
 ``mi_adamw_probe_flat``: the update's launch, loads and stores without the arithmetic)
 on every set, the current one included, against the current parameters and gradients,
-moves the values into the fastest set and frees the others.
+moves the values into the fastest set (if it beats the current one by at least
+``min_gain``, 1% by default: the twin ranks the update alone, and differences below that
+are within how closely it tracks the whole step) and frees the others.
 
 The placed streams:
 - per-tensor tables: exp_avg, exp_avg_sq and the bf16 copy, each as one block over
@@ -234,11 +236,13 @@ def _timed(run, launches: int) -> list[float]:
 
 @torch.no_grad()
 def place_buffers(opt, trials: int = 8, launches: int = 3, rounds: int = 2,
-                  reserve_bytes: int | None = None) -> dict:
+                  reserve_bytes: int | None = None, min_gain: float = 0.01) -> dict:
     """Choose where the optimizer's written streams live by timing the update's
     memory-only twin on the current set and on up to `trials` newly allocated sets
     (`rounds` interleaved rounds of `launches` timed launches each); move the values
-    into the fastest set and free the rest.  Returns what was tried and chosen."""
+    into the fastest set if its twin beats the current set's by at least `min_gain`
+    (below that, the difference is within how closely the twin's ranking tracks the
+    whole step), and free the rest.  Returns what was tried and chosen."""
     if opt.capturable:
         raise NotImplementedError("place_buffers: capturable=True is not supported")
     if any(g["amsgrad"] for g in opt.param_groups):
@@ -270,7 +274,8 @@ def place_buffers(opt, trials: int = 8, launches: int = 3, rounds: int = 2,
             for i in order:
                 times[i] += streams.twin(cands[i], launches)
         twin_ms = [statistics.mean(t) for t in times]
-        best = min(range(len(cands)), key=lambda i: twin_ms[i])
+        fastest = min(range(len(cands)), key=lambda i: twin_ms[i])
+        best = fastest if twin_ms[0] / twin_ms[fastest] - 1.0 >= min_gain else 0
         if best != 0:
             streams.adopt(cands[best])
             opt._launch_cache = None
@@ -281,6 +286,7 @@ def place_buffers(opt, trials: int = 8, launches: int = 3, rounds: int = 2,
         "layout": "flat" if opt._flat is not None else "tables",
         "streams": list(streams.names), "set_bytes": int(streams.set_bytes),
         "candidates": len(twin_ms), "twin_ms": [round(x, 5) for x in twin_ms],
+        "fastest": fastest, "min_gain": min_gain,
         "chosen": best, "twin_gain": round(twin_ms[0] / twin_ms[best] - 1.0, 5),
         "transient_bytes": int(streams.set_bytes) * (len(twin_ms) - 1),
         "seconds": round(time.perf_counter() - t0, 3),

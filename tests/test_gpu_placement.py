@@ -112,7 +112,13 @@ def test_place_buffers_report_and_parity(dev, flat):
     print(f"place_buffers ({'flat' if flat else 'tables'}): {rep}", flush=True)
     assert rep["layout"] == ("flat" if flat else "tables")
     assert rep["candidates"] == 4 and len(rep["twin_ms"]) == 4
-    assert 0 <= rep["chosen"] < 4 and rep["twin_ms"][rep["chosen"]] == min(rep["twin_ms"])
+    tw = rep["twin_ms"]
+    assert tw[rep["fastest"]] == min(tw) and rep["min_gain"] == 0.01
+    # the fastest set is taken only if it beats the current one by min_gain
+    if tw[0] / tw[rep["fastest"]] - 1 >= 0.01:
+        assert rep["chosen"] == rep["fastest"]
+    else:
+        assert rep["chosen"] == 0 and rep["twin_gain"] == 0
     names = ["param", "exp_avg", "exp_avg_sq", "copy"] if flat else ["exp_avg", "exp_avg_sq",
                                                                      "copy"]
     assert rep["streams"] == names
@@ -178,6 +184,9 @@ def test_place_buffers_refusals(dev):
     set_grads(ps, 1, 1e-2)
     rep = opt.place_buffers(trials=4, reserve_bytes=1 << 50)
     assert rep["candidates"] == 1 and rep["chosen"] == 0 and rep["transient_bytes"] == 0
+    # min_gain 0 takes the fastest of the candidates, whatever the margin
+    rep = opt.place_buffers(trials=2, min_gain=0.0)
+    assert rep["chosen"] == rep["fastest"]
 
 
 @pytest.mark.parametrize("flat", [False, True])
