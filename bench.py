@@ -14,7 +14,10 @@ in the flat-buffer layout, fp32 params/grads/moments, global grad-norm clip at
 mid-training (step 1000), lr 3e-4, betas (0.9, 0.95), eps 1e-8, weight decay 0.1.
 The other configurations of the workload list (125M, 350M, 1.3B with bf16
 moments, in the layouts the optimizer offers) are timed in the same run as rows
-of ``sweep``, each with its own ``roofline``.
+of ``sweep``, each with its own ``roofline``.  Before its timed steps each set
+takes one step and ``FusedAdamW.place_buffers(16)`` (``--placement-trials``): the
+streams the update writes move to the fastest of up to 16 more allocations, by
+the update's memory-only twin; each row's ``placement`` holds that report.
 
 Output: one JSON line.  ``value`` is the achieved HBM bandwidth of the whole
 step in GB/s, from algorithmic bytes (every byte the step must read or write,
@@ -648,7 +651,7 @@ def main() -> int:
                     help="FusedAdamW(clip_write_grads=True): the update also stores the clipped "
                          "gradients back, as torch's clip_grad_norm_ does (+4 B per parameter; "
                          "clip configurations only)")
-    ap.add_argument("--placement-trials", type=int, default=8,
+    ap.add_argument("--placement-trials", type=int, default=16,
                     help="before each configuration's timed steps, FusedAdamW.place_buffers "
                          "with this many candidate placements of the streams the update writes "
                          "(0: keep the first allocation)")

@@ -612,7 +612,7 @@ class FusedAdamW(Optimizer):
                 self._init_vmax(p, st)
             st["max_exp_avg_sq"].copy_(max_exp_avg_sq)
 
-    def place_buffers(self, trials: int = 8, launches: int = 3, rounds: int = 2,
+    def place_buffers(self, trials: int = 16, launches: int = 3, rounds: int = 2,
                       reserve_bytes: int | None = None, min_gain: float = 0.01) -> dict:
         """Move the streams the update writes to the fastest of up to `trials` newly
         allocated places, chosen by timing the update's memory-only twin on each against

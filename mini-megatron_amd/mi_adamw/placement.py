@@ -235,7 +235,7 @@ def _timed(run, launches: int) -> list[float]:
 
 
 @torch.no_grad()
-def place_buffers(opt, trials: int = 8, launches: int = 3, rounds: int = 2,
+def place_buffers(opt, trials: int = 16, launches: int = 3, rounds: int = 2,
                   reserve_bytes: int | None = None, min_gain: float = 0.01) -> dict:
     """Choose where the optimizer's written streams live by timing the update's
     memory-only twin on the current set and on up to `trials` newly allocated sets
