@@ -13,7 +13,12 @@ optimizer owns and writes, times the update's memory-only twin (``mi_adamw_probe
 on every set, the current one included, against the current parameters and gradients,
 moves the values into the fastest set (if it beats the current one by at least
 ``min_gain``, 1% by default: the twin ranks the update alone, and differences below that
-are within how closely it tracks the whole step) and frees the others.
+are within how closely it tracks the whole step) and frees the others.  Then, one stream
+at a time, it tries new allocations of that stream alone with the others kept, and moves
+the stream the same way: the speed is a property of how the streams' pages combine, and
+replacing a single stream of a slow set can make it fast, so this stage reaches further
+for the same memory (one stream per candidate rather than a set; at 6.7B only one whole
+set fits beside the optimizer's own, but four or five of each stream).
 
 The placed streams:
 - per-tensor tables: exp_avg, exp_avg_sq and the bf16 copy, each as one block over
@@ -80,7 +85,10 @@ class _Streams:
     def current(self):
         raise NotImplementedError
 
-    def allocate(self):
+    def allocate(self, names=None):
+        raise NotImplementedError
+
+    def stream_bytes(self, name: str) -> int:
         raise NotImplementedError
 
     def twin(self, cand, launches: int):
@@ -117,11 +125,15 @@ class _TableStreams(_Streams):
     def current(self):
         return {n: [self._tensor(p, st, n) for p, st in self.entries] for n in self.names}
 
-    def allocate(self):
+    def allocate(self, names=None):
+        names = self.names if names is None else names
         blocks = {n: torch.empty(self.total, dtype=self.dtypes[n], device=self.device)
-                  for n in self.names}
+                  for n in names}
         return {n: [blocks[n][o:o + p.numel()].view(p.shape)
-                    for o, (p, _) in zip(self.offs, self.entries)] for n in self.names}
+                    for o, (p, _) in zip(self.offs, self.entries)] for n in names}
+
+    def stream_bytes(self, name):
+        return self.total * torch.empty((), dtype=self.dtypes[name]).element_size()
 
     def _launch(self, cand):
         opt = self.opt
@@ -187,8 +199,13 @@ class _FlatStreams(_Streams):
     def current(self):
         return {n: getattr(self.flat, n) for n in self.names}
 
-    def allocate(self):
-        return {n: torch.empty_like(getattr(self.flat, n)) for n in self.names}
+    def allocate(self, names=None):
+        names = self.names if names is None else names
+        return {n: torch.empty_like(getattr(self.flat, n)) for n in names}
+
+    def stream_bytes(self, name):
+        t = getattr(self.flat, name)
+        return t.numel() * t.element_size()
 
     def twin(self, cand, launches):
         opt, fl, lib = self.opt, self.flat, _lib.load()
@@ -234,15 +251,43 @@ def _timed(run, launches: int) -> list[float]:
     return [e0.elapsed_time(e1) for e0, e1 in evs]
 
 
+def _choose(streams, cands, launches: int, rounds: int, min_gain: float):
+    """Twin ms of every candidate (index 0: the current streams), timed in `rounds`
+    interleaved rounds; the fastest; the one to take (the fastest if it beats the current
+    one by at least `min_gain`, else 0)."""
+    times = [[] for _ in cands]
+    for r in range(max(1, rounds)):
+        order = range(len(cands)) if r % 2 == 0 else reversed(range(len(cands)))
+        for i in order:
+            times[i] += streams.twin(cands[i], launches)
+    twin_ms = [statistics.mean(t) for t in times]
+    fastest = min(range(len(cands)), key=lambda i: twin_ms[i])
+    best = fastest if twin_ms[0] / twin_ms[fastest] - 1.0 >= min_gain else 0
+    return twin_ms, fastest, best
+
+
+def _allocate_up_to(streams, k: int, names=None) -> list:
+    out = []
+    for _ in range(k):
+        try:
+            out.append(streams.allocate(names))
+        except torch.cuda.OutOfMemoryError:
+            break
+    return out
+
+
 @torch.no_grad()
 def place_buffers(opt, trials: int = 16, launches: int = 3, rounds: int = 2,
-                  reserve_bytes: int | None = None, min_gain: float = 0.01) -> dict:
+                  reserve_bytes: int | None = None, min_gain: float = 0.01,
+                  per_stream: bool = True) -> dict:
     """Choose where the optimizer's written streams live by timing the update's
     memory-only twin on the current set and on up to `trials` newly allocated sets
     (`rounds` interleaved rounds of `launches` timed launches each); move the values
     into the fastest set if its twin beats the current set's by at least `min_gain`
     (below that, the difference is within how closely the twin's ranking tracks the
-    whole step), and free the rest.  Returns what was tried and chosen."""
+    whole step), and free the rest.  With `per_stream`, then do the same for each
+    stream alone (up to `trials` new allocations of it, the other streams kept).
+    Returns what was tried and chosen."""
     if opt.capturable:
         raise NotImplementedError("place_buffers: capturable=True is not supported")
     if any(g["amsgrad"] for g in opt.param_groups):
@@ -261,27 +306,38 @@ def place_buffers(opt, trials: int = 16, launches: int = 3, rounds: int = 2,
                    else _TableStreams(opt, device))
         avail, total = _free_bytes(device)
         reserve = max(2 << 30, total // 50) if reserve_bytes is None else int(reserve_bytes)
+        # stage 1: whole sets
         k = candidates_that_fit(streams.set_bytes, trials, avail, reserve)
-        cands = [streams.current()]
-        for _ in range(k):
-            try:
-                cands.append(streams.allocate())
-            except torch.cuda.OutOfMemoryError:
-                break
-        times = [[] for _ in cands]
-        for r in range(max(1, rounds)):
-            order = range(len(cands)) if r % 2 == 0 else reversed(range(len(cands)))
-            for i in order:
-                times[i] += streams.twin(cands[i], launches)
-        twin_ms = [statistics.mean(t) for t in times]
-        fastest = min(range(len(cands)), key=lambda i: twin_ms[i])
-        best = fastest if twin_ms[0] / twin_ms[fastest] - 1.0 >= min_gain else 0
+        cands = [streams.current()] + _allocate_up_to(streams, k)
+        twin_ms, fastest, best = _choose(streams, cands, launches, rounds, min_gain)
         if best != 0:
             streams.adopt(cands[best])
-            opt._launch_cache = None
-            opt._fast = None
-        torch.cuda.synchronize(device)
+        peak = streams.set_bytes * (len(cands) - 1)
         del cands
+        first_ms = twin_ms[0]
+        last_ms = twin_ms[best]
+        # stage 2: one stream at a time
+        stages = []
+        for name in (streams.names if per_stream else []):
+            avail, _ = _free_bytes(device)
+            k = candidates_that_fit(streams.stream_bytes(name), trials, avail, reserve)
+            if k == 0:
+                continue
+            cur = streams.current()
+            alts = _allocate_up_to(streams, k, [name])
+            cands = [cur] + [{**cur, name: a[name]} for a in alts]
+            ms, f, b = _choose(streams, cands, launches, rounds, min_gain)
+            if b != 0:
+                streams.adopt(cands[b])
+                last_ms = ms[b]
+            peak = max(peak, streams.stream_bytes(name) * len(alts))
+            stages.append({"stream": name, "candidates": len(ms),
+                           "twin_ms": [round(x, 5) for x in ms], "fastest": f, "chosen": b,
+                           "twin_gain": round(ms[0] / ms[b] - 1.0, 5)})
+            del cands, alts, cur
+        opt._launch_cache = None
+        opt._fast = None
+        torch.cuda.synchronize(device)
     return {
         "layout": "flat" if opt._flat is not None else "tables",
         "streams": list(streams.names), "set_bytes": int(streams.set_bytes),
@@ -289,5 +345,8 @@ def place_buffers(opt, trials: int = 16, launches: int = 3, rounds: int = 2,
         "fastest": fastest, "min_gain": min_gain,
         "chosen": best, "twin_gain": round(twin_ms[0] / twin_ms[best] - 1.0, 5),
         "transient_bytes": int(streams.set_bytes) * (len(twin_ms) - 1),
+        "per_stream": stages,
+        "total_twin_gain": round(first_ms / last_ms - 1.0, 5),
+        "peak_transient_bytes": int(peak),
         "seconds": round(time.perf_counter() - t0, 3),
     }

@@ -123,6 +123,14 @@ def test_place_buffers_report_and_parity(dev, flat):
                                                                      "copy"]
     assert rep["streams"] == names
     assert rep["transient_bytes"] == 3 * rep["set_bytes"]
+    # then each stream alone: 3 new allocations of it beside the current one, the same rule
+    assert [st["stream"] for st in rep["per_stream"]] == names
+    for st in rep["per_stream"]:
+        t = st["twin_ms"]
+        assert st["candidates"] == 4 and t[st["fastest"]] == min(t)
+        assert st["chosen"] in (0, st["fastest"])
+        assert (st["chosen"] != 0) == (t[0] / t[st["fastest"]] - 1 >= 0.01)
+    assert rep["peak_transient_bytes"] >= rep["transient_bytes"]
     _assert_same(a, b, oa, ob)
     _steps(a, b, oa, ob, 1, 3)
     _assert_same(a, b, oa, ob)
