@@ -302,6 +302,9 @@ def place_buffers(opt, trials: int = 16, launches: int = 3, rounds: int = 2,
         raise NotImplementedError("place_buffers: complex parameters are not supported")
     t0 = time.perf_counter()
     with torch.cuda.device(device):
+        # the twin stores back the values it reads, the current streams' included: work
+        # still queued on any stream (a step on another stream) must finish first
+        torch.cuda.synchronize(device)
         streams = (_FlatStreams(opt, device) if opt._flat is not None
                    else _TableStreams(opt, device))
         avail, total = _free_bytes(device)
