@@ -281,9 +281,10 @@ class FusedAdamW(Optimizer):
                       clip_write_grads the stored gradient is the pre-scaled,
                       clipped one).
     place_trials:     if > 0, run ``place_buffers(place_trials)`` once, after
-                      the first step that leaves every parameter with state:
-                      the streams the update writes move to the fastest of up
-                      to this many more allocations (report in ``placement``).
+                      the first step: the streams the update writes move to the
+                      fastest of up to this many more allocations (report in
+                      ``placement``).  State created later (a parameter without
+                      a gradient at that step) keeps its own allocation.
 
     Not supported (NotImplementedError at construction): differentiable, betas
     as tensors, param groups with different capturable settings, place_trials
@@ -855,10 +856,9 @@ class FusedAdamW(Optimizer):
             # the launch wrote these masters' copies
             for rec, _ in entries:
                 self._copy_sync[id(rec.p)] = (rec.p._version, rec.p.data_ptr())
-        if (getattr(self, "place_trials", 0) and self.placement is None
-                and all("exp_avg" in self.state.get(rec.p, {}) for rec in self._records())):
-            # the first step that left every parameter with state: place the written
-            # streams once, against this step's gradients
+        if getattr(self, "place_trials", 0) and self.placement is None:
+            # once, after the first step: place the written streams of every parameter
+            # with state, timed against this step's gradients
             self.placement = self.place_buffers(trials=self.place_trials)
         return loss
 

@@ -216,3 +216,40 @@ def test_place_trials_option_places_once_after_the_first_step(dev, flat):
     _steps(a, b, oa, ob, 1, 3)
     assert oa.placement is rep                     # once only
     _assert_same(a, b, oa, ob)
+
+
+def test_placement_with_groups_and_a_parameter_without_gradient(dev):
+    """Two param groups with their own hyperparameters; one parameter has no gradient at the
+    first step, so place_trials places the others and that one's state, created when its
+    gradient arrives, keeps its own allocation.  Every step equals an unplaced optimizer's."""
+    import mi_adamw
+    a = make_params(SHAPES, dev)
+    b = clone_params(a)
+
+    def groups(ps):
+        return [{"params": ps[:5]}, {"params": ps[5:], "lr": 1e-3, "weight_decay": 0.0,
+                                     "betas": (0.8, 0.99)}]
+    kw = dict(**HP, max_grad_norm=1.0, bf16_copy=True, state_dtype=torch.bfloat16)
+    oa = mi_adamw.FusedAdamW(groups(a), **kw, place_trials=3)
+    ob = mi_adamw.FusedAdamW(groups(b), **kw)
+    late = 3
+    for k in range(4):
+        set_grads(a, k, 3e-2)
+        if k == 0:
+            a[late].grad = None
+        for p, q in zip(a, b):
+            q.grad = None if p.grad is None else p.grad.clone()
+        oa.step()
+        ob.step()
+        if k == 0:
+            rep = oa.placement
+            assert rep is not None and rep["candidates"] == 4
+            assert "exp_avg" not in oa.state[a[late]]
+    torch.cuda.synchronize()
+    assert oa.placement is rep
+    for p, q in zip(a, b):
+        assert torch.equal(_bits(p), _bits(q))
+        for key in ("exp_avg", "exp_avg_sq"):
+            assert torch.equal(_bits(oa.state[p][key]), _bits(ob.state[q][key])), key
+        assert torch.equal(_bits(oa.bf16_param(p)), _bits(ob.bf16_param(q)))
+    assert float(oa.state[a[late]]["step"]) == 3.0 and float(oa.state[a[0]]["step"]) == 4.0
