@@ -3,7 +3,7 @@
 Builds the library (its host code: argument checks, the chunk-table builder, the
 gradient patch's host loop, the no-alloc scratch lookup), the native host extension
 (csrc/host.cpp: refcounting, the plan, prepare()'s checks and row patching), the oracle
-and the plain-C ABI checker with -fsanitize=address,undefined into _build/asan
+and the plain-C ABI test program with -fsanitize=address,undefined into _build/asan
 (``python -m mi_adamw.build --sanitize``, ``make asan`` in oracle/ and tests/c/), then
 runs, with clang's shared ASan runtime preloaded and leak detection off:
 - ``abi_check cpu`` (version, error text, chunk tables, every argument rejection);
