@@ -519,7 +519,7 @@ def run_config(name: str, steps: int, warmup: int, device, with_context: bool,
     params, opt, n, n_tensors = build_set(name, device, capturable, write_grads)
     total_b, upd_b = bytes_per_param(clip, state, copy, write_grads)
     placement = None
-    if trials > 0 and not capturable:
+    if trials > 0:
         # where the streams the update writes live: the fastest of `trials` more
         # allocations by the update's memory-only twin (FusedAdamW.place_buffers)
         from mi_adamw import placement as pl

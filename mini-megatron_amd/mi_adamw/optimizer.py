@@ -288,7 +288,7 @@ class FusedAdamW(Optimizer):
 
     Not supported (NotImplementedError at construction): differentiable, betas
     as tensors, param groups with different capturable settings, place_trials
-    with capturable or amsgrad.
+    with amsgrad.
     """
 
     def __init__(
@@ -364,9 +364,9 @@ class FusedAdamW(Optimizer):
                                       "supported")
         if not isinstance(place_trials, int) or place_trials < 0:
             raise ValueError(f"Invalid place_trials: {place_trials}")
-        if place_trials and (capturable or amsgrad):
-            raise NotImplementedError("FusedAdamW: place_trials with capturable=True or "
-                                      "amsgrad=True is not supported")
+        if place_trials and amsgrad:
+            raise NotImplementedError("FusedAdamW: place_trials with amsgrad=True is not "
+                                      "supported")
 
         self.capturable = bool(capturable)
         self.max_grad_norm = None if max_grad_norm is None else float(max_grad_norm)
@@ -416,6 +416,9 @@ class FusedAdamW(Optimizer):
         self.timing_events = None
         # place_trials: place_buffers' report once it has run (None until then)
         self.placement: dict | None = None
+        # a step was recorded into a graph: the graph keeps the addresses of the
+        # tables and buffers it recorded, so they must not move any more
+        self.captured = False
 
     # ------------------------------------------------------------------ torch API
 
@@ -627,7 +630,8 @@ class FusedAdamW(Optimizer):
         keeping `reserve_bytes` (default max(2 GiB, 2% of HBM)) free.  Returns a report
         of the candidates' twin times and the choice.  No counterpart in torch: the
         MI355X's bandwidth for the update's mix depends on the physical pages of its
-        written streams (10-13% between placements)."""
+        written streams (10-13% between placements).  With capturable=True, call it before
+        capturing: it raises once a step has been recorded into a graph."""
         from .placement import place_buffers
         return place_buffers(self, trials=trials, launches=launches, rounds=rounds,
                              reserve_bytes=reserve_bytes, min_gain=min_gain,
@@ -761,6 +765,9 @@ class FusedAdamW(Optimizer):
         native host path (``_host``) while nothing but the gradient addresses changes;
         anything else takes the general path below, which rebuilds what changed."""
         self._cuda_graph_capture_health_check()
+        if (self.capturable and torch.cuda.is_available()
+                and torch.cuda.is_current_stream_capturing()):
+            self.captured = True
         fast = self._fast
         if closure is None and fast is not None and self._fast_step(fast):
             return None

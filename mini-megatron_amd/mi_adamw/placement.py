@@ -288,8 +288,12 @@ def place_buffers(opt, trials: int = 16, launches: int = 3, rounds: int = 2,
     whole step), and free the rest.  With `per_stream`, then do the same for each
     stream alone (up to `trials` new allocations of it, the other streams kept).
     Returns what was tried and chosen."""
-    if opt.capturable:
-        raise NotImplementedError("place_buffers: capturable=True is not supported")
+    if getattr(opt, "captured", False):
+        raise RuntimeError("place_buffers: a step of this optimizer was recorded into a graph, "
+                           "which keeps the addresses of the buffers it recorded; place the "
+                           "buffers before capturing")
+    if torch.cuda.is_available() and torch.cuda.is_current_stream_capturing():
+        raise RuntimeError("place_buffers cannot run under graph capture")
     if any(g["amsgrad"] for g in opt.param_groups):
         raise NotImplementedError("place_buffers: amsgrad state is not placed")
     params = [p for g in opt.param_groups for p in g["params"]]

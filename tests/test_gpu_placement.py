@@ -179,8 +179,6 @@ def test_place_buffers_refusals(dev):
         mi_adamw.FusedAdamW(ps, **HP).place_buffers(trials=1)
     with pytest.raises(NotImplementedError, match="amsgrad"):
         mi_adamw.FusedAdamW(ps, **HP, amsgrad=True).place_buffers(trials=1)
-    with pytest.raises(NotImplementedError, match="capturable"):
-        mi_adamw.FusedAdamW(ps, **HP, capturable=True).place_buffers(trials=1)
     opt = mi_adamw.FusedAdamW(ps, **HP)
     set_grads(ps, 0, 1e-2)
     opt.step()
@@ -253,3 +251,48 @@ def test_placement_with_groups_and_a_parameter_without_gradient(dev):
             assert torch.equal(_bits(oa.state[p][key]), _bits(ob.state[q][key])), key
         assert torch.equal(_bits(oa.bf16_param(p)), _bits(ob.bf16_param(q)))
     assert float(oa.state[a[late]]["step"]) == 3.0 and float(oa.state[a[0]]["step"]) == 4.0
+
+
+def test_capturable_placed_before_capture_replays_bit_identically(dev):
+    """capturable=True with place_trials: the first (eager) step places the streams; a step
+    recorded into a HIP graph afterwards, replayed with new gradients in the same tensors,
+    is bit-identical to an unplaced capturable optimizer's eager steps.  place_buffers after
+    the capture raises: the graph keeps the addresses it recorded."""
+    import mi_adamw
+    a = make_params(SHAPES, dev)
+    b = clone_params(a)
+    kw = dict(**HP, max_grad_norm=1.0, bf16_copy=True, capturable=True)
+    oa = mi_adamw.FusedAdamW(a, **kw, place_trials=2)
+    ob = mi_adamw.FusedAdamW(b, **kw)
+    for p in a + b:
+        p.grad = torch.zeros_like(p)
+
+    def fill(k):
+        set_grads(a, k, 3e-2)
+        for p, q in zip(a, b):
+            q.grad.copy_(p.grad)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for k in range(3):
+            fill(k)
+            oa.step()
+            ob.step()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    assert oa.placement is not None and oa.placement["candidates"] == 3
+    _assert_same(a, b, oa, ob)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        oa.step()
+    assert oa.captured
+    for k in range(3, 7):
+        fill(k)
+        graph.replay()
+        ob.step()
+        torch.cuda.synchronize()
+        _assert_same(a, b, oa, ob)
+        torch.randn(1 << 20, device=dev).sum().item()     # other eager work between replays
+    assert float(oa.state[a[0]]["step"]) == 7.0
+    with pytest.raises(RuntimeError, match="recorded into a graph"):
+        oa.place_buffers(trials=1)

@@ -106,9 +106,9 @@ def test_extra_options_are_validated():
         with pytest.raises(ValueError, match="place_trials"):
             mi_adamw.FusedAdamW(_params(), place_trials=bad)
     with pytest.raises(NotImplementedError, match="place_trials"):
-        mi_adamw.FusedAdamW(_params(), place_trials=2, capturable=True)
-    with pytest.raises(NotImplementedError, match="place_trials"):
         mi_adamw.FusedAdamW(_params(), place_trials=2, amsgrad=True)
+    capt = mi_adamw.FusedAdamW(_params(), place_trials=2, capturable=True)
+    assert capt.place_trials == 2 and capt.captured is False
     opt = mi_adamw.FusedAdamW(_params(), place_trials=4)
     assert opt.place_trials == 4 and opt.placement is None
 
