@@ -569,7 +569,8 @@ class FusedAdamW(Optimizer):
             c.copy_(p.detach())
         else:
             c = self._copies.get(id(p))
-            if c is None or c.shape != p.shape or c.device != p.device:
+            if (c is None or c.shape != p.shape or c.device != p.device
+                    or not c.is_contiguous()):
                 c = self._copies[id(p)] = self._new_copy(p)
                 self._launch_cache = None
             else:

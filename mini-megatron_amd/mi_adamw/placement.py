@@ -141,8 +141,12 @@ class _TableStreams(_Streams):
         sa = 8 if opt.state_dtype == torch.bfloat16 else 16
         for i, (p, _) in enumerate(self.entries):
             g = p.grad
-            if (p.numel() == 0 or g is None or g.numel() != p.numel()
-                    or not g.is_contiguous()):
+            n = p.numel()
+            # the twin reads and writes n contiguous elements from each pointer: a row
+            # whose tensors are not dense and of p's size is left out (the step converts
+            # such state before it uses it)
+            ts = [p, g] + [cand[k][i] for k in self.names]
+            if n == 0 or any(t is None or t.numel() != n or not t.is_contiguous() for t in ts):
                 continue
             pp, gp = p.data_ptr(), g.data_ptr()
             mp, vp = cand["exp_avg"][i].data_ptr(), cand["exp_avg_sq"][i].data_ptr()

@@ -296,3 +296,33 @@ def test_capturable_placed_before_capture_replays_bit_identically(dev):
     assert float(oa.state[a[0]]["step"]) == 7.0
     with pytest.raises(RuntimeError, match="recorded into a graph"):
         oa.place_buffers(trials=1)
+
+
+def test_twin_leaves_out_rows_that_are_not_dense(dev):
+    """A state entry put into the dict as a strided view (not dense, more storage than its
+    elements) is left out of the twin's rows, so the twin never touches memory beyond the
+    tensors; the next step converts it and every step equals an unplaced optimizer's."""
+    import mi_adamw
+    a = make_params(SHAPES, dev)
+    b = clone_params(a)
+    oa = mi_adamw.FusedAdamW(a, **HP, max_grad_norm=1.0)
+    ob = mi_adamw.FusedAdamW(b, **HP, max_grad_norm=1.0)
+    _steps(a, b, oa, ob, 0, 1)
+    j = 7                                   # the (70001,) parameter
+    guard = torch.full((2 * a[j].numel(),), 7.0, device=dev)
+    strided = guard[::2]
+    strided.copy_(oa.state[a[j]]["exp_avg"])
+    oa.state[a[j]]["exp_avg"] = strided
+    from mi_adamw import placement
+    streams = placement._TableStreams(oa, dev)
+    launch = streams._launch(streams.current())
+    dense = sum(1 for p in a if p.numel())
+    assert launch.n_rows == dense - 1                # the strided entry's row is left out
+    assert int(launch.host_rows["numel"].sum()) == sum(p.numel() for p in a) - a[j].numel()
+    before = guard[1::2].clone()
+    rep = oa.place_buffers(trials=2)
+    assert rep["candidates"] == 3
+    torch.cuda.synchronize()
+    assert torch.equal(guard[1::2], before)          # the gaps were never written
+    _steps(a, b, oa, ob, 1, 2)
+    _assert_same(a, b, oa, ob)
