@@ -67,6 +67,16 @@ def candidates_that_fit(set_bytes: int, trials: int, free_bytes: int, reserve_by
     return int(max(0, min(trials, (free_bytes - reserve_bytes) // set_bytes)))
 
 
+def twin_row_ok(tensors, dtypes, n: int, device: torch.device) -> bool:
+    """Whether the twin may read and store back `n` contiguous elements at each tensor's
+    data_ptr(): every tensor present, strided, of `n` elements, of the dtype the kernel
+    reads it as, on `device`, and dense (a tensor that is not, or a smaller element type,
+    would put the accesses outside its memory; a host tensor is not device memory)."""
+    return n > 0 and all(
+        t is not None and t.layout == torch.strided and t.device == device and t.dtype == dt
+        and t.numel() == n and t.is_contiguous() for t, dt in zip(tensors, dtypes, strict=True))
+
+
 def _free_bytes(device: torch.device) -> tuple[int, int]:
     """(bytes an allocation can still get: the device's free memory plus what torch's
     caching allocator holds unused, the device's total)."""
@@ -139,14 +149,16 @@ class _TableStreams(_Streams):
         opt = self.opt
         rows = []
         sa = 8 if opt.state_dtype == torch.bfloat16 else 16
+        dtypes = [torch.float32, torch.float32] + [self.dtypes[k] for k in self.names]
+        cur = self.current()
         for i, (p, _) in enumerate(self.entries):
             g = p.grad
             n = p.numel()
-            # the twin reads and writes n contiguous elements from each pointer: a row
-            # whose tensors are not dense and of p's size is left out (the step converts
-            # such state before it uses it)
-            ts = [p, g] + [cand[k][i] for k in self.names]
-            if n == 0 or any(t is None or t.numel() != n or not t.is_contiguous() for t in ts):
+            # a row the twin cannot read as it stands is left out (the step converts such
+            # state before it uses it, or refuses the parameter), for every candidate
+            # alike, so that all of them are timed over the same rows
+            if not all(twin_row_ok([p, g] + [c[k][i] for k in self.names], dtypes, n,
+                                   self.device) for c in (cand, cur)):
                 continue
             pp, gp = p.data_ptr(), g.data_ptr()
             mp, vp = cand["exp_avg"][i].data_ptr(), cand["exp_avg_sq"][i].data_ptr()
@@ -181,7 +193,9 @@ class _TableStreams(_Streams):
             for n in self.names:
                 for i, (p, st) in enumerate(self.entries):
                     new, old = cand[n][i], cur[n][i]
-                    if new is old:
+                    if new is old or old.numel() != new.numel():
+                        # an entry of another size stays as it is: the step replaces a
+                        # copy of the wrong size and refuses such state
                         continue
                     new.copy_(old.reshape(new.shape))
                     if n == "copy":
@@ -306,6 +320,8 @@ def place_buffers(opt, trials: int = 16, launches: int = 3, rounds: int = 2,
     device = params[0].device
     if device.type != "cuda":
         raise RuntimeError("place_buffers needs parameters on a ROCm GPU")
+    if any(p.device != device for p in params):
+        raise NotImplementedError("place_buffers: all parameters must be on one device")
     if any(torch.is_complex(p) for p in params):
         raise NotImplementedError("place_buffers: complex parameters are not supported")
     t0 = time.perf_counter()

@@ -326,3 +326,31 @@ def test_twin_leaves_out_rows_that_are_not_dense(dev):
     assert torch.equal(guard[1::2], before)          # the gaps were never written
     _steps(a, b, oa, ob, 1, 2)
     _assert_same(a, b, oa, ob)
+
+
+def test_twin_leaves_out_host_and_narrower_state(dev):
+    """A state entry in host memory, and one of a narrower type than the state dtype, are
+    left out of the twin's rows for every candidate (the twin would read host memory, or
+    past the narrower tensor's end); the move converts them as the step would, and every
+    step equals that of an unplaced optimizer given the same entries."""
+    import mi_adamw
+    from mi_adamw import placement
+    a = make_params(SHAPES, dev)
+    b = clone_params(a)
+    oa = mi_adamw.FusedAdamW(a, **HP, max_grad_norm=1.0, bf16_copy=True)
+    ob = mi_adamw.FusedAdamW(b, **HP, max_grad_norm=1.0, bf16_copy=True)
+    _steps(a, b, oa, ob, 0, 1)
+    for o, ps in ((oa, a), (ob, b)):
+        o.state[ps[7]]["exp_avg"] = o.state[ps[7]]["exp_avg"].cpu()           # (70001,)
+        o.state[ps[3]]["exp_avg_sq"] = o.state[ps[3]]["exp_avg_sq"].bfloat16()  # (144, 48)
+    streams = placement._TableStreams(oa, dev)
+    for cand in (streams.current(), streams.allocate()):
+        launch = streams._launch(cand)
+        assert launch.n_rows == sum(1 for p in a if p.numel()) - 2
+        assert int(launch.host_rows["numel"].sum()) == (sum(p.numel() for p in a)
+                                                        - a[7].numel() - a[3].numel())
+    oa.place_buffers(trials=2, min_gain=0.0)
+    _steps(a, b, oa, ob, 1, 2)
+    _assert_same(a, b, oa, ob)
+    assert oa.state[a[7]]["exp_avg"].device == dev
+    assert oa.state[a[3]]["exp_avg_sq"].dtype == torch.float32
