@@ -154,7 +154,8 @@ class FlatLayout:
         return view
 
     def copy_view(self, p: torch.Tensor) -> torch.Tensor:
-        """p's slice of the bf16 copy buffer (made once: the buffer never moves)."""
+        """p's slice of the bf16 copy buffer (made once per buffer: adopt_buffers, which
+        replaces the buffer, drops the slices made of the old one)."""
         v = self._copy_views.get(id(p))
         if v is None:
             v = self._copy_views[id(p)] = self._view(self.copy, p)
