@@ -631,8 +631,12 @@ class FusedAdamW(Optimizer):
         keeping `reserve_bytes` (default max(2 GiB, 2% of HBM)) free.  Returns a report
         of the candidates' twin times and the choice.  No counterpart in torch: the
         MI355X's bandwidth for the update's mix depends on the physical pages of its
-        written streams (10-13% between placements).  With capturable=True, call it before
-        capturing: it raises once a step has been recorded into a graph."""
+        written streams (10-13% between placements).  A move replaces the state entries
+        and copies (and, flat, the parameters' ``.data``) with views of the new places, as
+        load_state_dict replaces state: tensors taken from ``state``, ``bf16_params()`` or
+        ``bf16_param()`` before the call keep the old values and are no longer updated;
+        take them again after it.  With capturable=True, call it before capturing: it
+        raises once a step has been recorded into a graph."""
         from .placement import place_buffers
         return place_buffers(self, trials=trials, launches=launches, rounds=rounds,
                              reserve_bytes=reserve_bytes, min_gain=min_gain,
