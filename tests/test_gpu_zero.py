@@ -389,3 +389,39 @@ def test_bench_range_shard_rows_step_as_the_flat_step(dev):
         assert torch.equal(getattr(oa._flat, key), getattr(ob._flat, key)), key
     assert all(float(oa.state[p]["step"]) == float(ob.state[q]["step"]) == 1003.0
                for p, q in zip(a, b))
+
+
+@pytest.mark.parametrize("state_dtype", [torch.float32, torch.bfloat16])
+def test_range_step_after_placement(dev, state_dtype):
+    """The range step over buffers that place_buffers (min_gain 0, so it moves whenever a
+    candidate is any faster) and a forced move of the parameter and copy buffers put
+    elsewhere between steps: it reads the buffers where they are now, stays bit-identical
+    to the unplaced flat step, and its native begin() resumes after each move."""
+    import mi_adamw
+    from mi_adamw import placement
+    a, b, oa, ob = _flat_pair(dev, SHAPES, state_dtype, 2, 1.0)
+    zs = mi_adamw.ZeroRangeStep(ob, 3)
+    moved = []
+    for step in range(6):
+        set_grads(a, step, 3e-2)
+        for p, q in zip(a, b):
+            q.grad.copy_(p.grad)
+        if step == 2:
+            rep = ob.place_buffers(trials=2, launches=1, rounds=1, min_gain=0.0)
+            moved.append((rep["chosen"], [s["chosen"] for s in rep["per_stream"]]))
+        if step == 4:
+            streams = placement._FlatStreams(ob, dev)
+            before = ob._flat.param.data_ptr()
+            streams.adopt(streams.allocate(["param", "copy"]))
+            assert ob._flat.param.data_ptr() != before
+            assert all(ob._flat.is_param_view(q) for q in b)
+        oa.step()
+        zs.step()
+    torch.cuda.synchronize()
+    for key in ("param", "exp_avg", "exp_avg_sq", "copy"):
+        assert torch.equal(getattr(oa._flat, key), getattr(ob._flat, key)), key
+    assert torch.equal(oa.last_grad_norm.view(torch.int32), ob.last_grad_norm.view(torch.int32))
+    for p, q in zip(a, b):
+        assert torch.equal(p, q)
+    # begin() natively at steps 1, 3 and 5; the Python body at 0 and after each move
+    assert zs.native_begins == 3, moved
