@@ -29,14 +29,19 @@ def dev():
     return torch.device("cuda", 0)
 
 
+@pytest.mark.parametrize("placed", [False, True])
 @pytest.mark.parametrize("flat", [False, True])
-def test_training_on_bf16_copies_is_bit_identical(dev, flat):
+def test_training_on_bf16_copies_is_bit_identical(dev, flat, placed):
+    """With `placed`, the bf16-weights model's optimizer places its streams after its first
+    step (place_trials), again before its third (min_gain 0, so it moves whenever a
+    candidate is any faster), and moves them before its fourth: the forward must read the
+    copies where they are now."""
     a = refgpt.tiny(dev, seed=11)
     b = refgpt.tiny(dev, seed=11)
     hp = dict(lr=1e-3, betas=(0.9, 0.95), weight_decay=0.1, bf16_copy=True, max_grad_norm=1.0,
               flat_buffer=flat)
     oa = mi_adamw.FusedAdamW(a.parameters(), **hp)
-    ob = mi_adamw.FusedAdamW(b.parameters(), **hp)
+    ob = mi_adamw.FusedAdamW(b.parameters(), **hp, place_trials=2 if placed else 0)
     for it in range(5):
         ids, labels, mask = refgpt.batch(dev, seed=100 + it)
         oa.zero_grad()
@@ -50,6 +55,19 @@ def test_training_on_bf16_copies_is_bit_identical(dev, flat):
         assert _bits_equal(la.detach(), lb.detach()), it
         for p, q in zip(a.parameters(), b.parameters()):
             assert _bits_equal(p.grad, q.grad), it
+        if placed and it == 2:
+            ob.place_buffers(trials=2, launches=1, rounds=1, min_gain=0.0)
+        if placed and it == 3:
+            # and a move forced through the layout's streams, whatever the timing says
+            from mi_adamw import placement
+            cls = placement._FlatStreams if flat else placement._TableStreams
+            streams = cls(ob, dev)
+            new = streams.allocate()
+            streams.adopt(new)
+            ob._launch_cache = None
+            ob._fast = None
+            assert ob.bf16_param(next(b.parameters())).data_ptr() == (
+                new["copy"].data_ptr() if flat else new["copy"][0].data_ptr())
         oa.step()
         ob.step()
         torch.cuda.synchronize()
@@ -57,6 +75,7 @@ def test_training_on_bf16_copies_is_bit_identical(dev, flat):
             assert _bits_equal(p.detach(), q.detach()), it
             assert _bits_equal(ob.bf16_param(q), q.detach().bfloat16()), it
         print(f"iteration {it}: loss {la.item():.6f} identical", flush=True)
+    assert (ob.placement is not None) == placed
 
 
 @pytest.mark.parametrize("flat", [False, True])
