@@ -512,7 +512,8 @@ def placement_ab(opt, orig: dict, streams, steps: int, warmup: int, rounds: int 
 
 def run_config(name: str, steps: int, warmup: int, device, with_context: bool,
                capturable: bool = False, write_grads: bool = False,
-               range_world: int = 0, trials: int = 0, ab: bool = False) -> dict:
+               range_world: int = 0, trials: int = 0, ab: bool = False,
+               passes: int = 1) -> dict:
     shape_name, clip, state, copy, flat, start_step, gstd = CONFIGS[name]
     log(f"[bench] {name}: building {shape_name} set" + (" (capturable)" if capturable else "")
         + (" (clipped grads written back)" if write_grads else ""))
@@ -535,6 +536,20 @@ def run_config(name: str, steps: int, warmup: int, device, with_context: bool,
             placement["ab"] = placement_ab(opt, orig, streams, steps, warmup)
             log(f"[bench] {name}: placement A/B {placement['ab']}")
         del orig, streams
+        if passes > 1:
+            # more passes of the same search, each from where the last one left the streams,
+            # with the step timed before and after each
+            later = []
+            for k in range(2, passes + 1):
+                before = time_fused(opt, steps, warmup)[0]
+                rep = opt.place_buffers(trials=trials)
+                after = time_fused(opt, steps, warmup)[0]
+                later.append({"pass": k, "chosen": rep["chosen"],
+                              "per_stream_chosen": [st["chosen"] for st in rep["per_stream"]],
+                              "total_twin_gain": rep["total_twin_gain"],
+                              "step_ms_before": round(before, 5), "step_ms_after": round(after, 5)})
+                log(f"[bench] {name}: placement pass {later[-1]}")
+            placement["later_passes"] = later
     log(f"[bench] {name}: {n} params in {n_tensors} tensors; timing {steps} steps")
     gpu_ms, wall_ms, norm_ms, upd_ms, step_ms = time_fused(opt, steps, warmup)
     # after the timed region: the update's memory-only twin on the same tensors
@@ -656,6 +671,9 @@ def main() -> int:
                     help="before each configuration's timed steps, FusedAdamW.place_buffers "
                          "with this many candidate placements of the streams the update writes "
                          "(0: keep the first allocation)")
+    ap.add_argument("--placement-passes", type=int, default=1,
+                    help="run place_buffers this many times before the timed steps, timing the "
+                         "step before and after every pass after the first")
     ap.add_argument("--placement-ab", action="store_true",
                     help="also time each configuration's step on its original streams against "
                          "the placed ones, alternating rounds in this process")
@@ -698,7 +716,8 @@ def main() -> int:
                               with_context=not args.no_context and nm == args.config,
                               capturable=args.capturable, write_grads=args.clip_write_grads,
                               range_world=args.range_world if nm == args.config else 0,
-                              trials=args.placement_trials, ab=args.placement_ab)
+                              trials=args.placement_trials, ab=args.placement_ab,
+                              passes=args.placement_passes)
                for nm in names}
     if args.calibrate_copy:
         src = torch.ones(1 << 28, device=device)

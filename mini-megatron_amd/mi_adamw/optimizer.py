@@ -619,14 +619,15 @@ class FusedAdamW(Optimizer):
 
     def place_buffers(self, trials: int = 16, launches: int = 3, rounds: int = 2,
                       reserve_bytes: int | None = None, min_gain: float = 0.01,
-                      per_stream: bool = True) -> dict:
+                      per_stream: bool = True, sweeps: int = 3) -> dict:
         """Move the streams the update writes to the fastest of up to `trials` newly
         allocated places, chosen by timing the update's memory-only twin on each against
         the current parameters and gradients (so call it after a backward, or with the
         gradients set).  Tables: exp_avg, exp_avg_sq and the bf16 copy become views of one
         block per stream; flat: the parameter, moment and copy buffers move, if the
         fastest twin beats the current set's by at least `min_gain`; with `per_stream`,
-        then each stream alone the same way, the others kept.  Values are
+        then each stream alone the same way, the others kept, in up to `sweeps` sweeps
+        over the streams (another sweep only after one that moved a stream).  Values are
         moved bit for bit.  Transient memory: one stream set per candidate, as many as fit
         keeping `reserve_bytes` (default max(2 GiB, 2% of HBM)) free.  Returns a report
         of the candidates' twin times and the choice.  No counterpart in torch: the
@@ -640,7 +641,7 @@ class FusedAdamW(Optimizer):
         from .placement import place_buffers
         return place_buffers(self, trials=trials, launches=launches, rounds=rounds,
                              reserve_bytes=reserve_bytes, min_gain=min_gain,
-                             per_stream=per_stream)
+                             per_stream=per_stream, sweeps=sweeps)
 
     def _amsgrad_of(self, p: torch.Tensor) -> bool:
         for g in self.param_groups:

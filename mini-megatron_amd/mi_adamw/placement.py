@@ -18,7 +18,9 @@ at a time, it tries new allocations of that stream alone with the others kept, a
 the stream the same way: the speed is a property of how the streams' pages combine, and
 replacing a single stream of a slow set can make it fast, so this stage reaches further
 for the same memory (one stream per candidate rather than a set; at 6.7B only one whole
-set fits beside the optimizer's own, but four or five of each stream).
+set fits beside the optimizer's own, but four or five of each stream).  A stream's best
+place depends on where the others are, so the streams are swept again after a sweep that
+moved one, up to ``sweeps`` sweeps.
 
 The placed streams:
 - per-tensor tables: exp_avg, exp_avg_sq and the bf16 copy, each as one block over
@@ -297,14 +299,16 @@ def _allocate_up_to(streams, k: int, names=None) -> list:
 @torch.no_grad()
 def place_buffers(opt, trials: int = 16, launches: int = 3, rounds: int = 2,
                   reserve_bytes: int | None = None, min_gain: float = 0.01,
-                  per_stream: bool = True) -> dict:
+                  per_stream: bool = True, sweeps: int = 3) -> dict:
     """Choose where the optimizer's written streams live by timing the update's
     memory-only twin on the current set and on up to `trials` newly allocated sets
     (`rounds` interleaved rounds of `launches` timed launches each); move the values
     into the fastest set if its twin beats the current set's by at least `min_gain`
     (below that, the difference is within how closely the twin's ranking tracks the
     whole step), and free the rest.  With `per_stream`, then do the same for each
-    stream alone (up to `trials` new allocations of it, the other streams kept).
+    stream alone (up to `trials` new allocations of it, the other streams kept), in
+    sweeps over the streams: a stream's best place depends on where the others are, so
+    a sweep that moved a stream is followed by another, up to `sweeps` sweeps.
     Returns what was tried and chosen."""
     if getattr(opt, "captured", False):
         raise RuntimeError("place_buffers: a step of this optimizer was recorded into a graph, "
@@ -343,25 +347,32 @@ def place_buffers(opt, trials: int = 16, launches: int = 3, rounds: int = 2,
         del cands
         first_ms = twin_ms[0]
         last_ms = twin_ms[best]
-        # stage 2: one stream at a time
+        # stage 2: one stream at a time, in sweeps while a sweep moves a stream
         stages = []
-        for name in (streams.names if per_stream else []):
-            avail, _ = _free_bytes(device)
-            k = candidates_that_fit(streams.stream_bytes(name), trials, avail, reserve)
-            if k == 0:
-                continue
-            cur = streams.current()
-            alts = _allocate_up_to(streams, k, [name])
-            cands = [cur] + [{**cur, name: a[name]} for a in alts]
-            ms, f, b = _choose(streams, cands, launches, rounds, min_gain)
-            if b != 0:
-                streams.adopt(cands[b])
+        n_sweeps = 0
+        while per_stream and n_sweeps < max(1, sweeps):
+            n_sweeps += 1
+            moved = False
+            for name in streams.names:
+                avail, _ = _free_bytes(device)
+                k = candidates_that_fit(streams.stream_bytes(name), trials, avail, reserve)
+                if k == 0:
+                    continue
+                cur = streams.current()
+                alts = _allocate_up_to(streams, k, [name])
+                cands = [cur] + [{**cur, name: a[name]} for a in alts]
+                ms, f, b = _choose(streams, cands, launches, rounds, min_gain)
+                if b != 0:
+                    streams.adopt(cands[b])
+                    moved = True
                 last_ms = ms[b]
-            peak = max(peak, streams.stream_bytes(name) * len(alts))
-            stages.append({"stream": name, "candidates": len(ms),
-                           "twin_ms": [round(x, 5) for x in ms], "fastest": f, "chosen": b,
-                           "twin_gain": round(ms[0] / ms[b] - 1.0, 5)})
-            del cands, alts, cur
+                peak = max(peak, streams.stream_bytes(name) * len(alts))
+                stages.append({"sweep": n_sweeps, "stream": name, "candidates": len(ms),
+                               "twin_ms": [round(x, 5) for x in ms], "fastest": f,
+                               "chosen": b, "twin_gain": round(ms[0] / ms[b] - 1.0, 5)})
+                del cands, alts, cur
+            if not moved:
+                break
         opt._launch_cache = None
         opt._fast = None
         torch.cuda.synchronize(device)
@@ -372,7 +383,7 @@ def place_buffers(opt, trials: int = 16, launches: int = 3, rounds: int = 2,
         "fastest": fastest, "min_gain": min_gain,
         "chosen": best, "twin_gain": round(twin_ms[0] / twin_ms[best] - 1.0, 5),
         "transient_bytes": int(streams.set_bytes) * (len(twin_ms) - 1),
-        "per_stream": stages,
+        "per_stream": stages, "sweeps": n_sweeps,
         "total_twin_gain": round(first_ms / last_ms - 1.0, 5),
         "peak_transient_bytes": int(peak),
         "seconds": round(time.perf_counter() - t0, 3),

@@ -123,8 +123,16 @@ def test_place_buffers_report_and_parity(dev, flat):
                                                                      "copy"]
     assert rep["streams"] == names
     assert rep["transient_bytes"] == 3 * rep["set_bytes"]
-    # then each stream alone: 3 new allocations of it beside the current one, the same rule
-    assert [st["stream"] for st in rep["per_stream"]] == names
+    # then each stream alone: 3 new allocations of it beside the current one, the same
+    # rule, in sweeps over the streams; another sweep follows only one that moved a stream
+    sweeps = rep["sweeps"]
+    assert 1 <= sweeps <= 3
+    by_sweep = [[st for st in rep["per_stream"] if st["sweep"] == k] for k in range(1, sweeps + 1)]
+    assert sum(map(len, by_sweep)) == len(rep["per_stream"])
+    for k, sw in enumerate(by_sweep, 1):
+        assert [st["stream"] for st in sw] == names
+        moved = any(st["chosen"] != 0 for st in sw)
+        assert moved == (k < sweeps) or (moved and k == sweeps == 3)
     for st in rep["per_stream"]:
         t = st["twin_ms"]
         assert st["candidates"] == 4 and t[st["fastest"]] == min(t)
