@@ -1098,9 +1098,11 @@ class FusedAdamW(Optimizer):
             raise RuntimeError(f"FusedAdamW: state[{key!r}] has {t.numel()} elements but its "
                                f"parameter has {p.numel()}")
         if t.dtype != want or t.device != p.device or not t.is_contiguous():
+            # .contiguous(), not to(memory_format=contiguous_format): to() returns the
+            # tensor itself when dtype and device already match and its suggested
+            # memory format is contiguous, which a 1-D or 2-D strided view reports
             with torch.no_grad():
-                t = st[key] = t.to(device=p.device, dtype=want,
-                                   memory_format=torch.contiguous_format)
+                t = st[key] = t.to(device=p.device, dtype=want).contiguous()
         return t
 
     def _tensor_rows(self, entries, hyper_idx, ams):

@@ -219,6 +219,48 @@ def test_native_path_falls_back_on_every_other_change(dev):
     assert native["native"] == 1
 
 
+@pytest.mark.parametrize("view", ["strided", "transposed"])
+def test_state_replaced_by_a_non_dense_view(dev, view):
+    """A moment put into the state dict as a view that is not dense (every other element
+    of a larger buffer, or a transposed matrix) after the native path has a plan: the
+    step falls back, replaces the entry by a dense copy with the same values and steps
+    it like torch (whose per-tensor ops take any strides); the next steps are native
+    again.  The buffer around the strided view is never written."""
+    import mi_adamw
+    ref = make_params(SHAPES, dev)
+    ours = clone_params(ref)
+    topt = torch.optim.AdamW(ref, foreach=False, **HP)
+    oopt = mi_adamw.FusedAdamW(ours, **HP)
+    spacer = []
+    for k in range(2):
+        _assign(ref, ours, _fresh_grads(ref, k), spacer)
+        oopt.step()
+        topt.step()
+    j = 7 if view == "strided" else 3          # (70001,) or (144, 48)
+    st = oopt.state[ours[j]]
+    if view == "strided":
+        guard = torch.full((2 * ours[j].numel(),), 7.0, device=dev)
+        t = guard[::2]
+        t.copy_(st["exp_avg"])
+        st["exp_avg"] = t
+    else:
+        v = st["exp_avg_sq"]
+        st["exp_avg_sq"] = v.t().contiguous().t()
+        assert not st["exp_avg_sq"].is_contiguous()
+    before = oopt.native_steps
+    for k in range(2, 5):
+        _assign(ref, ours, _fresh_grads(ref, k), spacer)
+        oopt.step()
+        topt.step()
+        torch.cuda.synchronize()
+        assert _same(ref, ours, topt, oopt) == 0, k
+    assert oopt.native_steps - before == 2
+    for key in ("exp_avg", "exp_avg_sq"):
+        assert st[key].is_contiguous()
+    if view == "strided":
+        assert torch.equal(guard[1::2], torch.full_like(guard[1::2], 7.0))
+
+
 def test_native_path_follows_the_lr_schedule(dev):
     """LambdaLR rewrites group["lr"] every iteration (main.py:178-180,210): the native path
     forms the scalars from the groups at every step."""

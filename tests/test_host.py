@@ -95,6 +95,30 @@ def test_capturable_group_constants():
         _capt_hyper(dict(g, lr=torch.tensor(6e-4, dtype=torch.float64)), torch.device("cpu"))
 
 
+@pytest.mark.parametrize("view", ["strided", "transposed", "wrong_dtype"])
+def test_state_entries_are_made_dense_for_the_kernel(view):
+    """A state entry put into the dict as a strided view, a transposed view or another
+    dtype is replaced by a dense copy of the state dtype with the same values before its
+    pointer goes into a table (the kernel reads numel contiguous elements from it)."""
+    p = torch.nn.Parameter(torch.randn(6, 5))
+    opt = mi_adamw.FusedAdamW([p])
+    vals = torch.randn(6, 5)
+    if view == "strided":
+        base = torch.full((60,), 7.0)
+        t = base[::2]
+        t.copy_(vals.reshape(-1))
+    elif view == "transposed":
+        t = vals.t().contiguous().t()
+    else:
+        t = vals.double()
+    st = {"exp_avg": t}
+    out = opt._state_tensor(p, st, "exp_avg")
+    assert out.is_contiguous() and out.dtype == torch.float32 and st["exp_avg"] is out
+    assert torch.equal(out.reshape(-1), vals.reshape(-1).float())
+    if view == "strided":
+        assert out.data_ptr() != base.data_ptr()
+
+
 def test_extra_options_are_validated():
     with pytest.raises(ValueError):
         mi_adamw.FusedAdamW(_params(), max_grad_norm=0.0)
