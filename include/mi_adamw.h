@@ -29,7 +29,9 @@
  * use (lerp, addcmul and addcdiv as fused multiply-adds; division by the host
  * scalar bc2_sqrt as a multiply by its reciprocal rounded to fp32).  The caller computes
  * the per-step scalars on the host in float64 (adam.py:529-536) and passes them
- * rounded to fp32 in mi_adamw_hyper.
+ * rounded to fp32 in mi_adamw_hyper.  The *_fused_chain entry points follow torch's
+ * fused=True chain instead (torch._fused_adamw_, see mi_adamw_fused_hyper); the
+ * capturable entry point follows torch's capturable chain.
  */
 #ifndef MI_ADAMW_H
 #define MI_ADAMW_H
@@ -40,7 +42,7 @@
 extern "C" {
 #endif
 
-#define MI_ADAMW_ABI_VERSION 7
+#define MI_ADAMW_ABI_VERSION 8
 #define MI_ADAMW_MAX_HYPER 16      /* hyperparameter sets per launch */
 #define MI_ADAMW_MAX_NORM_BLOCKS 4096 /* partial sums per grad-norm launch */
 
@@ -131,6 +133,34 @@ typedef struct mi_adamw_capt_hyper {
     int32_t lr_mode;       /* MI_ADAMW_LR_*                                                  */
     const float *lr_ptr;   /* LR_DEVICE: device fp32 learning rate                           */
 } mi_adamw_capt_hyper;
+
+/* One parameter group of a step in torch's fused=True chain.  The reference builds
+ * its optimizer as torch.optim.AdamW(..., fused=args.fused) (main.py:80,144,177); with
+ * --fused that runs adam.py:803-895 (_fused_adam): the step counts += 1 on the device,
+ * then torch._fused_adamw_, whose per-element math is adam_math in
+ * ATen/native/hip/fused_adam_utils.cuh (ADAMW mode).  The hyperparameters stay float64
+ * there, and each workgroup forms the per-step values from the fp32 step count:
+ *   bc1 = f32(1 - pow(beta1, step)), bc2_sqrt = f32(sqrt(1 - pow(beta2, step))),
+ *   step_size = f32(lr / (double)bc1)          (pow, sqrt, division in float64)
+ * Each element, from fp32 p, g, m, v (g after the clip scale and the maximize sign):
+ *   p = f32(fma(-(lr*wd), p, p))      when weight_decay != 0   (float64)
+ *   m = f32(fma(beta1, m, (1-beta1)*g))                        (float64)
+ *   v = f32(fma(beta2, v, ((1-beta2)*g)*g))                    (float64)
+ *   d = f32((double)(sqrtf(v) / bc2_sqrt) + eps)   (amsgrad: from fmaxf(vmax, v))
+ *   p = p - (step_size * m) / d                                (fp32)
+ * the fused multiply-adds where torch-ROCm's build of that kernel has them. */
+typedef struct mi_adamw_fused_hyper {
+    double lr;             /* the learning rate (a host tensor lr: its value)            */
+    double beta1;
+    double beta2;
+    double weight_decay;
+    double eps;
+    float step;            /* the step count after this step's increment; unused when the
+                              launch reads device step counts (d_steps)                   */
+    float grad_sign;       /* -1 with maximize=True, else 1                               */
+    const float *lr_ptr;   /* non-NULL: a device fp32 learning rate (a device tensor lr),
+                              read by the kernel in place of lr                           */
+} mi_adamw_fused_hyper;
 
 /* Library identification: "mi_adamw <abi> gfx950 ...". */
 const char *mi_adamw_version(void);
@@ -294,6 +324,31 @@ int mi_adamw_step_capturable(const mi_adamw_tensor *d_tensors, const mi_adamw_ch
                              const float *d_steps, const int32_t *d_step_index,
                              const float *d_grad_scale, int32_t state_dtype, int32_t flags,
                              int32_t max_blocks, void *stream);
+
+/* The fused AdamW update in torch's fused=True chain (mi_adamw_fused_hyper) over
+ * every chunk of the tables, or over one contiguous range (_flat).  Replaces
+ * torch._fused_adamw_ (adam.py:878-895) for torch.optim.AdamW(fused=True), which the
+ * reference builds with --fused (main.py:144,177).  hypers: host array of n_hyper
+ * (<= MI_ADAMW_MAX_HYPER) sets, indexed by mi_adamw_tensor.hyper.  d_steps and
+ * d_step_index: both NULL (each set's step count is hypers[i].step), or, as in
+ * mi_adamw_step_capturable, device fp32 step counts already incremented for this step
+ * and one int32 index into them per row of the tensor table (the launch may then be
+ * recorded into a HIP graph).  grad_prescale, d_grad_scale, state_dtype, flags and
+ * max_blocks are those of mi_adamw_step_prescaled; amsgrad's running maximum is
+ * fmaxf(max_exp_avg_sq, exp_avg_sq), as ::max in that kernel.  In the flat variant
+ * `t` is a host struct of device pointers, t->hyper is ignored and the step count is
+ * hyper->step. */
+int mi_adamw_step_fused_chain(const mi_adamw_tensor *d_tensors, const mi_adamw_chunk *d_chunks,
+                              int64_t n_chunks, int64_t chunk_elems,
+                              const mi_adamw_fused_hyper *hypers, int32_t n_hyper,
+                              const float *d_steps, const int32_t *d_step_index,
+                              const float *d_grad_scale, float grad_prescale,
+                              int32_t state_dtype, int32_t flags, int32_t max_blocks,
+                              void *stream);
+int mi_adamw_step_flat_fused_chain(const mi_adamw_tensor *t, const mi_adamw_fused_hyper *hyper,
+                                   const float *d_grad_scale, float grad_prescale,
+                                   int64_t chunk_elems, int32_t state_dtype, int32_t flags,
+                                   int32_t max_blocks, void *stream);
 
 /* Measurement helper with no counterpart in the reference, for benchmarks that want
  * the memory ceiling of the update on the tensors it actually runs on: the same

@@ -25,7 +25,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_DIR = os.environ.get("MI_ADAMW_LIB_DIR") or HERE
 LIB_PATH = os.path.join(LIB_DIR, "libmi_adamw.so")
 
-ABI_VERSION = 7
+ABI_VERSION = 8
 MAX_HYPER = 16
 MAX_NORM_BLOCKS = 4096
 NOALLOC_SCRATCH_BYTES = 4096
@@ -68,6 +68,8 @@ EXPORTS = (
     "mi_adamw_step_prescaled",
     "mi_adamw_step_flat_prescaled",
     "mi_adamw_step_capturable",
+    "mi_adamw_step_fused_chain",
+    "mi_adamw_step_flat_fused_chain",
     "mi_adamw_widen_bf16",
     "mi_adamw_probe",
     "mi_adamw_probe_flat",
@@ -129,10 +131,26 @@ class CaptHyper(ctypes.Structure):
     ]
 
 
+class FusedHyper(ctypes.Structure):
+    """mi_adamw_fused_hyper: one param group of a step in torch's fused=True chain."""
+
+    _fields_ = [
+        ("lr", ctypes.c_double),
+        ("beta1", ctypes.c_double),
+        ("beta2", ctypes.c_double),
+        ("weight_decay", ctypes.c_double),
+        ("eps", ctypes.c_double),
+        ("step", ctypes.c_float),
+        ("grad_sign", ctypes.c_float),
+        ("lr_ptr", ctypes.c_void_p),
+    ]
+
+
 assert ctypes.sizeof(TensorRow) == 64
 assert ctypes.sizeof(ChunkRow) == 8
 assert ctypes.sizeof(Hyper) == 32
 assert ctypes.sizeof(CaptHyper) == 48 and CaptHyper.lr_ptr.offset == 40
+assert ctypes.sizeof(FusedHyper) == 56 and FusedHyper.lr_ptr.offset == 48
 
 _vp = ctypes.c_void_p
 _i64 = ctypes.c_int64
@@ -159,6 +177,10 @@ _SIGNATURES = {
                                      ctypes.c_int),
     "mi_adamw_step_capturable": ([_vp, _vp, _i64, _i64, _vp, _i32, _vp, _vp, _vp, _i32, _i32,
                                   _i32, _vp], ctypes.c_int),
+    "mi_adamw_step_fused_chain": ([_vp, _vp, _i64, _i64, _vp, _i32, _vp, _vp, _vp, _f32, _i32,
+                                   _i32, _i32, _vp], ctypes.c_int),
+    "mi_adamw_step_flat_fused_chain": ([_vp, _vp, _vp, _f32, _i64, _i32, _i32, _i32, _vp],
+                                       ctypes.c_int),
     "mi_adamw_widen_bf16": ([_vp, _vp, _i64, _i64, _vp], ctypes.c_int),
     "mi_adamw_probe": ([_vp, _vp, _i64, _i64, _i32, _i32, _i32, _vp], ctypes.c_int),
     "mi_adamw_probe_flat": ([_vp, _i64, _i32, _i32, _i32, _vp], ctypes.c_int),
@@ -170,7 +192,8 @@ _host = None
 # The entry points the host extension calls, in the order _host.bind takes them.
 HOST_BINDINGS = ("mi_adamw_set_grads", "mi_adamw_grad_norm", "mi_adamw_grad_norm_flat",
                  "mi_adamw_grad_sumsq", "mi_adamw_grad_sumsq_flat", "mi_adamw_norm_from_sumsq",
-                 "mi_adamw_step_prescaled", "mi_adamw_step_flat_prescaled")
+                 "mi_adamw_step_prescaled", "mi_adamw_step_flat_prescaled",
+                 "mi_adamw_step_fused_chain", "mi_adamw_step_flat_fused_chain")
 
 
 class MiAdamwError(RuntimeError):

@@ -24,7 +24,8 @@
 //   prepare(plan, stream) -> int        steps 1-3: READY, READY_MOVED, FALLBACK or ERROR
 //   last_error(plan) -> int             the library's code behind the last ERROR
 //   norm(plan, stream, d_norm) -> int   mi_adamw_grad_norm* (or sumsq + finalize)
-//   update(plan, stream, hypers, n) -> int   mi_adamw_step*_prescaled
+//   update(plan, stream, hypers, n) -> int   mi_adamw_step*_prescaled, or with the
+//                                       fused=True chain mi_adamw_step*_fused_chain
 //   sync_versions(plan, dict)           dict[id(p)] = (p._version, p.data_ptr())
 
 #include <Python.h>
@@ -68,6 +69,12 @@ struct Api {
                           int32_t, void*) = nullptr;
     int (*step_flat_prescaled)(const mi_adamw_tensor*, const mi_adamw_hyper*, const float*,
                                float, int64_t, int32_t, int32_t, int32_t, void*) = nullptr;
+    int (*step_fused_chain)(const mi_adamw_tensor*, const mi_adamw_chunk*, int64_t, int64_t,
+                            const mi_adamw_fused_hyper*, int32_t, const float*, const int32_t*,
+                            const float*, float, int32_t, int32_t, int32_t, void*) = nullptr;
+    int (*step_flat_fused_chain)(const mi_adamw_tensor*, const mi_adamw_fused_hyper*,
+                                 const float*, float, int64_t, int32_t, int32_t, int32_t,
+                                 void*) = nullptr;
 };
 Api g_api;
 bool g_bound = false;
@@ -111,6 +118,7 @@ struct Plan {
     int64_t chunk_elems = 0;
     int32_t max_blocks = 0, state_code = 0, flags = 0;
     bool clip = false;
+    bool fused_chain = false;        // the hyperparameter sets are mi_adamw_fused_hyper
     float max_norm = 0.0f, prescale = 1.0f;
     double* partials = nullptr;
     float* coef = nullptr;
@@ -150,12 +158,13 @@ bool is_tensor(PyObject* obj) { return obj && THPVariable_Check(obj); }
 // ---------------------------------------------------------------------------
 
 PyObject* py_bind(PyObject*, PyObject* const* args, Py_ssize_t nargs) {
-    if (nargs != 8) {
-        PyErr_SetString(PyExc_TypeError, "bind: 8 function addresses");
+    constexpr int kN = 10;
+    if (nargs != kN) {
+        PyErr_SetString(PyExc_TypeError, "bind: 10 function addresses");
         return nullptr;
     }
-    void* a[8];
-    for (int i = 0; i < 8; ++i) {
+    void* a[kN];
+    for (int i = 0; i < kN; ++i) {
         a[i] = PyLong_AsVoidPtr(args[i]);
         if (!a[i]) {
             if (!PyErr_Occurred()) PyErr_SetString(PyExc_ValueError, "bind: null address");
@@ -170,6 +179,8 @@ PyObject* py_bind(PyObject*, PyObject* const* args, Py_ssize_t nargs) {
     std::memcpy(&g_api.norm_from_sumsq, &a[5], sizeof(void*));
     std::memcpy(&g_api.step_prescaled, &a[6], sizeof(void*));
     std::memcpy(&g_api.step_flat_prescaled, &a[7], sizeof(void*));
+    std::memcpy(&g_api.step_fused_chain, &a[8], sizeof(void*));
+    std::memcpy(&g_api.step_flat_fused_chain, &a[9], sizeof(void*));
     g_bound = true;
     Py_RETURN_NONE;
 }
@@ -185,7 +196,7 @@ PyObject* py_bind(PyObject*, PyObject* const* args, Py_ssize_t nargs) {
 //   launch:          (tables, d_rows, d_chunks, n_chunks, n_rows, host_rows, flat_row_addr,
 //                     flat_hyper)
 //   options:         (chunk_elems, max_blocks, state_code, flags, clip, max_norm, prescale,
-//                     partials, coef, sumsq, stream)
+//                     partials, coef, sumsq, stream, fused_chain)
 //   keep:            objects to keep alive while the plan exists
 PyObject* plan_new(PyObject* args);
 
@@ -263,12 +274,14 @@ PyObject* plan_new(PyObject* args) {
         }
         pl->flat_hyper = flat_hyper;
         long long chunk = 0;
-        int max_blocks = 0, state_code = 0, flags = 0, clip = 0;
+        int max_blocks = 0, state_code = 0, flags = 0, clip = 0, fused_chain = 0;
         float max_norm = 0, prescale = 1;
         unsigned long long partials = 0, coef = 0, sumsq = 0, stream = 0;
-        if (!PyArg_ParseTuple(opts_t, "LiiipffKKKK", &chunk, &max_blocks, &state_code, &flags,
-                              &clip, &max_norm, &prescale, &partials, &coef, &sumsq, &stream))
+        if (!PyArg_ParseTuple(opts_t, "LiiipffKKKKp", &chunk, &max_blocks, &state_code, &flags,
+                              &clip, &max_norm, &prescale, &partials, &coef, &sumsq, &stream,
+                              &fused_chain))
             goto fail;
+        pl->fused_chain = fused_chain;
         pl->chunk_elems = chunk;
         pl->max_blocks = max_blocks;
         pl->state_code = state_code;
@@ -491,11 +504,27 @@ PyObject* py_update(PyObject*, PyObject* const* args, Py_ssize_t nargs) {
     Plan* pl = get_plan(args[0]);
     if (!pl) return nullptr;
     void* s = PyLong_AsVoidPtr(args[1]);
-    const mi_adamw_hyper* h = static_cast<const mi_adamw_hyper*>(PyLong_AsVoidPtr(args[2]));
+    void* hv = PyLong_AsVoidPtr(args[2]);
     const long nh = PyLong_AsLong(args[3]);
     if (PyErr_Occurred()) return nullptr;
     const int32_t flags = pl->flags | (pl->clip ? MI_ADAMW_F_CLIP : 0);
     int rc;
+    if (pl->fused_chain) {
+        const mi_adamw_fused_hyper* fh = static_cast<const mi_adamw_fused_hyper*>(hv);
+        if (pl->tables) {
+            rc = g_api.step_fused_chain(pl->d_rows, pl->d_chunks, pl->n_chunks, pl->chunk_elems,
+                                        fh, static_cast<int32_t>(nh), nullptr, nullptr,
+                                        pl->coef, pl->prescale, pl->state_code, flags,
+                                        pl->max_blocks, s);
+        } else {
+            if (pl->flat_hyper >= nh) return PyLong_FromLong(MI_ADAMW_E_INVALID);
+            rc = g_api.step_flat_fused_chain(&pl->flat_row, fh + pl->flat_hyper, pl->coef,
+                                             pl->prescale, pl->chunk_elems, pl->state_code,
+                                             flags, pl->max_blocks, s);
+        }
+        return PyLong_FromLong(rc);
+    }
+    const mi_adamw_hyper* h = static_cast<const mi_adamw_hyper*>(hv);
     if (pl->tables) {
         rc = g_api.step_prescaled(pl->d_rows, pl->d_chunks, pl->n_chunks, pl->chunk_elems, h,
                                   static_cast<int32_t>(nh), pl->coef, pl->prescale,

@@ -12,10 +12,13 @@
 //   mi_adamw_update_kernel pass 2: p, g, m, v streamed with dwordx4 loads and
 //                          stores, the AdamW op chain in fp32 registers, optional
 //                          bf16 moments, bf16 model copy, gradient write-back and
-//                          amsgrad's running maximum of v.  Two chains: torch's
-//                          default one (per-step scalars from the host) and its
+//                          amsgrad's running maximum of v.  Three chains: torch's
+//                          default one (per-step scalars from the host), its
 //                          capturable one (per-step scalars formed per workgroup
-//                          from a device step count, for HIP graph capture).
+//                          from a device step count, for HIP graph capture) and
+//                          its fused=True one (_fused_adamw_: float64 scalars and
+//                          float64 moment updates, per-step values formed per
+//                          workgroup from the step count).
 //   mi_adamw_scale_kernel  g *= coef in place (clip_grad_norm_'s write-back).
 //   mi_adamw_widen_kernel  bf16 -> fp32 of many tensors in one launch (the backward of
 //                          the bf16 weight copies the forward runs on), exact.
@@ -26,10 +29,12 @@
 // tensor) so that all parameter tensors go through one launch, or one
 // contiguous range in the flat-buffer layout.
 //
-// The element math follows torch's per-op chain (torch/optim/adam.py:419-547)
-// with one fp32 rounding per ATen op.  The file is compiled with
+// The default element math follows torch's per-op chain (torch/optim/adam.py:419-547)
+// with one fp32 rounding per ATen op; the fused=True chain follows adam_math of
+// ATen/native/hip/fused_adam_utils.cuh.  The file is compiled with
 // -ffp-contract=off; each fused multiply-add below is explicit and sits where
-// torch-ROCm's own kernels fuse (lerp, addcmul, addcdiv).
+// torch-ROCm's own kernels fuse (lerp, addcmul, addcdiv; in the fused chain the
+// float64 moment sums and the weight decay).
 
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -37,6 +42,7 @@
 #include <string.h>
 
 #include <atomic>
+#include <cmath>
 #include <mutex>
 #include <vector>
 
@@ -73,6 +79,9 @@ static_assert(offsetof(mi_adamw_tensor, hyper) == 56 && offsetof(mi_adamw_tensor
 static_assert(sizeof(mi_adamw_chunk) == 8, "mi_adamw_chunk is two int32");
 static_assert(sizeof(mi_adamw_capt_hyper) == 48 && offsetof(mi_adamw_capt_hyper, lr_ptr) == 40,
               "mi_adamw_capt_hyper: ten 4-byte fields, then the lr pointer");
+static_assert(sizeof(mi_adamw_fused_hyper) == 56 && offsetof(mi_adamw_fused_hyper, step) == 40 &&
+                  offsetof(mi_adamw_fused_hyper, lr_ptr) == 48,
+              "mi_adamw_fused_hyper: five doubles, two floats, then the lr pointer");
 
 // ---------------------------------------------------------------------------
 // Element math
@@ -142,6 +151,41 @@ __device__ __forceinline__ void adamw_elem(float& p, float g, float& m, float& v
     }
 }
 
+// The scalars of torch's fused=True chain for one workgroup (FusedHyper): the float64
+// hyperparameters as _fused_adamw_ receives them, and the per-step values it forms.
+struct FusedScalars {
+    double beta1, one_minus_beta1;
+    double beta2, one_minus_beta2;
+    double lr_wd;          // lr * weight_decay
+    double eps;
+    float step_size;       // f32(lr / (double)f32(1 - beta1^step))
+    float bc2_sqrt;        // f32(sqrt(1 - beta2^step))
+    float grad_sign;
+    bool decay;            // weight_decay != 0
+};
+
+// One element of adam_math (fused_adam_utils.cuh, ADAMW mode): m, v and the decayed
+// p are float64 expressions of fp32 values, each rounded once to fp32; the contractions
+// are those of torch-ROCm's build of that kernel (the left product of each sum fused).
+// ::max there is fmaxf.  g already carries the clip scale and sign.
+template <bool kAms, bool kCapt>
+__device__ __forceinline__ void adamw_elem(float& p, float g, float& m, float& v, float& x,
+                                           const FusedScalars& h) {
+    if (h.decay)                                           // param -= lr * wd * param
+        p = static_cast<float>(__builtin_fma(-h.lr_wd, double(p), double(p)));
+    const double dg = g;
+    m = static_cast<float>(__builtin_fma(h.beta1, double(m), h.one_minus_beta1 * dg));
+    v = static_cast<float>(__builtin_fma(h.beta2, double(v), (h.one_minus_beta2 * dg) * dg));
+    float dv = v;
+    if (kAms) {
+        x = __builtin_fmaxf(x, v);
+        dv = x;
+    }
+    const float q = __builtin_sqrtf(dv) / h.bc2_sqrt;     // fp32 sqrt and division
+    const float d = static_cast<float>(double(q) + h.eps); // + eps in float64
+    p = p - (h.step_size * m) / d;                         // fp32
+}
+
 // ---------------------------------------------------------------------------
 // Streaming loads and stores.  The update touches every value once per step, so
 // its loads and stores carry the nontemporal hint (measured: ordinary ones make
@@ -191,10 +235,10 @@ __device__ __forceinline__ void st4_bf16(uint16_t* p, f32x4 v) {
     __builtin_nontemporal_store(w, (GLOBAL u32x2*)(p));
 }
 
-// adamw_elem on the four lanes of a dwordx4 group.
-template <bool kAms, bool kCapt>
+// adamw_elem on the four lanes of a dwordx4 group (H: ElemScalars or FusedScalars).
+template <bool kAms, bool kCapt, class H>
 __device__ __forceinline__ void adamw_vec(f32x4& p, f32x4 g, f32x4& m, f32x4& v, f32x4& x,
-                                          const ElemScalars& h) {
+                                          const H& h) {
     float p0 = p.x, p1 = p.y, p2 = p.z, p3 = p.w;
     float m0 = m.x, m1 = m.y, m2 = m.z, m3 = m.w;
     float v0 = v.x, v1 = v.y, v2 = v.z, v3 = v.w;
@@ -288,7 +332,9 @@ struct FlatSource {
 
 // Default chain: the host formed every per-step value (adam.py:529-536).
 struct StaticHyper {
+    using Scalars = ElemScalars;
     static constexpr bool kCapt = false;
+    static constexpr bool kLate = false;
     static constexpr bool kProbe = false;
     HyperPack hp;
     __device__ __forceinline__ ElemScalars get(const mi_adamw_tensor& t, int32_t) const {
@@ -309,7 +355,9 @@ struct CaptPack {
 // change during the launch, so they are read through the constant address
 // space (scalar loads).
 struct CaptHyper {
+    using Scalars = ElemScalars;
     static constexpr bool kCapt = true;
+    static constexpr bool kLate = true;
     static constexpr bool kProbe = false;
     CaptPack cp;
     const float* steps;
@@ -344,13 +392,79 @@ struct CaptHyper {
     }
 };
 
+// One set of the fused=True chain as the kernel takes it: the float64 hyperparameters
+// and, with host step counts, the two per-step values the library formed on the host
+// from them (fused_set_from).
+struct FusedSet {
+    double beta1, one_minus_beta1;
+    double beta2, one_minus_beta2;
+    double lr, weight_decay, eps;
+    float bc1;                   // f32(1 - pow(beta1, step))
+    float bc2_sqrt;              // f32(sqrt(1 - pow(beta2, step)))
+    float grad_sign;
+    int32_t decay;               // weight_decay != 0
+    const float* lr_ptr;         // device fp32 lr, or NULL
+};
+
+struct FusedPack {
+    FusedSet h[MI_ADAMW_MAX_HYPER];
+};
+
+// pow in float64, out of line: inlined into the update it adds 10-15 VGPRs to every
+// instance of the device-step chain.
+__device__ __attribute__((noinline)) double pow_f64(double x, double y) { return pow(x, y); }
+
+// torch's fused=True chain: the per-step values of fused_adam_utils.cuh
+// FusedAdamMathFunctor, as adam_math's fp32 (opmath_t) parameters take them.
+// bc1 and bc2_sqrt come from the set (host step counts) or, with kDevSteps, are formed
+// here from the row's device step count with the device pow and sqrt, as that functor
+// does; step_size = f32(lr / bc1) and lr * weight_decay are formed here in float64 in
+// both cases, from the host lr or a device lr.  Device step counts and a device lr
+// were written by earlier work on the stream and do not change during the launch, so
+// they are read through the constant address space.
+template <bool kDevSteps>
+struct FusedHyper {
+    using Scalars = FusedScalars;
+    static constexpr bool kCapt = false;
+    static constexpr bool kLate = true;
+    static constexpr bool kProbe = false;
+    FusedPack fp;
+    const float* steps;
+    const int32_t* step_index;
+    __device__ __forceinline__ FusedScalars get(const mi_adamw_tensor& t, int32_t row) const {
+        const FusedSet& c = fp.h[t.hyper];
+        float bc1 = c.bc1, bc2_sqrt = c.bc2_sqrt;
+        if (kDevSteps) {
+            const int32_t slot = *((const CONSTANT int32_t*)(step_index) + row);
+            const double step = *((const CONSTANT float*)(steps) + slot);
+            bc1 = static_cast<float>(1.0 - pow_f64(c.beta1, step));
+            bc2_sqrt = static_cast<float>(sqrt(1.0 - pow_f64(c.beta2, step)));
+        }
+        const double lr = c.lr_ptr ? double(*(const CONSTANT float*)(c.lr_ptr)) : c.lr;
+        FusedScalars s;
+        s.beta1 = c.beta1;
+        s.one_minus_beta1 = c.one_minus_beta1;
+        s.beta2 = c.beta2;
+        s.one_minus_beta2 = c.one_minus_beta2;
+        s.lr_wd = lr * c.weight_decay;
+        s.eps = c.eps;
+        s.step_size = static_cast<float>(lr / double(bc1));
+        s.bc2_sqrt = bc2_sqrt;
+        s.grad_sign = c.grad_sign;
+        s.decay = c.decay != 0;
+        return s;
+    }
+};
+
 // Memory-only twin of the update, for measurement (mi_adamw_probe): the same
 // loads and stores, launch shape and cache hints, with the arithmetic left out.
 // Every value is stored back as it was read (the bf16 copy as the bf16 of the
 // master, which the step keeps it equal to), so running it leaves the tensors
 // unchanged.
 struct ProbeHyper {
+    using Scalars = ElemScalars;
     static constexpr bool kCapt = false;
+    static constexpr bool kLate = false;
     static constexpr bool kProbe = true;
     __device__ __forceinline__ ElemScalars get(const mi_adamw_tensor&, int32_t) const {
         return ElemScalars{};
@@ -561,13 +675,25 @@ struct Tile {
     }
 };
 
+// Waves per SIMD each instance must allow: 8 (two workgroups per CU, at most 64 VGPRs)
+// for the fused=True chain's instances without amsgrad, whose float64 math would
+// otherwise take 65-70 VGPRs and halve the workgroups in flight; 4 (one workgroup,
+// what 1024-thread workgroups need anyway) for the rest.
+template <class HS, bool kAms>
+constexpr int update_waves_per_eu() {
+    return (HS::kLate && !HS::kCapt && !kAms) ? 8 : 4;
+}
+
 template <class Src, class HS, typename StateT, bool kClip, bool kCopy, bool kWriteGrad, bool kAms>
-__global__ __launch_bounds__(kUpdThreads) void mi_adamw_update_kernel(
+__global__ __launch_bounds__(kUpdThreads)
+__attribute__((amdgpu_waves_per_eu(update_waves_per_eu<HS, kAms>())))
+void mi_adamw_update_kernel(
     Src src, int64_t n_chunks, int64_t chunk_elems, HS hs,
     const float* __restrict__ grad_scale, float pre) {
     using IO = StateIO<StateT>;
     using T = Tile<StateT, kAms>;
     constexpr bool kCapt = HS::kCapt;
+    constexpr bool kLate = HS::kLate;
     constexpr bool kProbe = HS::kProbe;
     const float scale = kClip ? *grad_scale : 1.0f;
     for (int64_t c = blockIdx.x; c < n_chunks; c += gridDim.x) {
@@ -575,11 +701,11 @@ __global__ __launch_bounds__(kUpdThreads) void mi_adamw_update_kernel(
         int64_t begin, end;
         int32_t row;
         src.get(c, chunk_elems, t, begin, end, row);
-        // Default chain: the scalars are kernel arguments.  Capturable chain: they
-        // take a few hundred instructions (two powf, three divisions), formed once
-        // the first tile's loads are in flight.
-        ElemScalars h;
-        if (!kCapt) h = hs.get(t, row);
+        // Default chain: the scalars are kernel arguments.  Capturable and fused
+        // chains: they take a few hundred instructions (two pow, divisions), formed
+        // once the first tile's loads are in flight.
+        typename HS::Scalars h;
+        if (!kLate) h = hs.get(t, row);
         float* __restrict__ P = t.param;
         float* __restrict__ G = t.grad;
         void* __restrict__ M = t.exp_avg;
@@ -594,7 +720,7 @@ __global__ __launch_bounds__(kUpdThreads) void mi_adamw_update_kernel(
             if (i < vend) {
                 T cur;
                 cur.load(P, G, M, V, X, i);
-                if (kCapt) {
+                if (kLate) {
                     __builtin_amdgcn_sched_barrier(0);
                     h = hs.get(t, row);
                 }
@@ -627,7 +753,7 @@ __global__ __launch_bounds__(kUpdThreads) void mi_adamw_update_kernel(
         }
         // Scalar path: the ragged tail of a vector tensor, or a whole tensor
         // whose pointers are not aligned for dwordx4.
-        if (kCapt && vend < end) h = hs.get(t, row);
+        if (kLate && vend < end) h = hs.get(t, row);
         const float gmul = h.grad_sign;
         for (int64_t j = vend + threadIdx.x; j < end; j += kUpdThreads) {
             float g1 = ld1(G + j) * pre;
@@ -880,6 +1006,31 @@ int launch_probe(const Src& src, int64_t n_chunks, int64_t chunk_elems, int32_t 
                                                               nullptr, 1.0f, flags, grid, s);
 }
 
+// The kernel's form of one mi_adamw_fused_hyper.  With host step counts the per-step
+// values torch's kernel forms in float64 on the device are formed here with the host
+// libm pow and sqrt, then rounded to fp32 as adam_math takes them.  (The device pow and
+// libm pow can differ in the last float64 bit; for the betas tested over steps 1-1e6
+// that never moves the fp32 values.)
+FusedSet fused_set_from(const mi_adamw_fused_hyper& h, bool host_steps) {
+    FusedSet f;
+    memset(&f, 0, sizeof(f));
+    f.beta1 = h.beta1;
+    f.one_minus_beta1 = 1.0 - h.beta1;
+    f.beta2 = h.beta2;
+    f.one_minus_beta2 = 1.0 - h.beta2;
+    f.lr = h.lr;
+    f.weight_decay = h.weight_decay;
+    f.eps = h.eps;
+    if (host_steps) {
+        f.bc1 = static_cast<float>(1.0 - std::pow(h.beta1, double(h.step)));
+        f.bc2_sqrt = static_cast<float>(std::sqrt(1.0 - std::pow(h.beta2, double(h.step))));
+    }
+    f.grad_sign = h.grad_sign;
+    f.decay = h.weight_decay != 0.0;
+    f.lr_ptr = h.lr_ptr;
+    return f;
+}
+
 // Validate one host-visible tensor descriptor for the flat entry points.
 int check_flat(const mi_adamw_tensor* t, int32_t state_dtype, int32_t flags) {
     if (!t || t->numel <= 0 || !t->param || !t->grad || !t->exp_avg || !t->exp_avg_sq)
@@ -955,9 +1106,9 @@ int scratch_on(hipStream_t s, double** out) {
 extern "C" {
 
 const char* mi_adamw_version(void) {
-    return "mi_adamw 7 gfx950 fused clip+adamw (fp32/bf16 state, bf16 copy, amsgrad, flat, "
-           "capturable, bf16 widen, memory probe, no-alloc norm, range norm, grad prescale, "
-           "grad patch)";
+    return "mi_adamw 8 gfx950 fused clip+adamw (fp32/bf16 state, bf16 copy, amsgrad, flat, "
+           "capturable, fused=True chain, bf16 widen, memory probe, no-alloc norm, range norm, "
+           "grad prescale, grad patch)";
 }
 
 const char* mi_adamw_strerror(int code) {
@@ -1189,6 +1340,53 @@ int mi_adamw_step_capturable(const mi_adamw_tensor* d_tensors, const mi_adamw_ch
     TableSource src{d_tensors, d_chunks};
     return launch_update(src, n_chunks, chunk_elems, hs, d_grad_scale, state_dtype, flags,
                          max_blocks, static_cast<hipStream_t>(stream));
+}
+
+int mi_adamw_step_fused_chain(const mi_adamw_tensor* d_tensors, const mi_adamw_chunk* d_chunks,
+                              int64_t n_chunks, int64_t chunk_elems,
+                              const mi_adamw_fused_hyper* hypers, int32_t n_hyper,
+                              const float* d_steps, const int32_t* d_step_index,
+                              const float* d_grad_scale, float grad_prescale,
+                              int32_t state_dtype, int32_t flags, int32_t max_blocks,
+                              void* stream) {
+    if (!d_tensors || !d_chunks || !hypers || n_hyper <= 0 || n_hyper > MI_ADAMW_MAX_HYPER ||
+        !finite(grad_prescale) || (d_steps == nullptr) != (d_step_index == nullptr))
+        return MI_ADAMW_E_INVALID;
+    TableSource src{d_tensors, d_chunks};
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    if (d_steps) {
+        FusedHyper<true> hs;
+        memset(&hs, 0, sizeof(hs));
+        for (int32_t i = 0; i < n_hyper; ++i) hs.fp.h[i] = fused_set_from(hypers[i], false);
+        hs.steps = d_steps;
+        hs.step_index = d_step_index;
+        return launch_update(src, n_chunks, chunk_elems, hs, d_grad_scale, state_dtype, flags,
+                             max_blocks, s, grad_prescale);
+    }
+    FusedHyper<false> hs;
+    memset(&hs, 0, sizeof(hs));
+    for (int32_t i = 0; i < n_hyper; ++i) hs.fp.h[i] = fused_set_from(hypers[i], true);
+    return launch_update(src, n_chunks, chunk_elems, hs, d_grad_scale, state_dtype, flags,
+                         max_blocks, s, grad_prescale);
+}
+
+int mi_adamw_step_flat_fused_chain(const mi_adamw_tensor* t, const mi_adamw_fused_hyper* hyper,
+                                   const float* d_grad_scale, float grad_prescale,
+                                   int64_t chunk_elems, int32_t state_dtype, int32_t flags,
+                                   int32_t max_blocks, void* stream) {
+    if (!hyper || !chunk_elems_ok(chunk_elems) || !finite(grad_prescale))
+        return MI_ADAMW_E_INVALID;
+    int rc = check_flat(t, state_dtype, flags);
+    if (rc != MI_ADAMW_OK) return rc;
+    FusedHyper<false> hs;
+    memset(&hs, 0, sizeof(hs));
+    hs.fp.h[0] = fused_set_from(*hyper, true);
+    FlatSource src;
+    src.t = *t;
+    src.t.hyper = 0;
+    const int64_t n_chunks = (t->numel + chunk_elems - 1) / chunk_elems;
+    return launch_update(src, n_chunks, chunk_elems, hs, d_grad_scale, state_dtype, flags,
+                         max_blocks, static_cast<hipStream_t>(stream), grad_prescale);
 }
 
 int mi_adamw_probe(const mi_adamw_tensor* d_tensors, const mi_adamw_chunk* d_chunks,

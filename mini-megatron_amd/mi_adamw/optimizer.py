@@ -125,6 +125,32 @@ def _capt_hyper(group: dict, device: torch.device) -> _lib.CaptHyper:
     return h
 
 
+def _fused_hyper(group: dict, step: float, device: torch.device) -> _lib.FusedHyper:
+    """One group's set for torch's fused=True chain (adam.py:803-895 -> _fused_adamw_).
+
+    The hyperparameters go in as the float64 values that op receives; ``step`` is the
+    count after this step's increment (unused when the launch reads device step counts).
+    A tensor lr: on the CPU, its value as a float64 (the op's tensor-lr overload takes
+    ``lr.item()``); on the parameters' device, a one-element fp32 tensor read by the
+    kernel (the op reads it as fp32 there)."""
+    lr = group["lr"]
+    beta1, beta2 = (float(b) for b in group["betas"])
+    h = _lib.FusedHyper(lr=0.0, beta1=beta1, beta2=beta2,
+                        weight_decay=float(group["weight_decay"]), eps=float(group["eps"]),
+                        step=float(np.float32(step)),
+                        grad_sign=-1.0 if group["maximize"] else 1.0, lr_ptr=None)
+    if not isinstance(lr, torch.Tensor):
+        h.lr = float(lr)
+    elif lr.device.type == "cpu":
+        h.lr = float(lr.item())
+    else:
+        if lr.dtype != torch.float32 or lr.device != device or lr.numel() != 1:
+            raise NotImplementedError("FusedAdamW(fused=True): a device lr must be a one-element "
+                                      "float32 tensor on the parameters' device")
+        h.lr_ptr = lr.data_ptr()
+    return h
+
+
 def _refuse_under_capture(what: str) -> None:
     """Host-to-device uploads cannot be recorded into a graph: a step under capture
     must find everything an earlier eager step built."""
@@ -242,7 +268,7 @@ class _Fast:
     the Python objects whose identity says the plan still describes this optimizer."""
 
     __slots__ = ("plan", "cache", "steps", "state", "groups_key", "options", "hyper_group",
-                 "hyper_steps", "harr", "harr_addr", "clip", "device", "dev_index")
+                 "hyper_steps", "harr", "harr_addr", "clip", "device", "dev_index", "fused")
 
 
 class FusedAdamW(Optimizer):
@@ -833,7 +859,10 @@ class FusedAdamW(Optimizer):
             gis = sorted({rec.gi for rec, _ in entries})
             remap = {gi: i for i, gi in enumerate(gis)}
             hyper_idx = [remap[rec.gi] for rec, _ in entries]
-            hypers = [_capt_hyper(self.param_groups[gi], device) for gi in gis]
+            groups = self.param_groups
+            hyper_fused = [bool(groups[gi]["fused"]) for gi in gis]
+            hypers = [_fused_hyper(groups[gi], 0.0, device) if f
+                      else _capt_hyper(groups[gi], device) for gi, f in zip(gis, hyper_fused)]
             hyper_ams = [ams_g[gi] for gi in gis]
         else:
             # step_t += 1 for every param with a grad (adam.py:414), in one op.
@@ -858,12 +887,15 @@ class FusedAdamW(Optimizer):
                     if h is None:
                         h = keys[k] = len(keys)
                     hyper_idx.append(h)
-            hypers = [_hyper(self.param_groups[gi], step) for (gi, step) in keys]
+            groups = self.param_groups
+            hyper_fused = [bool(groups[gi]["fused"]) for (gi, _) in keys]
+            hypers = [_fused_hyper(groups[gi], step, device) if f else _hyper(groups[gi], step)
+                      for (gi, step), f in zip(keys, hyper_fused)]
             hyper_ams = [ams_g[gi] for (gi, _) in keys]
             hyper_group = [gi for (gi, _) in keys]
 
         with torch.cuda.device(device):
-            self._launch(entries, hyper_idx, hypers, hyper_ams, device,
+            self._launch(entries, hyper_idx, hypers, hyper_ams, hyper_fused, device,
                          None if self.capturable else hyper_group)
         if self._copy_sync is not None:
             # the launch wrote these masters' copies
@@ -904,11 +936,12 @@ class FusedAdamW(Optimizer):
 
     def _groups_key(self) -> tuple:
         """The groups' parameters (by identity, so a parameter swapped into a group's list
-        in place is seen) and amsgrad settings."""
-        return tuple((tuple(map(id, g["params"])), bool(g["amsgrad"])) for g in self.param_groups)
+        in place is seen), amsgrad settings and chains (fused)."""
+        return tuple((tuple(map(id, g["params"])), bool(g["amsgrad"]), bool(g["fused"]))
+                     for g in self.param_groups)
 
-    def _make_fast(self, entries, hyper_idx, hyper_group, ams, launch, device, stream, partials,
-                   coef, state_code, flags):
+    def _make_fast(self, entries, hyper_idx, hyper_group, ams, fused, launch, device, stream,
+                   partials, coef, state_code, flags):
         """The native path's plan for the steps after this one, when this step's launch is
         one the native path can repeat: every parameter stepped, one launch that the norm
         pass shares, one hyperparameter set per param group."""
@@ -949,7 +982,7 @@ class FusedAdamW(Optimizer):
                 (int(self.chunk_elems), int(self.max_blocks), int(state_code), int(flags), clip,
                  float(self.max_grad_norm or 0.0), float(self.grad_prescale),
                  partials.data_ptr(), coef.data_ptr(), 0 if sumsq is None else sumsq.data_ptr(),
-                 int(stream)),
+                 int(stream), bool(fused)),
                 (launch.rows, launch.chunks, launch.host_rows, self._steps, hyper_steps,
                  partials, coef, sumsq))
         except (TypeError, ValueError):
@@ -963,7 +996,8 @@ class FusedAdamW(Optimizer):
         fast.options = self._options_key()
         fast.hyper_group = list(hyper_group)
         fast.hyper_steps = hyper_steps
-        fast.harr = (_lib.Hyper * len(hyper_group))()
+        fast.fused = bool(fused)
+        fast.harr = ((_lib.FusedHyper if fused else _lib.Hyper) * len(hyper_group))()
         fast.harr_addr = ctypes.addressof(fast.harr)
         fast.clip = clip
         fast.device = device
@@ -1011,8 +1045,12 @@ class FusedAdamW(Optimizer):
             return False
         groups = self.param_groups
         harr = fast.harr
-        for h, gi in enumerate(fast.hyper_group):
-            harr[h] = _hyper(groups[gi], float(fast.hyper_steps[h]))
+        if fast.fused:
+            for h, gi in enumerate(fast.hyper_group):
+                harr[h] = _fused_hyper(groups[gi], float(fast.hyper_steps[h]), fast.device)
+        else:
+            for h, gi in enumerate(fast.hyper_group):
+                harr[h] = _hyper(groups[gi], float(fast.hyper_steps[h]))
         ev = self.timing_events
         if ev is not None:
             ev[0].record()
@@ -1135,10 +1173,10 @@ class FusedAdamW(Optimizer):
         return self._copies[id(p)]
 
     @staticmethod
-    def _signature(entries, hyper_idx, hyper_ams) -> tuple[list, list]:
+    def _signature(entries, hyper_idx, hyper_ams, hyper_fused) -> tuple[list, list]:
         """What a launch's tables encode, in two parts: the hyperparameter assignment,
-        the amsgrad setting of each hyperparameter set (which decides how the entries
-        are split into launches), and the parameter and state pointers, which rarely
+        the amsgrad setting and chain of each hyperparameter set (which decide how the
+        entries are split into launches), and the parameter and state pointers, which rarely
         change; and the gradient pointers, which change whenever zero_grad() frees the
         gradients and backward allocates them elsewhere."""
         # the element count and contiguity too: a parameter narrowed or re-strided in place
@@ -1149,6 +1187,7 @@ class FusedAdamW(Optimizer):
                for rec, _ in entries]
         sig.append(tuple(hyper_idx))
         sig.append(tuple(bool(a) for a in hyper_ams))
+        sig.append(tuple(bool(f) for f in hyper_fused))
         return sig, [g.data_ptr() for _, g in entries]
 
     @staticmethod
@@ -1160,7 +1199,7 @@ class FusedAdamW(Optimizer):
                               max_exp_avg_sq=int(r["max_exp_avg_sq"]), numel=int(r["numel"]),
                               hyper=0, flags=int(r["flags"]))
 
-    def _launch(self, entries, hyper_idx, hypers, hyper_ams, device,
+    def _launch(self, entries, hyper_idx, hypers, hyper_ams, hyper_fused, device,
                 hyper_group: list | None = None) -> None:
         lib = _lib.load()
         self._fast = None
@@ -1171,28 +1210,28 @@ class FusedAdamW(Optimizer):
             flags |= _lib.F_BF16_COPY
         state_code = _lib.STATE_BF16 if self.state_dtype == torch.bfloat16 else _lib.STATE_F32
 
-        # Partition into launches of one amsgrad setting and at most MAX_HYPER
-        # hyperparameter sets each.
-        n_ams = sum(hyper_ams)
-        if len(hypers) <= _lib.MAX_HYPER and n_ams in (0, len(hypers)):
-            parts = [(entries, hyper_idx, hypers, n_ams > 0, None)]
+        # Partition into launches of one amsgrad setting and one chain (default or
+        # fused=True) and at most MAX_HYPER hyperparameter sets each.
+        kinds = list(zip(hyper_ams, hyper_fused))
+        if len(hypers) <= _lib.MAX_HYPER and len(set(kinds)) == 1:
+            parts = [(entries, hyper_idx, hypers, kinds[0], None)]
         else:
             parts = []
-            for ams in (False, True):
-                hsel = [h for h in range(len(hypers)) if hyper_ams[h] == ams]
+            for kind in sorted(set(kinds)):
+                hsel = [h for h in range(len(hypers)) if kinds[h] == kind]
                 for start in range(0, len(hsel), _lib.MAX_HYPER):
                     block = hsel[start:start + _lib.MAX_HYPER]
                     remap = {h: j for j, h in enumerate(block)}
                     sel = [i for i, h in enumerate(hyper_idx) if h in remap]
                     parts.append(([entries[i] for i in sel],
                                   [remap[hyper_idx[i]] for i in sel],
-                                  [hypers[h] for h in block], ams,
+                                  [hypers[h] for h in block], kind,
                                   np.asarray(sel, dtype=np.int64)))
 
         # Tables: reused while the pointers and the hyperparameter assignment are
         # unchanged; when only the gradients moved, the rows are rewritten and the
         # chunk tables kept.
-        sig, grads = self._signature(entries, hyper_idx, hyper_ams)
+        sig, grads = self._signature(entries, hyper_idx, hyper_ams, hyper_fused)
         cache = self._launch_cache
         if cache is not None and cache.sig == sig and cache.device == device:
             launches, norm_launch = cache.launches, cache.norm_launch
@@ -1215,7 +1254,7 @@ class FusedAdamW(Optimizer):
                 self._check_param(rec.p, g)
                 if rec.p.device != device:
                     raise NotImplementedError("FusedAdamW: all parameters must be on one device")
-            launches = [self._new_launch(e, hi, a, device) for e, hi, _, a, _ in parts]
+            launches = [self._new_launch(e, hi, k[0], device) for e, hi, _, k, _ in parts]
             if len(parts) == 1:
                 norm_launch = launches[0]
             else:
@@ -1265,10 +1304,13 @@ class FusedAdamW(Optimizer):
                 flags |= _lib.F_WRITE_GRAD
         if ev is not None:
             ev[1].record()
-        for launch, (_, _, hs, ams, _) in zip(launches, parts):
+        for launch, (_, _, hs, (ams, fused), _) in zip(launches, parts):
             if launch.n_chunks == 0:
                 continue
             lflags = flags | (_lib.F_AMSGRAD if ams else 0)
+            if fused:
+                self._launch_fused_chain(launch, hs, coef, state_code, lflags, stream)
+                continue
             if self.capturable:
                 carr = (_lib.CaptHyper * len(hs))(*hs)
                 _lib.check(lib.mi_adamw_step_capturable(
@@ -1306,5 +1348,27 @@ class FusedAdamW(Optimizer):
             ev[2].record()
         if len(parts) == 1 and hyper_group is not None:
             self._fast = self._make_fast(entries, hyper_idx, hyper_group, hyper_ams[0],
-                                         launches[0], device, stream, partials, coef,
-                                         state_code, flags & ~_lib.F_CLIP)
+                                         hyper_fused[0], launches[0], device, stream, partials,
+                                         coef, state_code, flags & ~_lib.F_CLIP)
+
+    def _launch_fused_chain(self, launch: _Launch, hs: list, coef: torch.Tensor,
+                            state_code: int, flags: int, stream: int) -> None:
+        """One launch of torch's fused=True chain: the tables (with the device step counts
+        when capturable) or the one flat range."""
+        lib = _lib.load()
+        pre = self.grad_prescale
+        if launch.n_rows == 1 and not launch.tables:
+            row = self._row_struct(launch)
+            row_h = hs[int(launch.host_rows[0]["hyper"])]
+            _lib.check(lib.mi_adamw_step_flat_fused_chain(
+                ctypes.byref(row), ctypes.byref(row_h), coef.data_ptr(), pre, self.chunk_elems,
+                state_code, flags, self.max_blocks, stream), "mi_adamw_step_flat_fused_chain")
+            return
+        farr = (_lib.FusedHyper * len(hs))(*hs)
+        steps = idx = None
+        if self.capturable:
+            steps, idx = self._steps.data_ptr(), launch.step_index.data_ptr()
+        _lib.check(lib.mi_adamw_step_fused_chain(
+            launch.rows.data_ptr(), launch.chunks.data_ptr(), launch.n_chunks, self.chunk_elems,
+            farr, len(hs), steps, idx, coef.data_ptr(), pre, state_code, flags, self.max_blocks,
+            stream), "mi_adamw_step_fused_chain")

@@ -122,7 +122,7 @@ class ZeroRangeStep:
                 [-2] * n, [True] * n, [p.grad.data_ptr() for _, p in entries], False,
                 (steps.data_ptr(), steps.numel()), (hyper_steps.ctypes.data, len(hyper_steps)),
                 (False, 0, 0, 0, 0, 0, ctypes.addressof(row), 0),
-                (0, 0, 0, 0, False, 0.0, 1.0, 0, 0, 0, int(stream)),
+                (0, 0, 0, 0, False, 0.0, 1.0, 0, 0, 0, int(stream), False),
                 (steps, hyper_steps, row))
         except (TypeError, ValueError):
             return
@@ -141,10 +141,17 @@ class ZeroRangeStep:
         host = _lib._host
         if host.prepare(pl.plan, self._stream()) != host.READY:
             return None
-        from .optimizer import _hyper
         self.native_begins += 1
-        return [_hyper(g, float(pl.hyper_steps[gi])) if nonempty else None
+        return [self._group_hyper(g, float(pl.hyper_steps[gi])) if nonempty else None
                 for gi, (g, nonempty) in enumerate(zip(opt.param_groups, pl.nonempty))]
+
+    def _group_hyper(self, group: dict, step: float):
+        """The group's set at step `step`: torch's fused=True chain for a fused group, the
+        default chain otherwise (as FusedAdamW.step takes them)."""
+        from .optimizer import _fused_hyper, _hyper
+        if group["fused"]:
+            return _fused_hyper(group, step, self.flat.device)
+        return _hyper(group, step)
 
     def segments(self, rank: int) -> list[tuple[int, int, int]]:
         """(param group, lo, hi) pieces of rank's slice, one per group it overlaps."""
@@ -157,9 +164,10 @@ class ZeroRangeStep:
         return out
 
     @torch.no_grad()
-    def begin(self) -> list[_lib.Hyper]:
+    def begin(self) -> list:
         """Advance every parameter's step count by one (each rank keeps the same count) and
-        return one hyperparameter set per param group.  Every parameter must have its
+        return one hyperparameter set per param group (an mi_adamw_hyper, or for a group
+        with fused=True an mi_adamw_fused_hyper).  Every parameter must have its
         gradient view and all parameters of a group one step count, as in the flat step.
         After the first call, the checks and the counting run natively while nothing they
         cover changed; any change (a replaced tensor, a moved gradient, a new group, a loaded
@@ -168,7 +176,6 @@ class ZeroRangeStep:
         if hypers is not None:
             return hypers
         opt = self.opt
-        from .optimizer import _hyper
         steps = opt._steps_for(self.flat.device)
         group_slots = []
         for group in opt.param_groups:
@@ -203,7 +210,7 @@ class ZeroRangeStep:
                 hypers.append(None)
                 continue
             steps[idx] += 1
-            hypers.append(_hyper(group, float(steps[idx[0]])))
+            hypers.append(self._group_hyper(group, float(steps[idx[0]])))
         self._make_plan(self._stream())
         return hypers
 
@@ -279,11 +286,15 @@ class ZeroRangeStep:
                     exp_avg_sq=flat.exp_avg_sq.data_ptr() + s_item * lo,
                     param_copy=0 if flat.copy is None else flat.copy.data_ptr() + 2 * lo,
                     max_exp_avg_sq=0, numel=hi - lo, hyper=0, flags=_lib.T_VEC)
-                _lib.check(lib.mi_adamw_step_flat_prescaled(
-                    ctypes.byref(row), ctypes.byref(hypers[gi]),
-                    None if coef is None else coef.data_ptr(), self.grad_prescale,
-                    opt.chunk_elems, state, flags, opt.max_blocks, stream),
-                    "mi_adamw_step_flat_prescaled")
+                h = hypers[gi]
+                fused = isinstance(h, _lib.FusedHyper)
+                fn = (lib.mi_adamw_step_flat_fused_chain if fused
+                      else lib.mi_adamw_step_flat_prescaled)
+                _lib.check(fn(ctypes.byref(row), ctypes.byref(h),
+                              None if coef is None else coef.data_ptr(), self.grad_prescale,
+                              opt.chunk_elems, state, flags, opt.max_blocks, stream),
+                           "mi_adamw_step_flat_fused_chain" if fused
+                           else "mi_adamw_step_flat_prescaled")
 
     @torch.no_grad()
     def step(self):

@@ -231,6 +231,104 @@ void oracle_adamw_capt_bf16state(float *p, const float *g, uint16_t *m, uint16_t
     }
 }
 
+/* torch's fused=True chain: torch.optim.AdamW(fused=True) -> adam.py:803-895
+ * (_fused_adam: step counts += 1 on the device, then torch._fused_adamw_), whose
+ * per-element math is adam_math in ATen/native/hip/fused_adam_utils.cuh (ADAMW
+ * mode).  lr, the betas, weight decay and eps stay float64 there, so m, v and the
+ * decayed p are formed in float64 from the fp32 values and rounded once to fp32:
+ *   p  = f32(p - (lr*wd) * p)                       (only when wd != 0)
+ *   m  = f32(beta1*m + (1-beta1)*g)
+ *   v  = f32(beta2*v + ((1-beta2)*g)*g)
+ *   d  = f32((double)(sqrtf(v) / bc2_sqrt) + eps)   (amsgrad: from max(vmax, v))
+ *   p  = p - (step_size * m) / d                    (fp32 ops)
+ * The per-step values are float64 on the device and reach adam_math as fp32:
+ *   bc1 = f32(1 - pow(beta1, step)), bc2_sqrt = f32(sqrt(1 - pow(beta2, step))),
+ *   step_size = f32(lr / (double)bc1).
+ * Which float64 `a*b + c*d` torch-ROCm's compiler contracted into one fused
+ * multiply-add is the model's choice (oracle_fused_model); the pinned model is the
+ * one torch's own GPU results select on inputs where the candidates round apart. */
+void oracle_fused_scalars(double lr, double beta1, double beta2, float step, float *bc1,
+                          float *bc2_sqrt, float *step_size)
+{
+    double b1c = 1.0 - pow(beta1, (double)step);
+    double b2c = 1.0 - pow(beta2, (double)step);
+    *bc1 = (float)b1c;
+    *bc2_sqrt = (float)sqrt(b2c);
+    *step_size = (float)(lr / (double)*bc1);
+}
+
+/* oracle_fused_scalars' bc1 and bc2_sqrt for n step counts (beta1 for bc1, beta2 for
+ * bc2_sqrt). */
+void oracle_fused_scalars_many(double beta1, double beta2, const float *steps, int64_t n,
+                               float *bc1, float *bc2_sqrt)
+{
+    for (int64_t i = 0; i < n; ++i) {
+        float ss;
+        oracle_fused_scalars(1.0, beta1, beta2, steps[i], &bc1[i], &bc2_sqrt[i], &ss);
+    }
+}
+
+static inline void fused_elem(float *p, float g, float *m, float *v, float *vmax,
+                              const oracle_fused *h, const oracle_fused_model *fm)
+{
+    const double omb1 = 1.0 - h->beta1, omb2 = 1.0 - h->beta2;
+    float pp = *p;
+    if (h->weight_decay != 0.0) {
+        const double t = h->lr * h->weight_decay;
+        pp = fm->wd_fma ? (float)fma(-t, (double)pp, (double)pp)
+                        : (float)((double)pp - t * (double)pp);
+    }
+    const double dm = (double)*m, dg = (double)g, dvv = (double)*v;
+    float mm, vv;
+    switch (fm->m_mode) {
+    case 1: mm = (float)fma(h->beta1, dm, omb1 * dg); break;
+    case 2: mm = (float)fma(omb1, dg, h->beta1 * dm); break;
+    default: mm = (float)(h->beta1 * dm + omb1 * dg); break;
+    }
+    const double q = omb2 * dg;
+    switch (fm->v_mode) {
+    case 1: vv = (float)fma(h->beta2, dvv, q * dg); break;
+    case 2: vv = (float)fma(q, dg, h->beta2 * dvv); break;
+    default: vv = (float)(h->beta2 * dvv + q * dg); break;
+    }
+    /* amsgrad: ::max on the device is fmaxf (the number if one operand is NaN) */
+    const float dv = vmax ? (*vmax = fmaxf(*vmax, vv)) : vv;
+    const float d = (float)((double)(sqrtf(dv) / h->bc2_sqrt) + h->eps);
+    pp = pp - (h->step_size * mm) / d;
+    *p = pp; *m = mm; *v = vv;
+}
+
+void oracle_adamw_fused_f32(float *p, const float *g, float *m, float *v, float *vmax,
+                            int64_t n, const oracle_fused *h, const oracle_fused_model *fm,
+                            float grad_scale, int apply_scale)
+{
+    for (int64_t i = 0; i < n; ++i) {
+        float gi = g[i];
+        if (apply_scale) gi = gi * grad_scale;
+        gi = gi * h->grad_sign;
+        fused_elem(&p[i], gi, &m[i], &v[i], vmax ? &vmax[i] : NULL, h, fm);
+    }
+}
+
+void oracle_adamw_fused_bf16state(float *p, const float *g, uint16_t *m, uint16_t *v,
+                                  uint16_t *vmax, int64_t n, const oracle_fused *h,
+                                  const oracle_fused_model *fm, float grad_scale,
+                                  int apply_scale)
+{
+    for (int64_t i = 0; i < n; ++i) {
+        float gi = g[i];
+        if (apply_scale) gi = gi * grad_scale;
+        gi = gi * h->grad_sign;
+        float mm = oracle_bf16_to_f32(m[i]);
+        float vv = oracle_bf16_to_f32(v[i]);
+        float mx = vmax ? oracle_bf16_to_f32(vmax[i]) : 0.0f;
+        fused_elem(&p[i], gi, &mm, &vv, vmax ? &mx : NULL, h, fm);
+        m[i] = oracle_f32_to_bf16(mm);
+        v[i] = oracle_f32_to_bf16(vv);
+        if (vmax) vmax[i] = oracle_f32_to_bf16(mx);
+    }
+}
+
 void oracle_to_bf16(const float *x, uint16_t *out, int64_t n)
 {
     for (int64_t i = 0; i < n; ++i) out[i] = oracle_f32_to_bf16(x[i]);

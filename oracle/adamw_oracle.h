@@ -52,6 +52,29 @@ typedef struct oracle_capt {
     float grad_sign;
 } oracle_capt;
 
+/* torch's fused=True chain (ATen/native/hip/fused_adam_utils.cuh adam_math): which
+ * float64 `a*b + c*d` forms one fused multiply-add. */
+typedef struct oracle_fused_model {
+    int wd_fma;       /* 1: p - (lr*wd)*p as fma(-(lr*wd), p, p); 0: two roundings       */
+    int m_mode;       /* beta1*m + (1-beta1)*g: 0 = no fma, 1 = fma(beta1, m, (1-beta1)*g),
+                                                2 = fma(1-beta1, g, beta1*m)            */
+    int v_mode;       /* beta2*v + ((1-beta2)*g)*g: 0 = no fma, 1 = fma(beta2, v, .),
+                                                2 = fma((1-beta2)*g, g, beta2*v)        */
+} oracle_fused_model;
+
+/* Scalars of the fused chain: the float64 hyperparameters as _fused_adamw_ receives
+ * them and the per-step values it forms (oracle_fused_scalars). */
+typedef struct oracle_fused {
+    double lr;
+    double beta1;
+    double beta2;
+    double weight_decay;
+    double eps;
+    float step_size;       /* f32(lr / (double)bc1)                                      */
+    float bc2_sqrt;        /* f32(sqrt(1 - pow(beta2, step)))                           */
+    float grad_sign;       /* -1.0f when maximize, else 1.0f                             */
+} oracle_fused;
+
 uint16_t oracle_f32_to_bf16(float x);
 float oracle_bf16_to_f32(uint16_t h);
 
@@ -77,6 +100,23 @@ void oracle_adamw_capt_f32(float *p, const float *g, float *m, float *v, float *
 void oracle_adamw_capt_bf16state(float *p, const float *g, uint16_t *m, uint16_t *v,
                                  uint16_t *vmax, int64_t n, const oracle_capt *h,
                                  const oracle_opmodel *om, float grad_scale, int apply_scale);
+
+/* The fused=True chain's per-step values (libm pow in float64). */
+void oracle_fused_scalars(double lr, double beta1, double beta2, float step, float *bc1,
+                          float *bc2_sqrt, float *step_size);
+
+/* bc1 and bc2_sqrt of oracle_fused_scalars for n step counts. */
+void oracle_fused_scalars_many(double beta1, double beta2, const float *steps, int64_t n,
+                               float *bc1, float *bc2_sqrt);
+
+/* torch's fused=True chain, fp32 and bf16-stored moments. */
+void oracle_adamw_fused_f32(float *p, const float *g, float *m, float *v, float *vmax,
+                            int64_t n, const oracle_fused *h, const oracle_fused_model *fm,
+                            float grad_scale, int apply_scale);
+void oracle_adamw_fused_bf16state(float *p, const float *g, uint16_t *m, uint16_t *v,
+                                  uint16_t *vmax, int64_t n, const oracle_fused *h,
+                                  const oracle_fused_model *fm, float grad_scale,
+                                  int apply_scale);
 
 void oracle_to_bf16(const float *x, uint16_t *out, int64_t n);
 

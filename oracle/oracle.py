@@ -117,6 +117,42 @@ class Capt(ctypes.Structure):
     ]
 
 
+class FusedModel(ctypes.Structure):
+    """oracle_fused_model: which float64 ``a*b + c*d`` of the fused=True chain is one
+    fused multiply-add (adamw_oracle.h)."""
+
+    _fields_ = [("wd_fma", ctypes.c_int), ("m_mode", ctypes.c_int), ("v_mode", ctypes.c_int)]
+
+    def __repr__(self) -> str:  # pragma: no cover - debugging aid
+        return f"FusedModel(wd_fma={self.wd_fma}, m_mode={self.m_mode}, v_mode={self.v_mode})"
+
+
+# torch 2.10.0+rocm7.0 on gfx950, torch._fused_adamw_ (fused_adam_utils.cuh adam_math):
+# the compiler contracted each float64 sum with its left product, m = fma(beta1, m,
+# (1-beta1)*g) and v = fma(beta2, v, ((1-beta2)*g)*g), and p - (lr*wd)*p into one fma.
+# The m and v forms are pinned bit for bit by torch's GPU results on inputs where the
+# three candidates round apart (tests/golden/fused_golden.npz, written by
+# tests/golden/make_fused_golden.py from the cases fused_cases.c finds); the two forms
+# of the weight-decay op give the same fp32 result for every fp32 p at lr*wd = 3e-5
+# (none of 4e9 random draws separates them), so that field is not pinned by data.
+FUSED_TORCH_ROCM = FusedModel(wd_fma=1, m_mode=1, v_mode=1)
+
+
+class Fused(ctypes.Structure):
+    """oracle_fused: the fused=True chain's scalars (adamw_oracle.h)."""
+
+    _fields_ = [
+        ("lr", ctypes.c_double),
+        ("beta1", ctypes.c_double),
+        ("beta2", ctypes.c_double),
+        ("weight_decay", ctypes.c_double),
+        ("eps", ctypes.c_double),
+        ("step_size", ctypes.c_float),
+        ("bc2_sqrt", ctypes.c_float),
+        ("grad_sign", ctypes.c_float),
+    ]
+
+
 def _load(path: str = _LIB_PATH):
     if not os.path.exists(path):
         raise RuntimeError(f"oracle library missing: build it with `make -C {_HERE}`")
@@ -141,6 +177,21 @@ def _load(path: str = _LIB_PATH):
                                                 ctypes.POINTER(Capt), ctypes.POINTER(OpModel),
                                                 ctypes.c_float, ctypes.c_int]
     lib.oracle_adamw_capt_bf16state.restype = None
+    lib.oracle_fused_scalars.argtypes = [ctypes.c_double] * 3 + [ctypes.c_float, f32p, f32p,
+                                                                  f32p]
+    lib.oracle_fused_scalars.restype = None
+    lib.oracle_fused_scalars_many.argtypes = [ctypes.c_double, ctypes.c_double, f32p, i64,
+                                              f32p, f32p]
+    lib.oracle_fused_scalars_many.restype = None
+    lib.oracle_adamw_fused_f32.argtypes = [f32p, f32p, f32p, f32p, f32p, i64,
+                                           ctypes.POINTER(Fused), ctypes.POINTER(FusedModel),
+                                           ctypes.c_float, ctypes.c_int]
+    lib.oracle_adamw_fused_f32.restype = None
+    lib.oracle_adamw_fused_bf16state.argtypes = [f32p, f32p, u16p, u16p, u16p, i64,
+                                                 ctypes.POINTER(Fused),
+                                                 ctypes.POINTER(FusedModel), ctypes.c_float,
+                                                 ctypes.c_int]
+    lib.oracle_adamw_fused_bf16state.restype = None
     lib.oracle_to_bf16.argtypes = [f32p, u16p, i64]
     lib.oracle_to_bf16.restype = None
     lib.oracle_sumsq_f64.argtypes = [f32p, i64]
@@ -308,6 +359,64 @@ def adamw_step_capt_bf16state(p, g, m_bits, v_bits, *, lr, betas, eps, weight_de
                                       None if vmax_bits is None else _u16(vmax_bits), n,
                                       ctypes.byref(h), ctypes.byref(opmodel), scale,
                                       0 if grad_scale is None else 1)
+
+
+def fused_scalars(lr, beta1, beta2, step) -> tuple[float, float, float]:
+    """(bc1, bc2_sqrt, step_size) of the fused=True chain at step ``step`` (the fp32
+    count after its increment): float64 on the device in torch
+    (fused_adam_utils.cuh FusedAdamMathFunctor), each reaching adam_math as fp32.
+    libm's pow here; the device pow differs from it in the last float64 bit at some
+    steps, which the fp32 roundings absorb (a GPU test compares the two)."""
+    bc1, bc2s, ss = ctypes.c_float(), ctypes.c_float(), ctypes.c_float()
+    lib().oracle_fused_scalars(float(lr), float(beta1), float(beta2),
+                               float(np.float32(step)), ctypes.byref(bc1), ctypes.byref(bc2s),
+                               ctypes.byref(ss))
+    return bc1.value, bc2s.value, ss.value
+
+
+def fused_scalars_many(beta1, beta2, steps) -> tuple[np.ndarray, np.ndarray]:
+    """(bc1, bc2_sqrt) of ``fused_scalars`` for an array of fp32 step counts."""
+    steps = np.ascontiguousarray(steps, dtype=np.float32)
+    bc1 = np.empty_like(steps)
+    bc2s = np.empty_like(steps)
+    lib().oracle_fused_scalars_many(float(beta1), float(beta2), _f32(steps), steps.size,
+                                    _f32(bc1), _f32(bc2s))
+    return bc1, bc2s
+
+
+def fused_from_group(lr, beta1, beta2, eps, weight_decay, step, maximize=False) -> Fused:
+    """The fused chain's scalars: lr (a float, or a tensor lr's value as float64), the
+    betas, weight decay and eps as float64, the per-step values from ``fused_scalars``."""
+    _, bc2s, ss = fused_scalars(lr, beta1, beta2, step)
+    return Fused(lr=float(lr), beta1=float(beta1), beta2=float(beta2),
+                 weight_decay=float(weight_decay), eps=float(eps), step_size=ss,
+                 bc2_sqrt=bc2s, grad_sign=-1.0 if maximize else 1.0)
+
+
+def adamw_step_fused(p, g, m, v, *, lr, betas, eps, weight_decay, step, maximize=False,
+                     grad_scale=None, vmax=None, model=FUSED_TORCH_ROCM) -> None:
+    """One step of torch's fused=True chain on fp32 numpy arrays, in place."""
+    h = fused_from_group(lr, betas[0], betas[1], eps, weight_decay, step, maximize)
+    n = p.size
+    if not (g.size == m.size == v.size == n) or (vmax is not None and vmax.size != n):
+        raise ValueError("p, g, m, v sizes differ")
+    scale = 1.0 if grad_scale is None else float(np.float32(grad_scale))
+    lib().oracle_adamw_fused_f32(_f32(p), _f32(g), _f32(m), _f32(v),
+                                 None if vmax is None else _f32(vmax), n, ctypes.byref(h),
+                                 ctypes.byref(model), scale, 0 if grad_scale is None else 1)
+
+
+def adamw_step_fused_bf16state(p, g, m_bits, v_bits, *, lr, betas, eps, weight_decay, step,
+                               maximize=False, grad_scale=None, vmax_bits=None,
+                               model=FUSED_TORCH_ROCM) -> None:
+    """The fused=True chain with bf16-stored moments (uint16 bit arrays)."""
+    h = fused_from_group(lr, betas[0], betas[1], eps, weight_decay, step, maximize)
+    n = p.size
+    scale = 1.0 if grad_scale is None else float(np.float32(grad_scale))
+    lib().oracle_adamw_fused_bf16state(_f32(p), _f32(g), _u16(m_bits), _u16(v_bits),
+                                       None if vmax_bits is None else _u16(vmax_bits), n,
+                                       ctypes.byref(h), ctypes.byref(model), scale,
+                                       0 if grad_scale is None else 1)
 
 
 def to_bf16_bits(x: np.ndarray) -> np.ndarray:

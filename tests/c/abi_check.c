@@ -15,7 +15,11 @@
  *                     sets, bf16 moments and bf16 model copy: bit-exact;
  *                   - flat range with amsgrad: p, m, v, max_exp_avg_sq bit-exact;
  *                   - capturable chain through tables: two tensors at different
- *                     device step counts, a float lr, then a device lr: bit-exact.
+ *                     device step counts, a float lr, then a device lr: bit-exact;
+ *                   - torch's fused=True chain: a flat range with the clip, then
+ *                     tables with two sets (one without weight decay, with
+ *                     maximize), then tables at device step counts with a device
+ *                     lr: bit-exact.
  *
  * The per-step scalars are computed here as the header documents (float64 on
  * the host, as torch/optim/adam.py:529-536 does, then cast to fp32), with
@@ -226,6 +230,26 @@ static int cpu_checks(void)
     CHECK(mi_adamw_grad_norm_flat_noalloc(NULL, 10, 4096, 1.0f, fake_f, fake_f, NULL) ==
               MI_ADAMW_E_INVALID, "no-alloc norm without a gradient");
     CHECK(strstr(mi_adamw_strerror(MI_ADAMW_E_SCRATCH), "scratch") != NULL, "scratch error text");
+    mi_adamw_fused_hyper fh[1];
+    memset(fh, 0, sizeof fh);
+    CHECK(mi_adamw_step_fused_chain(NULL, fake, 1, 4096, fh, 1, NULL, NULL, NULL, 1.0f, 0, 0, 0,
+                                    NULL) == MI_ADAMW_E_INVALID, "fused chain without tables");
+    CHECK(mi_adamw_step_fused_chain(fake, fake, 1, 4096, fh, MI_ADAMW_MAX_HYPER + 1, NULL, NULL,
+                                    NULL, 1.0f, 0, 0, 0, NULL) == MI_ADAMW_E_INVALID,
+          "fused chain with too many sets");
+    CHECK(mi_adamw_step_fused_chain(fake, fake, 1, 4096, fh, 1, fake_f, NULL, NULL, 1.0f, 0, 0, 0,
+                                    NULL) == MI_ADAMW_E_INVALID,
+          "fused chain with device steps but no step index");
+    CHECK(mi_adamw_step_fused_chain(fake, fake, 1, 4096, fh, 1, NULL, NULL, NULL, NAN, 0, 0, 0,
+                                    NULL) == MI_ADAMW_E_INVALID, "fused chain with a NaN pre-scale");
+    CHECK(mi_adamw_step_fused_chain(fake, fake, 1, 4096, fh, 1, NULL, NULL, NULL, 1.0f, 0,
+                                    MI_ADAMW_F_CLIP, 0, NULL) == MI_ADAMW_E_INVALID,
+          "fused chain clip without a scale");
+    t.grad = (float *)(uintptr_t)(8192 + 4);
+    CHECK(mi_adamw_step_flat_fused_chain(&t, fh, NULL, 1.0f, 4096, MI_ADAMW_STATE_F32, 0, 0,
+                                         NULL) == MI_ADAMW_E_ALIGN, "misaligned fused flat range");
+    CHECK(mi_adamw_step_flat_fused_chain(&t, NULL, NULL, 1.0f, 4096, MI_ADAMW_STATE_F32, 0, 0,
+                                         NULL) == MI_ADAMW_E_INVALID, "fused flat without a set");
     printf("abi_check cpu: ok (%s)\n", mi_adamw_version());
     return 0;
 }
@@ -658,6 +682,154 @@ static void set_grads_case(void)
            "mi_adamw_set_grads: bit-exact\n");
 }
 
+/* One set of torch's fused=True chain (mi_adamw_fused_hyper) and the oracle's scalars for
+ * it: the float64 hyperparameters, and the per-step values formed from the step count with
+ * libm pow, as the library forms them on the host. */
+static void fused_set(mi_adamw_fused_hyper *h, oracle_fused *o, double lr, double b1, double b2,
+                      double wd, float step, int maximize)
+{
+    memset(h, 0, sizeof *h);
+    h->lr = lr;
+    h->beta1 = b1;
+    h->beta2 = b2;
+    h->weight_decay = wd;
+    h->eps = 1e-8;
+    h->step = step;
+    h->grad_sign = maximize ? -1.0f : 1.0f;
+    memset(o, 0, sizeof *o);
+    o->lr = lr;
+    o->beta1 = b1;
+    o->beta2 = b2;
+    o->weight_decay = wd;
+    o->eps = 1e-8;
+    float bc1;
+    oracle_fused_scalars(lr, b1, b2, step, &bc1, &o->bc2_sqrt, &o->step_size);
+    o->grad_sign = h->grad_sign;
+}
+
+/* torch's fused=True chain: tensor 0 as a flat range with the clip; both tensors through
+ * tables with two sets (the second without weight decay, with maximize); then the tables
+ * at device step counts (3 and 1) with a device lr, where beta1 = 0.5 and beta2 = 0.75 make
+ * pow exact at those steps on the host and the device alike. */
+static void fused_case(void)
+{
+    static const oracle_fused_model TORCH_FUSED = {1, 1, 1};
+    enum { NT = 2 };
+    const int64_t numel[NT] = {3 * 4096 + 1, 50003};
+    float *p[NT], *g[NT], *m[NT], *v[NT], *pr[NT], *mr[NT], *vr[NT];
+    void *dp[NT], *dg[NT], *dm[NT], *dv[NT];
+    mi_adamw_tensor rows[NT];
+    for (int k = 0; k < NT; ++k) {
+        const int64_t n = numel[k];
+        p[k] = malloc(n * 4); g[k] = malloc(n * 4); m[k] = malloc(n * 4); v[k] = malloc(n * 4);
+        pr[k] = malloc(n * 4); mr[k] = malloc(n * 4); vr[k] = malloc(n * 4);
+        CHECK(p[k] && g[k] && m[k] && v[k] && pr[k] && mr[k] && vr[k], "host allocation");
+        fill(p[k], n, 0.02f, 0);
+        fill(g[k], n, 2e-2f, 0);
+        fill(m[k], n, 1e-3f, 0);
+        fill(v[k], n, 1e-6f, 1);
+        memcpy(pr[k], p[k], n * 4);
+        memcpy(mr[k], m[k], n * 4);
+        memcpy(vr[k], v[k], n * 4);
+        dp[k] = dev_copy(p[k], n * 4);
+        dg[k] = dev_copy(g[k], n * 4);
+        dm[k] = dev_copy(m[k], n * 4);
+        dv[k] = dev_copy(v[k], n * 4);
+        memset(&rows[k], 0, sizeof rows[k]);
+        rows[k].param = dp[k];
+        rows[k].grad = dg[k];
+        rows[k].exp_avg = dm[k];
+        rows[k].exp_avg_sq = dv[k];
+        rows[k].numel = n;
+        rows[k].hyper = k;
+        rows[k].flags = MI_ADAMW_T_VEC;
+    }
+    {
+        const int64_t n = numel[0];
+        double *d_partials;
+        float *d_norm, *d_coef;
+        HIP(hipMalloc((void **)&d_partials, MI_ADAMW_MAX_NORM_BLOCKS * sizeof(double)));
+        HIP(hipMalloc((void **)&d_norm, 4));
+        HIP(hipMalloc((void **)&d_coef, 4));
+        int rc = mi_adamw_grad_norm_flat(dg[0], n, 4096, 1.0f, d_partials, d_norm, d_coef, NULL);
+        CHECK(rc == 0, "mi_adamw_grad_norm_flat: %s", mi_adamw_strerror(rc));
+        mi_adamw_fused_hyper h;
+        oracle_fused o;
+        fused_set(&h, &o, 3e-4, 0.9, 0.95, 0.1, 1000.0f, 0);
+        rc = mi_adamw_step_flat_fused_chain(&rows[0], &h, d_coef, 1.0f, 4096, MI_ADAMW_STATE_F32,
+                                            MI_ADAMW_F_CLIP, 0, NULL);
+        CHECK(rc == 0, "mi_adamw_step_flat_fused_chain: %s", mi_adamw_strerror(rc));
+        HIP(hipDeviceSynchronize());
+        float coef;
+        back(&coef, d_coef, 4);
+        CHECK(coef < 1.0f, "the clip triggers (coef %g)", coef);
+        oracle_adamw_fused_f32(pr[0], g[0], mr[0], vr[0], NULL, n, &o, &TORCH_FUSED, coef, 1);
+        back(p[0], dp[0], n * 4);
+        back(m[0], dm[0], n * 4);
+        back(v[0], dv[0], n * 4);
+        same_f32(p[0], pr[0], n, "param (fused chain, flat, clip)");
+        same_f32(m[0], mr[0], n, "exp_avg (fused chain, flat, clip)");
+        same_f32(v[0], vr[0], n, "exp_avg_sq (fused chain, flat, clip)");
+        HIP(hipFree(d_partials)); HIP(hipFree(d_norm)); HIP(hipFree(d_coef));
+    }
+    const int64_t n_chunks = mi_adamw_build_chunks(numel, NT, 4096, NULL, 0);
+    mi_adamw_chunk *chunks = malloc(n_chunks * sizeof *chunks);
+    CHECK(chunks && mi_adamw_build_chunks(numel, NT, 4096, chunks, n_chunks) == n_chunks,
+          "chunk table");
+    void *d_rows = dev_copy(rows, sizeof rows);
+    void *d_chunks = dev_copy(chunks, n_chunks * sizeof *chunks);
+    const float steps[3] = {9.0f, 1.0f, 3.0f};      /* the device step buffer */
+    const int32_t step_index[NT] = {2, 1};          /* row -> index into steps */
+    float *d_steps = dev_copy(steps, sizeof steps);
+    int32_t *d_index = dev_copy(step_index, sizeof step_index);
+    const float lr_dev = 2e-3f;
+    float *d_lr = dev_copy(&lr_dev, sizeof lr_dev);
+    for (int pass = 0; pass < 2; ++pass) {
+        mi_adamw_fused_hyper h[NT];
+        oracle_fused o[NT];
+        int rc;
+        if (pass == 0) {
+            fused_set(&h[0], &o[0], 3e-4, 0.9, 0.95, 0.1, 1001.0f, 0);
+            fused_set(&h[1], &o[1], 1e-3, 0.9, 0.999, 0.0, 7.0f, 1);
+            rc = mi_adamw_step_fused_chain(d_rows, d_chunks, n_chunks, 4096, h, NT, NULL, NULL,
+                                           NULL, 1.0f, MI_ADAMW_STATE_F32, 0, 0, NULL);
+        } else {
+            for (int k = 0; k < NT; ++k) {
+                fused_set(&h[k], &o[k], (double)lr_dev, 0.5, 0.75, 0.1,
+                          steps[step_index[k]], 0);
+                h[k].lr = 0.0;           /* the kernel reads the device lr */
+                h[k].lr_ptr = d_lr;
+                h[k].step = 0.0f;        /* and the device step counts */
+            }
+            rc = mi_adamw_step_fused_chain(d_rows, d_chunks, n_chunks, 4096, h, NT, d_steps,
+                                           d_index, NULL, 1.0f, MI_ADAMW_STATE_F32, 0, 0, NULL);
+        }
+        CHECK(rc == 0, "mi_adamw_step_fused_chain (pass %d): %s", pass, mi_adamw_strerror(rc));
+        HIP(hipDeviceSynchronize());
+        for (int k = 0; k < NT; ++k) {
+            const int64_t n = numel[k];
+            oracle_adamw_fused_f32(pr[k], g[k], mr[k], vr[k], NULL, n, &o[k], &TORCH_FUSED, 1.0f,
+                                   0);
+            back(p[k], dp[k], n * 4);
+            back(m[k], dm[k], n * 4);
+            back(v[k], dv[k], n * 4);
+            same_f32(p[k], pr[k], n, pass ? "param (fused chain, device steps)"
+                                          : "param (fused chain, tables)");
+            same_f32(m[k], mr[k], n, "exp_avg (fused chain)");
+            same_f32(v[k], vr[k], n, "exp_avg_sq (fused chain)");
+        }
+    }
+    for (int k = 0; k < NT; ++k) {
+        HIP(hipFree(dp[k])); HIP(hipFree(dg[k])); HIP(hipFree(dm[k])); HIP(hipFree(dv[k]));
+        free(p[k]); free(g[k]); free(m[k]); free(v[k]); free(pr[k]); free(mr[k]); free(vr[k]);
+    }
+    HIP(hipFree(d_rows)); HIP(hipFree(d_chunks)); HIP(hipFree(d_steps)); HIP(hipFree(d_index));
+    HIP(hipFree(d_lr));
+    free(chunks);
+    printf("abi_check gpu: fused=True chain, flat with clip, tables with two sets, device steps "
+           "and lr: bit-exact\n");
+}
+
 static int gpu_checks(void)
 {
     int count = 0;
@@ -670,6 +842,7 @@ static int gpu_checks(void)
     capt_case();
     split_case(3000000 + 96, 3);
     set_grads_case();
+    fused_case();
     printf("abi_check gpu: ok (%s)\n", mi_adamw_version());
     return 0;
 }

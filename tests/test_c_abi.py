@@ -3,8 +3,9 @@
 CPU: version, error text, the chunk-table helper and the argument rejections
 that return before any launch.  GPU: flat clip, tensor/chunk tables with bf16
 state and copy, amsgrad, the capturable chain, the clip split over slices with
-the data-parallel pre-scale (and the no-alloc norm), and gradient pointers
-patched into a table, each bit-exact against the C oracle.
+the data-parallel pre-scale (and the no-alloc norm), gradient pointers patched
+into a table, and torch's fused=True chain (flat with the clip, tables, device step
+counts and lr), each bit-exact against the C oracle.
 """
 from __future__ import annotations
 
@@ -32,4 +33,4 @@ def test_c_host_cpu_checks():
 @pytest.mark.gpu
 def test_c_host_gpu_parity_against_oracle():
     out = _run("gpu")
-    assert out.count("bit-exact") == 6 and "abi_check gpu: ok" in out
+    assert out.count("bit-exact") == 7 and "abi_check gpu: ok" in out

@@ -95,6 +95,24 @@ def test_capturable_group_constants():
         _capt_hyper(dict(g, lr=torch.tensor(6e-4, dtype=torch.float64)), torch.device("cpu"))
 
 
+def test_fused_chain_group_set():
+    """fused=True's per-group set: lr, betas, weight decay and eps as the float64 values
+    torch._fused_adamw_ receives, the step count as fp32, maximize as the sign; a CPU
+    tensor lr by value (the op's tensor-lr overload takes lr.item()); on a CPU device a
+    device lr is never formed."""
+    from mi_adamw.optimizer import _fused_hyper
+    g = dict(lr=6e-4, betas=(0.9, 0.999), eps=1e-8, weight_decay=0.1, maximize=True)
+    h = _fused_hyper(g, 1001.0, torch.device("cpu"))
+    assert (h.lr, h.beta1, h.beta2, h.weight_decay, h.eps) == (6e-4, 0.9, 0.999, 0.1, 1e-8)
+    assert h.step == 1001.0 and h.grad_sign == -1.0 and not h.lr_ptr
+    h = _fused_hyper(dict(g, lr=torch.tensor(6e-4), maximize=False), 3.0, torch.device("cpu"))
+    assert h.lr == float(np.float32(6e-4)) and h.grad_sign == 1.0 and not h.lr_ptr
+    h = _fused_hyper(dict(g, lr=torch.tensor(6e-4, dtype=torch.float64)), 3.0,
+                     torch.device("cpu"))
+    assert h.lr == 6e-4
+    assert ctypes.sizeof(h) == 56
+
+
 @pytest.mark.parametrize("view", ["strided", "transposed", "wrong_dtype"])
 def test_state_entries_are_made_dense_for_the_kernel(view):
     """A state entry put into the dict as a strided view, a transposed view or another

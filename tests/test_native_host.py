@@ -58,7 +58,7 @@ class _Setup:
             [True] * n_params, [p.grad.data_ptr() for p in self.params], False,
             (self.steps.data_ptr(), self.steps.numel()),
             (self.hyper_steps.ctypes.data, n_hyper), launch,
-            (4096, 0, 0, 0, True, 1.0, 1.0, 0, 0, 0, 123),
+            (4096, 0, 0, 0, True, 1.0, 1.0, 0, 0, 0, 123, False),
             (self.rows, self.steps, self.hyper_steps))
 
     def prepare(self, stream: int = 123) -> int:
@@ -177,12 +177,12 @@ def test_plan_refuses_bad_entries():
     with pytest.raises(ValueError):
         host.plan([p], [bad_state], [0], [0], [0], [True], [0], False, common["steps"],
                   common["hs"], (False, 0, 0, 1, 1, rows.ctypes.data, ctypes.addressof(row), 0),
-                  (4096, 0, 0, 0, False, 0.0, 1.0, 0, 0, 0, 0), ())
+                  (4096, 0, 0, 0, False, 0.0, 1.0, 0, 0, 0, 0, False), ())
     good_state = {"step": steps[0], "exp_avg": torch.zeros(4), "exp_avg_sq": torch.zeros(4)}
     with pytest.raises(ValueError):         # slot outside the step buffer
         host.plan([p], [good_state], [5], [0], [0], [True], [0], False, common["steps"],
                   common["hs"], (False, 0, 0, 1, 1, rows.ctypes.data, ctypes.addressof(row), 0),
-                  (4096, 0, 0, 0, False, 0.0, 1.0, 0, 0, 0, 0), ())
+                  (4096, 0, 0, 0, False, 0.0, 1.0, 0, 0, 0, 0, False), ())
 
 
 _SET_GRADS = ctypes.CFUNCTYPE(ctypes.c_int, ctypes.c_void_p, ctypes.c_int32, ctypes.c_int32,
