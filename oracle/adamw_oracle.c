@@ -23,6 +23,10 @@
  *       adam.py:499-502  step_size = lr / bc1, neg = -step_size, bc2_sqrt = sqrt(bc2)
  *       adam.py:520-522  d = sqrt(v) / (bc2_sqrt * neg) + eps / neg
  *       adam.py:527      p = p + m / d                                  (addcdiv_)
+ *   - torch/optim/adam.py:803-895  the fused=True path (_fused_adam ->
+ *     torch._fused_adamw_), per element adam_math of
+ *     ATen/native/hip/fused_adam_utils.cuh: float64 scalars and moment sums, one
+ *     rounding to fp32 each (see oracle_fused_scalars below).
  *   - torch/include/ATen/native/Lerp.h:21-35  the two-branch lerp formula.
  *   - torch/nn/utils/clip_grad.py:50-117,121-183  global L2 norm, then
  *     coef = clamp(max_norm * reciprocal(norm + 1e-6), max=1), g *= coef.

@@ -17,6 +17,11 @@ It restates, in NumPy plus the C kernels of ``adamw_oracle.c``:
   same loop with ``capturable=True`` (``adam.py:480-527``): the per-step values
   as fp32 0-d tensor ops, then ``p + m / (sqrt(v) / (sqrt(bc2) * -step_size) +
   eps / -step_size)``.
+* ``fused_scalars`` / ``adamw_step_fused`` / ``adamw_step_fused_bf16state`` -- torch's
+  ``fused=True`` chain (``adam.py:803-895`` -> ``torch._fused_adamw_``, per element
+  ``adam_math`` of ``ATen/native/hip/fused_adam_utils.cuh``): float64 hyperparameters,
+  m, v and the decayed p formed in float64 and rounded once, per-step values formed
+  in float64 and handed over as fp32.
 * ``total_norm`` / ``clip_coef`` -- ``torch/nn/utils/clip_grad.py:50-117``
   (global L2 norm over all gradients) and ``:165-169`` (the clamped
   coefficient), the clip mini-megatron defines at ``config.py:16``
@@ -39,6 +44,14 @@ How each function is pinned (none of it is trusted on its own):
   the MI355X (a GPU test, with torch's own per-step values), and on the CPU by
   closed forms (step 1: ``bc1 = 1 - beta1``; lr 0 leaves p unchanged) and the
   mutation tests.
+* The fused=True chain: torch runs it only on the GPU (its CPU kernel is other
+  arithmetic), so fixtures written by torch's own GPU kernel
+  (``tests/golden/make_fused_golden.py``) pin it bit for bit on the CPU: whole chains
+  over the options, inputs on which the candidate fused multiply-add forms round apart
+  (found by ``tests/golden/fused_cases.c``; each other form is rejected), and per-step
+  values at (lr, step) where their candidate forms round apart.  Closed forms (lr = 0,
+  g = 0, the first step), a float64 bound, agreement with the default chain and the
+  mutation tests pin it further; on the GPU it is compared with torch directly.
 * The bf16 paths: a brute-force round-to-nearest-even check of
   ``oracle_f32_to_bf16`` over every rounding boundary class, and torch's own
   ``Tensor.to(torch.bfloat16)`` on the same values.

@@ -14,6 +14,11 @@
   result (a dropped term, a wrong sign or a swapped operand fails it).
 * bf16 rounding against torch's own Tensor.to(torch.bfloat16) over every
   rounding-boundary class.
+* torch's fused=True chain (oracle.adamw_step_fused): golden fixtures written by
+  torch's own GPU kernel (tests/golden/make_fused_golden.py), including inputs on
+  which the candidate fused multiply-add forms round apart (each other form is
+  rejected by them); closed forms (lr = 0, g = 0, the first step); a float64 bound;
+  and its agreement with the default chain to a few ulp.
 """
 from __future__ import annotations
 
@@ -367,3 +372,162 @@ def test_oracle_is_deterministic():
         runs.append((p, m, v))
     for a, b in zip(*runs):
         assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+
+
+# ---------------------------------------------------------------------------
+# torch's fused=True chain (torch._fused_adamw_), pinned by its own GPU results
+
+FUSED_GOLDEN = os.path.join(os.path.dirname(__file__), "golden", "fused_golden.npz")
+FUSED_HP = dict(lr=3e-4, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.1)
+# the one-step cases of make_fused_golden.py: name -> overrides of FUSED_HP and options
+FUSED_RUNS = {
+    "step1": {}, "betas_0.9_0.999": dict(betas=(0.9, 0.999)), "beta1_0.3": dict(betas=(0.3, 0.95)),
+    "mid": {}, "maximize": dict(maximize=True), "no_wd": dict(weight_decay=0.0),
+    "amsgrad": {}, "lr_device": {}, "late": {}, "lr0": dict(lr=0.0), "tiny_moments": {},
+}
+
+
+@pytest.fixture(scope="module")
+def fused_gold():
+    with np.load(FUSED_GOLDEN, allow_pickle=False) as z:
+        return {k: z[k] for k in z.files}
+
+
+@pytest.mark.parametrize("name", sorted(FUSED_RUNS))
+def test_fused_chain_matches_torch_gpu_golden(fused_gold, name):
+    gd = fused_gold
+    kw = dict(FUSED_HP)
+    kw.update({k: v for k, v in FUSED_RUNS[name].items() if k != "maximize"})
+    if f"run_{name}_lr" in gd:
+        kw["lr"] = float(gd[f"run_{name}_lr"])     # a device fp32 lr, read as float64
+    p, g, m, v = (gd[f"run_{name}_{k}_in"].copy() for k in "pgmv")
+    x = gd[f"run_{name}_x_in"].copy() if f"run_{name}_x_in" in gd else None
+    O.adamw_step_fused(p, g, m, v, step=float(gd[f"run_{name}_step"]), vmax=x,
+                       maximize=FUSED_RUNS[name].get("maximize", False), **kw)
+    for k, a in (("p", p), ("m", m), ("v", v)) + ((("x", x),) if x is not None else ()):
+        assert O.max_ulp(a, gd[f"run_{name}_{k}_out"])[0] == 0, k
+
+
+def test_fused_chain_three_chained_steps_golden(fused_gold):
+    gd = fused_gold
+    p, m, v = (gd[f"chain_{k}_in"].copy() for k in "pmv")
+    for k in range(3):
+        O.adamw_step_fused(p, gd["chain_g"][k].copy(), m, v, step=998 + k, **FUSED_HP)
+    for k, a in (("p", p), ("m", m), ("v", v)):
+        assert O.max_ulp(a, gd[f"chain_{k}_out"])[0] == 0, k
+
+
+def test_fused_per_step_values_golden(fused_gold):
+    """At (lr, step, betas) where f32(lr / f32(bc1)) and f32(lr / bc1) differ, and where
+    f32(sqrt(bc2)) and sqrtf(f32(bc2)) differ, torch's parameter after one step from 0
+    (no gradient, no weight decay: p is the update) selects the oracle's forms."""
+    gd = fused_gold
+    for (lr, step, b1, b2), want in zip(gd["scalar_cases"], gd["scalar_p_out"]):
+        p = np.zeros(8, np.float32)
+        m = np.full(8, 0.01, np.float32)
+        v = np.full(8, 1e-4, np.float32)
+        O.adamw_step_fused(p, np.zeros(8, np.float32), m, v, lr=float(lr), betas=(b1, b2),
+                           eps=1e-8, weight_decay=0.0, step=float(step))
+        assert np.array_equal(p.view(np.uint32), want.view(np.uint32)), (lr, step, b1, b2)
+
+
+def _fused_cases(gd, kind, model):
+    x, g = gd[f"case_{kind}_in"].copy(), gd[f"case_{kind}_g"].copy()
+    n = x.size
+    p = np.full(n, 0.01, np.float32)
+    z = np.zeros(n, np.float32)
+    m, v = (x, z.copy()) if kind == "m" else (z.copy(), x)
+    O.adamw_step_fused(p, g, m, v, step=1000, model=model, **FUSED_HP)
+    return (m if kind == "m" else v), gd[f"case_{kind}_out"]
+
+
+def test_fused_contraction_forms_are_pinned(fused_gold):
+    """On the inputs where the forms round apart, torch's kernel selects the left-product
+    fused multiply-add for both moments; the unfused and the right-product forms each
+    disagree with it on at least one input."""
+    pinned = O.FUSED_TORCH_ROCM
+    for kind in ("m", "v"):
+        got, want = _fused_cases(fused_gold, kind, pinned)
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), kind
+        for mode in (0, 2):
+            other = O.FusedModel(wd_fma=1, m_mode=mode if kind == "m" else 1,
+                                 v_mode=mode if kind == "v" else 1)
+            got, want = _fused_cases(fused_gold, kind, other)
+            assert not np.array_equal(got.view(np.uint32), want.view(np.uint32)), (kind, mode)
+
+
+def test_fused_lr_zero_and_zero_grad_closed_forms():
+    """lr = 0 leaves p bitwise unchanged (lr*wd = 0 and step_size = 0); g = 0 multiplies m
+    and v by beta1 and beta2 in float64 with one rounding to fp32."""
+    n = 4096
+    p0, m0, v0 = _rand(n, 21, 0.02), _rand(n, 22, 1e-3), np.abs(_rand(n, 23, 1e-6))
+    p, m, v = p0.copy(), m0.copy(), v0.copy()
+    O.adamw_step_fused(p, np.zeros(n, np.float32), m, v, lr=0.0, betas=(0.9, 0.95), eps=1e-8,
+                       weight_decay=0.1, step=1000)
+    assert np.array_equal(p.view(np.uint32), p0.view(np.uint32))
+    assert np.array_equal(m, (m0.astype(np.float64) * 0.9).astype(np.float32))
+    assert np.array_equal(v, (v0.astype(np.float64) * 0.95).astype(np.float32))
+
+
+def test_fused_first_step_closed_form():
+    """From zero state at step 1: m = f32((1 - beta1) g) with 1 - beta1 in float64,
+    v = f32((1 - beta2) g^2), and the bias-corrected update is lr * sign(g) up to eps."""
+    n = 8192
+    p0, g = _rand(n, 24, 0.02), _rand(n, 25, 1e-3)
+    p, m, v = p0.copy(), np.zeros(n, np.float32), np.zeros(n, np.float32)
+    lr, wd = 3e-4, 0.1
+    O.adamw_step_fused(p, g, m, v, lr=lr, betas=(0.9, 0.95), eps=1e-8, weight_decay=wd, step=1)
+    g64 = g.astype(np.float64)
+    assert np.array_equal(m, ((1 - 0.9) * g64).astype(np.float32))
+    assert O.max_ulp(v, ((1 - 0.95) * g64 * g64).astype(np.float32))[0] <= 1
+    expect = p0.astype(np.float64) * (1 - lr * wd) - lr * g64 / (np.abs(g64) + 1e-8)
+    assert np.all(np.abs(p - expect) <= 2.0 ** -21 * (np.abs(expect) + lr))
+
+
+@pytest.mark.parametrize("step,b1,b2", [(1, 0.9, 0.95), (7, 0.9, 0.999), (1000, 0.9, 0.95),
+                                        (3, 0.3, 0.95)])
+def test_fused_float64_bound(step, b1, b2):
+    """The fused chain against the whole step in float64: m and v within two fp32
+    roundings, p within the rounding of p plus a few roundings of the update."""
+    n = 1000
+    p0, g = _rand(n, 26, 0.02), _rand(n, 27, 1e-3)
+    m0, v0 = _rand(n, 28, 1e-3), np.abs(_rand(n, 29, 1e-6))
+    p, m, v = p0.copy(), m0.copy(), v0.copy()
+    lr, wd, eps = 6e-4, 0.1, 1e-8
+    O.adamw_step_fused(p, g.copy(), m, v, lr=lr, betas=(b1, b2), eps=eps, weight_decay=wd,
+                       step=step)
+    p64, m64, v64 = _float64_chain(p0, g, m0, v0, lr, b1, b2, eps, wd, step)
+    assert np.max(np.abs(m - m64) / (np.abs(m64) + np.abs(m0) + 1e-30)) <= 2 * 2.0 ** -24
+    assert np.max(np.abs(v - v64) / v64) <= 2 * 2.0 ** -24
+    ss = lr / (1 - b1 ** step)
+    d64 = np.sqrt(v64) / np.sqrt(1 - b2 ** step) + eps
+    bound = (np.abs(p64) * 2.0 ** -23
+             + 2.0 ** -20 * ss * (np.abs(m0) + np.abs(g) + np.abs(m64)) / d64)
+    assert np.all(np.abs(p - p64) <= bound)
+
+
+@pytest.mark.parametrize("amsgrad", [False, True])
+def test_fused_chain_agrees_with_the_default_chain(amsgrad):
+    """Both chains round the same real step: m within a few roundings of its operands'
+    scale (0.9 m + 0.1 g may cancel), v within 2 ulp, p within a few roundings of the
+    update (the running maximum of v taken in both)."""
+    n = 4096
+    p0, g = _rand(n, 30, 0.02), _rand(n, 31, 1e-3)
+    m0, v0 = _rand(n, 32, 1e-3), np.abs(_rand(n, 33, 1e-6))
+    x0 = (v0 * np.float32(1.5)).astype(np.float32)
+    x0[::2] = 0
+    out = []
+    for fn in (O.adamw_step_fused, O.adamw_step):
+        p, m, v, x = p0.copy(), m0.copy(), v0.copy(), x0.copy()
+        fn(p, g.copy(), m, v, vmax=x if amsgrad else None, step=1000, **FUSED_HP)
+        out.append((p, m, v, x))
+    (pf, mf, vf, xf), (pd, md, vd, xd) = out
+    assert np.all(np.abs(mf.astype(np.float64) - md) <= 2.0 ** -22 * (np.abs(m0) + np.abs(g)))
+    assert O.max_ulp(vf, vd)[0] <= 2
+    if amsgrad:
+        assert O.max_ulp(xf, xd)[0] <= 2
+    ss = FUSED_HP["lr"] / (1 - 0.9 ** 1000)
+    upd = ss * np.abs(md.astype(np.float64)) / (np.sqrt(np.maximum(vd, xd if amsgrad else vd))
+                                                 + 1e-8)
+    assert np.all(np.abs(pf.astype(np.float64) - pd) <= 2.0 ** -22 * np.abs(pd) + 2.0 ** -20 *
+                  (upd + ss * (np.abs(m0) + np.abs(g)) / (np.sqrt(vd) + 1e-8)))

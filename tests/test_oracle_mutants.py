@@ -5,8 +5,9 @@ Each case compiles a copy of oracle/adamw_oracle.c with one plausible mistake
 clamp, truncation instead of rounding, an off-by-one), points the oracle's
 wrappers at it, and runs the pinning checks of tests/test_oracle.py: golden
 fixtures from torch, closed forms, the float64 bound, bf16 rounding against
-torch, and the capturable chain's closed forms and its agreement with the
-default chain.  At least one check must fail for every mutant; the unmodified
+torch, the capturable chain's closed forms and its agreement with the default
+chain, and the fused=True chain's GPU fixtures, contraction forms, closed forms,
+float64 bound and agreement with the default chain.  At least one check must fail for every mutant; the unmodified
 source compiled the same way must pass them all.
 """
 from __future__ import annotations
@@ -50,10 +51,25 @@ MUTANTS = {
     "capt_no_bias_correction1": ("float step_size = lr_is_tensor ? lr / bc1 : (1.0f / bc1) * lr;",
                                  "float step_size = lr;"),
     "capt_eps_not_scaled": ("*den_add = (1.0f / neg) * eps;", "*den_add = eps;"),
+    # torch's fused=True chain
+    "fused_m_in_fp32": ("case 1: mm = (float)fma(h->beta1, dm, omb1 * dg); break;",
+                        "case 1: mm = fmaf((float)h->beta1, *m, (float)omb1 * g); break;"),
+    "fused_v_beta1": ("case 1: vv = (float)fma(h->beta2, dvv, q * dg); break;",
+                      "case 1: vv = (float)fma(h->beta1, dvv, q * dg); break;"),
+    "fused_eps_in_fp32": ("const float d = (float)((double)(sqrtf(dv) / h->bc2_sqrt) + h->eps);",
+                          "const float d = sqrtf(dv) / h->bc2_sqrt + (float)h->eps;"),
+    "fused_no_weight_decay": ("    if (h->weight_decay != 0.0) {\n        const double t",
+                              "    if (0) {\n        const double t"),
+    "fused_bc1_not_rounded": ("*step_size = (float)(lr / (double)*bc1);",
+                              "*step_size = (float)(lr / b1c);"),
+    "fused_amsgrad_max_unused": ("const float dv = vmax ? (*vmax = fmaxf(*vmax, vv)) : vv;",
+                                 "const float dv = vmax ? (*vmax = fmaxf(*vmax, vv), vv) : vv;"),
+    "fused_update_sign": ("pp = pp - (h->step_size * mm) / d;", "pp = pp + (h->step_size * mm) / d;"),
+    "fused_bc2_sqrt_in_fp32": ("*bc2_sqrt = (float)sqrt(b2c);", "*bc2_sqrt = sqrtf((float)b2c);"),
 }
 
 
-def _checks(gold):
+def _checks(gold, fused_gold):
     """Every pinning check of test_oracle, as (name, callable) pairs."""
     out = []
     for name in T.GOLDEN_CASES:
@@ -76,6 +92,22 @@ def _checks(gold):
     out.append(("sumsq_brute_force", T.test_sumsq_float64_brute_force))
     out.append(("bf16_vs_torch", T.test_bf16_rounding_matches_torch))
     out.append(("bf16_state", T.test_bf16state_with_exact_states_equals_fp32_then_round))
+    for name in T.FUSED_RUNS:
+        out.append((f"fused_golden:{name}",
+                    lambda n=name: T.test_fused_chain_matches_torch_gpu_golden(fused_gold, n)))
+    out.append(("fused_golden:chain",
+                lambda: T.test_fused_chain_three_chained_steps_golden(fused_gold)))
+    out.append(("fused_forms", lambda: T.test_fused_contraction_forms_are_pinned(fused_gold)))
+    out.append(("fused_per_step_values",
+                lambda: T.test_fused_per_step_values_golden(fused_gold)))
+    out.append(("fused_closed_forms", T.test_fused_lr_zero_and_zero_grad_closed_forms))
+    out.append(("fused_first_step", T.test_fused_first_step_closed_form))
+    for step, b1, b2 in ((1, 0.9, 0.95), (7, 0.9, 0.999), (1000, 0.9, 0.95), (3, 0.3, 0.95)):
+        out.append(("fused_float64_bound",
+                    lambda s=step, a=b1, b=b2: T.test_fused_float64_bound(s, a, b)))
+    for ams in (False, True):
+        out.append(("fused_vs_default",
+                    lambda a=ams: T.test_fused_chain_agrees_with_the_default_chain(a)))
     return out
 
 
@@ -90,11 +122,11 @@ def _build(src_text: str, out_dir: str, name: str) -> str:
     return so_path
 
 
-def _failures(gold, so_path: str) -> list[str]:
+def _failures(gold, fused_gold, so_path: str) -> list[str]:
     O.use_library(so_path)
     failed = []
     try:
-        for name, check in _checks(gold):
+        for name, check in _checks(gold, fused_gold):
             try:
                 check()
             except AssertionError:
@@ -110,17 +142,23 @@ def gold():
         return {k: z[k] for k in z.files}
 
 
-def test_unmodified_copy_passes_every_check(gold, tmp_path):
+@pytest.fixture(scope="module")
+def fused_gold():
+    with np.load(T.FUSED_GOLDEN, allow_pickle=False) as z:
+        return {k: z[k] for k in z.files}
+
+
+def test_unmodified_copy_passes_every_check(gold, fused_gold, tmp_path):
     so = _build(open(SOURCE).read(), str(tmp_path), "oracle_copy")
-    assert _failures(gold, so) == []
+    assert _failures(gold, fused_gold, so) == []
 
 
 @pytest.mark.parametrize("mutant", sorted(MUTANTS))
-def test_mutant_is_caught(gold, tmp_path, mutant):
+def test_mutant_is_caught(gold, fused_gold, tmp_path, mutant):
     old, new = MUTANTS[mutant]
     src = open(SOURCE).read()
     assert src.count(old) == 1, f"mutation site for {mutant} not found exactly once"
     so = _build(src.replace(old, new), str(tmp_path), f"oracle_{mutant}")
-    failed = _failures(gold, so)
+    failed = _failures(gold, fused_gold, so)
     print(f"{mutant}: caught by {failed}")
     assert failed, f"planted mistake {mutant} passed every pinning check"
