@@ -49,21 +49,28 @@ import torch  # noqa: E402
 PEAK_HBM_GBS = 8000.0   # MI355X published HBM3E bandwidth
 METRIC = "AdamW step ms + achieved HBM GB/s (% of MI355X peak), 125M→6.7B"
 
-# name: (shape, clip, state dtype, bf16 copy, flat buffer, stored step, grad std)
+# name: (shape, clip, state dtype, bf16 copy, flat buffer, stored step, grad std,
+#        torch's fused=True chain)
 CONFIGS = {
-    "125m-step1": ("gpt-125m", False, "fp32", False, False, 0, 1e-3),
-    "125m-clip": ("gpt-125m", True, "fp32", False, False, 1000, 1e-2),
-    "350m-master-clip-copy": ("gpt-350m", True, "fp32", True, False, 1000, 1e-3),
-    "1.3b-bf16state-copy": ("gpt-1.3b", False, "bf16", True, False, 1000, 1e-3),
-    "1.3b-bf16state-copy-clip": ("gpt-1.3b", True, "bf16", True, False, 1000, 1e-3),
-    "1.3b-bf16state-copy-clip-flat": ("gpt-1.3b", True, "bf16", True, True, 1000, 1e-3),
-    "6.7b-flat-clip-copy": ("gpt-6.7b", True, "fp32", True, True, 1000, 1e-3),
+    "125m-step1": ("gpt-125m", False, "fp32", False, False, 0, 1e-3, False),
+    "125m-clip": ("gpt-125m", True, "fp32", False, False, 1000, 1e-2, False),
+    "350m-master-clip-copy": ("gpt-350m", True, "fp32", True, False, 1000, 1e-3, False),
+    "1.3b-bf16state-copy": ("gpt-1.3b", False, "bf16", True, False, 1000, 1e-3, False),
+    "1.3b-bf16state-copy-clip": ("gpt-1.3b", True, "bf16", True, False, 1000, 1e-3, False),
+    "1.3b-bf16state-copy-clip-flat": ("gpt-1.3b", True, "bf16", True, True, 1000, 1e-3, False),
+    "6.7b-flat-clip-copy": ("gpt-6.7b", True, "fp32", True, True, 1000, 1e-3, False),
+    # the same steps in torch's fused=True chain (the reference's --fused)
+    "125m-clip-fused-chain": ("gpt-125m", True, "fp32", False, False, 1000, 1e-2, True),
+    "1.3b-bf16state-copy-clip-fused-chain": ("gpt-1.3b", True, "bf16", True, False, 1000, 1e-3,
+                                             True),
+    "6.7b-flat-clip-copy-fused-chain": ("gpt-6.7b", True, "fp32", True, True, 1000, 1e-3, True),
 }
 # The headline is the largest configuration that fits one GPU, the 6.7B flat clip + copy
 # step; the other configurations are timed in the same run, as rows of `sweep`.
 DEFAULT_CONFIG = "6.7b-flat-clip-copy"
 DEFAULT_SWEEP = ("1.3b-bf16state-copy-clip", "1.3b-bf16state-copy-clip-flat",
-                 "1.3b-bf16state-copy", "350m-master-clip-copy", "125m-clip", "125m-step1")
+                 "1.3b-bf16state-copy", "350m-master-clip-copy", "125m-clip", "125m-step1",
+                 "1.3b-bf16state-copy-clip-fused-chain", "125m-clip-fused-chain")
 # CPU baselines: the clip configurations of the workload list (125M, 350M, 1.3B, 6.7B)
 DEFAULT_CPU = ("6.7b-flat-clip-copy", "1.3b-bf16state-copy-clip", "350m-master-clip-copy",
                "125m-clip")
@@ -92,7 +99,7 @@ def build_set(name: str, device, capturable: bool = False, write_grads: bool = F
     import mi_adamw
     from mi_adamw.workloads import SHAPES, init_kind
 
-    shape_name, clip, state, copy, flat, start_step, gstd = CONFIGS[name]
+    shape_name, clip, state, copy, flat, start_step, gstd, chain = CONFIGS[name]
     shape = SHAPES[shape_name]
     params = []
     for i, (tname, shp) in enumerate(shape.tensors()):
@@ -107,7 +114,7 @@ def build_set(name: str, device, capturable: bool = False, write_grads: bool = F
         params.append(torch.nn.Parameter(t))
     opt = mi_adamw.FusedAdamW(params, **HP, max_grad_norm=1.0 if clip else None,
                               state_dtype=torch.bfloat16 if state == "bf16" else torch.float32,
-                              bf16_copy=copy, flat_buffer=flat, fused=False,
+                              bf16_copy=copy, flat_buffer=flat, fused=chain,
                               capturable=capturable, clip_write_grads=write_grads)
     for i, p in enumerate(params):
         g = torch.Generator(device)
@@ -189,7 +196,7 @@ def host_cpu() -> dict:
 def torch_gpu_rows(name: str, device, steps: int = 10, warmup: int = 3) -> dict:
     """torch's own GPU AdamW on the same set: per-tensor (foreach=False) and fused=True."""
     from mi_adamw.workloads import SHAPES
-    shape_name, clip, state, copy, flat, start_step, gstd = CONFIGS[name]
+    shape_name, clip, state, copy, flat, start_step, gstd, chain = CONFIGS[name]
     out = {}
     for label, kw in (("foreach_false", dict(foreach=False)), ("fused", dict(fused=True))):
         params = [torch.nn.Parameter(torch.randn(s, device=device).mul_(0.02))
@@ -251,7 +258,7 @@ def cpu_baseline(name: str, batch_params: int = 1 << 29, warmup: int = 2,
     fp32 moments and writes no bf16 copy: it moves 32 B per parameter with the clip,
     28 without, and ``value`` counts those bytes."""
     from mi_adamw.workloads import SHAPES
-    shape_name, clip, state, copy, flat, start_step, gstd = CONFIGS[name]
+    shape_name, clip, state, copy, flat, start_step, gstd, chain = CONFIGS[name]
     tensors = [s for _, s in SHAPES[shape_name].tensors()]
     numels = [math.prod(s) for s in tensors]
     info = host_cpu()
@@ -419,11 +426,13 @@ def load_traffic(name: str):
 
 
 def describe(name: str) -> str:
-    shape_name, clip, state, copy, flat, start_step, gstd = CONFIGS[name]
+    shape_name, clip, state, copy, flat, start_step, gstd, chain = CONFIGS[name]
     parts = [f"{shape_name}", "flat buffer" if flat else "per-tensor tables",
              "bf16 moments" if state == "bf16" else "fp32 moments"]
     if copy:
         parts.append("bf16 copy")
+    if chain:
+        parts.append("torch's fused=True chain")
     return ", ".join(parts) + (": fused clip + AdamW step" if clip else ": AdamW step")
 
 
@@ -514,7 +523,7 @@ def run_config(name: str, steps: int, warmup: int, device, with_context: bool,
                capturable: bool = False, write_grads: bool = False,
                range_world: int = 0, trials: int = 0, ab: bool = False,
                passes: int = 1) -> dict:
-    shape_name, clip, state, copy, flat, start_step, gstd = CONFIGS[name]
+    shape_name, clip, state, copy, flat, start_step, gstd, chain = CONFIGS[name]
     log(f"[bench] {name}: building {shape_name} set" + (" (capturable)" if capturable else "")
         + (" (clipped grads written back)" if write_grads else ""))
     params, opt, n, n_tensors = build_set(name, device, capturable, write_grads)
@@ -727,7 +736,7 @@ def main() -> int:
         torch.cuda.synchronize()
         del src, dst
     head = results[args.config]
-    shape_name, clip, state, copy, flat, start_step, gstd = CONFIGS[args.config]
+    shape_name, clip, state, copy, flat, start_step, gstd, chain = CONFIGS[args.config]
     line = {
         "metric": METRIC,
         "value": round(head["gbs"], 2),

@@ -522,12 +522,21 @@ def test_bench_bytes_per_parameter():
     spec.loader.exec_module(bench)
     expected = {"125m-step1": 28, "125m-clip": 32, "350m-master-clip-copy": 34,
                 "1.3b-bf16state-copy": 22, "1.3b-bf16state-copy-clip": 26,
-                "1.3b-bf16state-copy-clip-flat": 26, "6.7b-flat-clip-copy": 34}
+                "1.3b-bf16state-copy-clip-flat": 26, "6.7b-flat-clip-copy": 34,
+                "125m-clip-fused-chain": 32, "1.3b-bf16state-copy-clip-fused-chain": 26,
+                "6.7b-flat-clip-copy-fused-chain": 34}
     assert set(expected) == set(bench.CONFIGS)
-    # the headline is the largest configuration, and every other one is in the default sweep
+    # the headline is the largest configuration; every other one is in the default sweep
+    # but the headline's set in the fused=True chain, which only --sweep asks for
     assert bench.DEFAULT_CONFIG == "6.7b-flat-clip-copy"
-    assert set(bench.DEFAULT_SWEEP) | {bench.DEFAULT_CONFIG} == set(bench.CONFIGS)
+    assert (set(bench.CONFIGS) - set(bench.DEFAULT_SWEEP) - {bench.DEFAULT_CONFIG}
+            == {"6.7b-flat-clip-copy-fused-chain"})
     assert set(bench.DEFAULT_CPU) <= set(bench.CONFIGS)
+    # a fused-chain configuration is its base configuration in the other chain
+    for name, cfg in bench.CONFIGS.items():
+        assert cfg[-1] == name.endswith("-fused-chain")
+        if cfg[-1]:
+            assert bench.CONFIGS[name[:-len("-fused-chain")]][:-1] == cfg[:-1]
     for name, total in expected.items():
         _, clip, state, copy, *_ = bench.CONFIGS[name]
         step, update = bench.bytes_per_param(clip, state, copy)
@@ -550,7 +559,8 @@ def test_bench_cpu_host_record_and_streamed_baseline():
     try:
         SHAPES["gpt-tiny"] = GPTShape("gpt-tiny", layers=2, hidden=64, heads=2, ffn=256,
                                       vocab=1000, positions=128)
-        bench.CONFIGS["tiny-clip"] = ("gpt-tiny", True, "fp32", False, False, 1000, 1e-2)
+        bench.CONFIGS["tiny-clip"] = ("gpt-tiny", True, "fp32", False, False, 1000, 1e-2,
+                                      False)
         n = SHAPES["gpt-tiny"].numel()
         cb = bench.cpu_baseline("tiny-clip", batch_params=70_000, warmup=1, reps=2)
     finally:
