@@ -37,6 +37,7 @@ from typing import Any
 import numpy as np
 import torch
 from torch.optim import Optimizer
+from torch.optim.optimizer import _device_dtype_check_for_fused
 
 from . import _lib
 from .flat import FlatLayout
@@ -839,6 +840,10 @@ class FusedAdamW(Optimizer):
                 st = rec.st = self.state[rec.p]
             if len(st) == 0:
                 self._check_param(rec.p, g)
+                if self.param_groups[rec.gi]["fused"]:
+                    # adam.py:162-163: torch's fused kernel takes real floating-point params
+                    # only, and says so at their first step
+                    _device_dtype_check_for_fused(rec.p)
                 self._init_state(rec.p, st, ams_g[rec.gi])
             else:
                 if st["step"] is not views[rec.slot]:

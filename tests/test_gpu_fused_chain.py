@@ -324,3 +324,18 @@ def test_reference_schedule_and_checkpoint_interchange(dev):
             _compare(ours, ref, opt, topt)
         opt.zero_grad()
         topt.zero_grad()
+
+
+def test_fused_true_refuses_complex_params_as_torch_does(dev):
+    """torch's fused kernel takes real floating-point params only: AdamW(fused=True) raises
+    at a complex parameter's first step, with this message, and so does FusedAdamW."""
+    import mi_adamw
+    msgs = []
+    for cls in (torch.optim.AdamW, mi_adamw.FusedAdamW):
+        p = torch.nn.Parameter(torch.randn(8, dtype=torch.complex64, device=dev))
+        p.grad = torch.randn_like(p)
+        opt = cls([p], fused=True, **HP)
+        with pytest.raises(RuntimeError) as e:
+            opt.step()
+        msgs.append(str(e.value))
+    assert msgs[0] == msgs[1] and "`fused=True` requires" in msgs[0]
