@@ -5,10 +5,11 @@ model's parameters, and runs zero_grad, the forward (under bf16 autocast with --
 backward, optimizer.step() and the LambdaLR step (warm-up + cosine, main.py:36-43) every
 iteration.  Here the tiny GPT is compiled with inductor and trained that way for 10
 iterations with FusedAdamW (lr 6e-4, weight decay 0.1, config.py:11,13), with and without
-bf16 autocast, in both layouts.  The gradients inductor's backward hands to step() are
-also given, cloned, to torch.optim.AdamW(foreach=False) over a shadow copy of the
-parameters with its own LambdaLR: after every iteration the compiled model's parameters
-and FusedAdamW's moments must equal torch's bit for bit.  (Two compiled models stepped
+bf16 autocast, in both layouts, and with --amp --fused (main.py:80: fused=True).  The
+gradients inductor's backward hands to step() are also given, cloned, to
+torch.optim.AdamW (foreach=False, or fused=True) over a shadow copy of the parameters with
+its own LambdaLR: after every iteration the compiled model's parameters and FusedAdamW's
+moments must equal torch's bit for bit.  (Two compiled models stepped
 by the two optimizers would compare their backward passes too, and the embedding
 gradient accumulates with atomics, which is not bit-reproducible from run to run.)
 """
@@ -52,9 +53,10 @@ def _bits(t):
     return t.detach().view(torch.int32)
 
 
-@pytest.mark.parametrize("flat", [False, True])
-@pytest.mark.parametrize("amp", [False, True])
-def test_compiled_model_steps_as_torch_adamw(dev, amp, flat):
+@pytest.mark.parametrize("amp,flat,fused", [(False, False, False), (False, True, False),
+                                            (True, False, False), (True, True, False),
+                                            (True, False, True)])
+def test_compiled_model_steps_as_torch_adamw(dev, amp, flat, fused):
     import mi_adamw
     import refgpt
     torch._dynamo.reset()
@@ -62,14 +64,15 @@ def test_compiled_model_steps_as_torch_adamw(dev, amp, flat):
     shadow = [torch.nn.Parameter(p.detach().clone()) for p in model.parameters()]
     cmodel = torch.compile(model)
     hp = dict(lr=6e-4, weight_decay=0.1)
-    oopt = mi_adamw.FusedAdamW(cmodel.parameters(), **hp, fused=False, flat_buffer=flat)
-    topt = torch.optim.AdamW(shadow, **hp, foreach=False)
+    oopt = mi_adamw.FusedAdamW(cmodel.parameters(), **hp, fused=fused, flat_buffer=flat)
+    topt = (torch.optim.AdamW(shadow, **hp, fused=True) if fused
+            else torch.optim.AdamW(shadow, **hp, foreach=False))
     total = 10
     osch = torch.optim.lr_scheduler.LambdaLR(oopt, _lr_at(3, total))
     tsch = torch.optim.lr_scheduler.LambdaLR(topt, _lr_at(3, total))
     params = list(cmodel.parameters())
     ctx = torch.autocast("cuda", dtype=torch.bfloat16) if amp else contextlib.nullcontext()
-    print(f"amp {amp} flat {flat}: compiling the tiny GPT (inductor)", flush=True)
+    print(f"amp {amp} flat {flat} fused {fused}: compiling the tiny GPT (inductor)", flush=True)
     losses = []
     for it in range(total):
         ids, labels, mask = refgpt.batch(dev, seed=100 + it)
@@ -91,10 +94,12 @@ def test_compiled_model_steps_as_torch_adamw(dev, amp, flat):
             for key in ("exp_avg", "exp_avg_sq"):
                 assert torch.equal(_bits(oopt.state[p][key]), _bits(topt.state[q][key])), (it, key)
         if it == 0:
-            print(f"amp {amp} flat {flat}: first iteration done, loss {losses[0]:.4f}", flush=True)
+            print(f"amp {amp} flat {flat} fused {fused}: first iteration done, "
+                  f"loss {losses[0]:.4f}", flush=True)
     assert all(float(oopt.state[p]["step"]) == float(total) for p in params)
     assert oopt.param_groups[0]["lr"] == topt.param_groups[0]["lr"]
-    print(f"amp {amp} flat {flat}: {total} compiled iterations bit-identical to torch's AdamW, "
+    print(f"amp {amp} flat {flat} fused {fused}: {total} compiled iterations bit-identical "
+          f"to torch's AdamW, "
           f"loss {losses[0]:.4f} -> {losses[-1]:.4f}, {oopt.native_steps} native steps",
           flush=True)
     assert oopt.native_steps >= total - 2

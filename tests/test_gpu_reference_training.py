@@ -38,13 +38,15 @@ def _batch(dev):
     return x, y, torch.ones(B, S, device=dev)
 
 
-@pytest.mark.parametrize("variant", ["fp32", "clip-bf16-state-copy-bf16-weights"])
+@pytest.mark.parametrize("variant", ["fp32", "fp32-fused-true",
+                                     "clip-bf16-state-copy-bf16-weights"])
 def test_loss_decreases_with_the_fused_step(dev, variant):
     import mi_adamw
     model = _model(dev, 42)
     x, y, mask = _batch(dev)
-    if variant == "fp32":
-        opt = mi_adamw.FusedAdamW(model.parameters(), lr=1e-3)
+    if variant.startswith("fp32"):
+        # fp32-fused-true: the reference's --fused (main.py:80,177), torch's fused chain
+        opt = mi_adamw.FusedAdamW(model.parameters(), lr=1e-3, fused=variant.endswith("true"))
     else:
         opt = mi_adamw.FusedAdamW(model.parameters(), lr=1e-3, max_grad_norm=1.0,
                                   state_dtype=torch.bfloat16, bf16_copy=True)
@@ -52,7 +54,7 @@ def test_loss_decreases_with_the_fused_step(dev, variant):
         initial = model(x, y, mask)[1].item()
     for _ in range(200):
         opt.zero_grad()
-        if variant == "fp32":
+        if variant.startswith("fp32"):
             loss = model(x, y, mask)[1]
         else:
             with torch.autocast("cuda", dtype=torch.bfloat16), mi_adamw.bf16_weights(opt, model):
