@@ -345,6 +345,8 @@ def training_rows(device, batch: int, variants, iters: int = 20, warmup: int = 5
         "torch_fused_graph": lambda ps: torch.optim.AdamW(ps, **ref_hp, fused=True,
                                                           capturable=True),
         "mi_adamw": lambda ps: FusedAdamW(ps, **ref_hp, fused=False),
+        # the drop-in under the reference's --fused: torch's fused=True chain
+        "mi_adamw_fused_true": lambda ps: FusedAdamW(ps, **ref_hp, fused=True),
         "mi_adamw_placed": lambda ps: FusedAdamW(ps, **ref_hp, fused=False, place_trials=16),
         "mi_adamw_bf16_weights": lambda ps: FusedAdamW(ps, **ref_hp, fused=False, bf16_copy=True),
         "mi_adamw_flat": lambda ps: FusedAdamW(ps, **ref_hp, fused=False, flat_buffer=True),
@@ -787,7 +789,8 @@ def main() -> int:
         # batch for the bf16 copies against autocast's casts
         line["training"] = [
             training_rows(device, 4, ["torch_single_tensor", "torch_fused", "mi_adamw",
-                                      "mi_adamw_placed", "mi_adamw_bf16_weights", "mi_adamw_flat",
+                                      "mi_adamw_fused_true", "mi_adamw_placed",
+                                      "mi_adamw_bf16_weights", "mi_adamw_flat",
                                       "torch_fused_graph", "mi_adamw_flat_graph"]),
             training_rows(device, 16, ["mi_adamw", "mi_adamw_bf16_weights"]),
         ]
