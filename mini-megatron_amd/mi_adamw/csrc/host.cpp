@@ -371,7 +371,14 @@ int prepare(Plan* pl, uint64_t stream) {
         for (int k = 0; k < pl->n_state; ++k) {
             PyObject* o = PyDict_GetItem(en.st, pl->keys[k]);
             if (o != en.obj[k]) return kFallback;
-            if (k > 0 && tensor_ptr(o) != en.ptr[k]) return kFallback;
+            if (k > 0) {
+                // a moment re-strided or narrowed in place through .data keeps its object
+                // and address, but the row reads p's element count from it densely
+                const at::Tensor& t = THPVariable_Unpack(o);
+                if (reinterpret_cast<uint64_t>(t.data_ptr()) != en.ptr[k] ||
+                    !t.is_contiguous() || t.numel() != en.numel)
+                    return kFallback;
+            }
         }
         const uint64_t gp = reinterpret_cast<uint64_t>(g.data_ptr());
         pl->newgrad[i] = gp;

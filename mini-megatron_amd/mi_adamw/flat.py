@@ -131,7 +131,7 @@ class FlatLayout:
             buf = (self.exp_avg if key == "exp_avg" else self.exp_avg_sq
                    if key == "exp_avg_sq" else self.max_exp_avg_sq)
             if (buf is not None and t.data_ptr() == buf.data_ptr() + buf.element_size() * off
-                    and t.numel() == self.numels[id(p)]):
+                    and t.numel() == self.numels[id(p)] and t.is_contiguous()):
                 continue
             st[key] = self.adopt_state(p, key, t)
 
@@ -150,7 +150,12 @@ class FlatLayout:
         else:
             view = self._view(self.exp_avg if key == "exp_avg" else self.exp_avg_sq, p)
         self._check_size(p, t, f"state[{key!r}]")
-        view.copy_(t.reshape(view.shape))
+        src = t.reshape(view.shape)
+        if src.untyped_storage().data_ptr() == view.untyped_storage().data_ptr():
+            # the slice's own memory read in another order (re-strided in place): copy
+            # the values out first, so that no element is overwritten before it is read
+            src = src.clone()
+        view.copy_(src)
         return view
 
     def copy_view(self, p: torch.Tensor) -> torch.Tensor:
@@ -162,10 +167,10 @@ class FlatLayout:
         return v
 
     def _holds(self, buf: torch.Tensor, p: torch.Tensor, t: torch.Tensor | None) -> bool:
-        """t is p's slice of buf (a view at p's offset with p's element count)."""
+        """t is p's slice of buf (a dense view at p's offset with p's element count)."""
         off = self.offsets[id(p)]
         return (t is not None and t.data_ptr() == buf.data_ptr() + buf.element_size() * off
-                and t.numel() == self.numels[id(p)])
+                and t.numel() == self.numels[id(p)] and t.is_contiguous())
 
     @torch.no_grad()
     def adopt_buffers(self, bufs: dict, params, state) -> None:

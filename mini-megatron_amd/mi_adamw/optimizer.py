@@ -165,6 +165,12 @@ def _ptr(t: torch.Tensor | None) -> int:
     return 0 if t is None else t.data_ptr()
 
 
+def _layout(t: torch.Tensor | None) -> tuple:
+    """What a table row takes from a state tensor: its address, and that it is dense with
+    this many elements."""
+    return (0, 0, True) if t is None else (t.data_ptr(), t.numel(), t.is_contiguous())
+
+
 class _Rec:
     """One parameter's bookkeeping: group index, the parameter, its step slot, its state dict."""
 
@@ -1184,11 +1190,12 @@ class FusedAdamW(Optimizer):
         entries are split into launches), and the parameter and state pointers, which rarely
         change; and the gradient pointers, which change whenever zero_grad() frees the
         gradients and backward allocates them elsewhere."""
-        # the element count and contiguity too: a parameter narrowed or re-strided in place
-        # through .data keeps its address (a rebuild then checks it)
+        # the element count and contiguity too: a parameter or a moment narrowed or
+        # re-strided in place through .data keeps its address (a rebuild then checks or
+        # converts it)
         sig = [(rec.p.data_ptr(), rec.p.numel(), rec.p.is_contiguous(),
-                rec.st["exp_avg"].data_ptr(),
-                rec.st["exp_avg_sq"].data_ptr(), _ptr(rec.st.get("max_exp_avg_sq")))
+                _layout(rec.st["exp_avg"]), _layout(rec.st["exp_avg_sq"]),
+                _layout(rec.st.get("max_exp_avg_sq")))
                for rec, _ in entries]
         sig.append(tuple(hyper_idx))
         sig.append(tuple(bool(a) for a in hyper_ams))

@@ -219,26 +219,37 @@ def test_native_path_falls_back_on_every_other_change(dev):
     assert native["native"] == 1
 
 
-@pytest.mark.parametrize("view", ["strided", "transposed"])
-def test_state_replaced_by_a_non_dense_view(dev, view):
+@pytest.mark.parametrize("layout", ["tables", "flat"])
+@pytest.mark.parametrize("view", ["strided", "transposed", "restrided_in_place"])
+def test_state_replaced_by_a_non_dense_view(dev, view, layout):
     """A moment put into the state dict as a view that is not dense (every other element
-    of a larger buffer, or a transposed matrix) after the native path has a plan: the
-    step falls back, replaces the entry by a dense copy with the same values and steps
-    it like torch (whose per-tensor ops take any strides); the next steps are native
-    again.  The buffer around the strided view is never written."""
+    of a larger buffer, or a transposed matrix), or re-strided in place through .data
+    (same object and address, its elements read in another order, done to torch's state
+    too) after the native path has a plan: the step falls back, replaces the entry by a
+    dense copy with the same values and steps it like torch (whose per-tensor ops take any
+    strides); the next steps are native again.  In the flat layout the values go into
+    the tensor's slice of the moment buffer (its own memory, when re-strided in place).
+    The buffer around the strided view is never written."""
     import mi_adamw
     ref = make_params(SHAPES, dev)
     ours = clone_params(ref)
+    flat = layout == "flat"
     topt = torch.optim.AdamW(ref, foreach=False, **HP)
-    oopt = mi_adamw.FusedAdamW(ours, **HP)
+    oopt = mi_adamw.FusedAdamW(ours, **HP, flat_buffer=flat)
     spacer = []
     for k in range(2):
-        _assign(ref, ours, _fresh_grads(ref, k), spacer)
+        _assign(ref, ours, _fresh_grads(ref, k), spacer, inplace=flat)
         oopt.step()
         topt.step()
     j = 7 if view == "strided" else 3          # (70001,) or (144, 48)
     st = oopt.state[ours[j]]
-    if view == "strided":
+    if view == "restrided_in_place":
+        for opt, ps in ((oopt, ours), (topt, ref)):
+            v = opt.state[ps[j]]["exp_avg_sq"]
+            ptr = v.data_ptr()
+            v.data = v.data.as_strided((144, 48), (1, 144))
+            assert v.data_ptr() == ptr and not v.is_contiguous()
+    elif view == "strided":
         guard = torch.full((2 * ours[j].numel(),), 7.0, device=dev)
         t = guard[::2]
         t.copy_(st["exp_avg"])
@@ -249,7 +260,7 @@ def test_state_replaced_by_a_non_dense_view(dev, view):
         assert not st["exp_avg_sq"].is_contiguous()
     before = oopt.native_steps
     for k in range(2, 5):
-        _assign(ref, ours, _fresh_grads(ref, k), spacer)
+        _assign(ref, ours, _fresh_grads(ref, k), spacer, inplace=flat)
         oopt.step()
         topt.step()
         torch.cuda.synchronize()

@@ -98,8 +98,8 @@ def _unchanged(s, before_steps):
 
 @pytest.mark.parametrize("change", ["grad None", "grad non-contiguous", "grad dtype", "p.data",
                                     "p.data narrowed", "p.data re-strided", "grad narrowed",
-                                    "state replaced", "state data", "step replaced",
-                                    "other stream"])
+                                    "state replaced", "state data", "state re-strided",
+                                    "state narrowed", "step replaced", "other stream"])
 def test_every_other_change_falls_back_untouched(change):
     s = _Setup(n_params=2)
     assert s.prepare() == s.host.READY
@@ -144,6 +144,18 @@ def test_every_other_change_falls_back_untouched(change):
         s.states[1]["exp_avg"] = s.states[1]["exp_avg"].clone()
     elif change == "state data":
         s.states[1]["exp_avg_sq"].data = torch.zeros(p.numel())
+    elif change == "state re-strided":
+        # same object, address and element count, elements in another order
+        v = s.states[1]["exp_avg_sq"]
+        ptr = v.data_ptr()
+        v.data = v.data.as_strided((v.numel() // 2, 2), (1, v.numel() // 2))
+        assert v.data_ptr() == ptr and not v.is_contiguous()
+    elif change == "state narrowed":
+        # same object and address, fewer elements than the row reads
+        m = s.states[1]["exp_avg"]
+        ptr = m.data_ptr()
+        m.data = m.data[:m.numel() // 2]
+        assert m.data_ptr() == ptr
     elif change == "step replaced":
         s.states[1]["step"] = torch.tensor(8.0)
     elif change == "other stream":
