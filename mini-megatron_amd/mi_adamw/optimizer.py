@@ -1244,6 +1244,8 @@ class FusedAdamW(Optimizer):
         # unchanged; when only the gradients moved, the rows are rewritten and the
         # chunk tables kept.
         sig, grads = self._signature(entries, hyper_idx, hyper_ams, hyper_fused)
+        # the chunk tables are cut at chunk_elems: a new value needs new tables
+        sig.append(("chunk_elems", self.chunk_elems))
         cache = self._launch_cache
         if cache is not None and cache.sig == sig and cache.device == device:
             launches, norm_launch = cache.launches, cache.norm_launch

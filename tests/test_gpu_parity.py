@@ -478,6 +478,32 @@ def test_chunk_size_and_grid_shape_do_not_change_results(dev, state_dtype):
         assert max_ulp(n, norms[0]) <= 1
 
 
+def test_chunk_size_changed_between_steps(dev):
+    """chunk_elems and max_blocks changed on a live optimizer between steps: the chunk
+    tables are cut again at the new size (a table cut at the old size would step some
+    elements twice), and every step equals an untouched optimizer's.  The norm pass runs
+    under each chunking, with max_norm so large that the coefficient is exactly 1 (the
+    float64 partial sums, and so the last bit of the norm, depend on the chunking)."""
+    import mi_adamw
+    hp = dict(lr=3e-4, betas=(0.9, 0.95), weight_decay=0.1, max_grad_norm=1e9)
+    a = make_params(MINI_SHAPES, dev)
+    b = clone_params(a)
+    oa = mi_adamw.FusedAdamW(a, **hp)
+    ob = mi_adamw.FusedAdamW(b, **hp)
+    for step, (chunk, blocks) in enumerate(((4096, 0), (65536, 0), (8192, 7), (4096, 0))):
+        oa.chunk_elems, oa.max_blocks = chunk, blocks
+        set_grads(a, step, 1e-2)
+        for p, q in zip(a, b):
+            q.grad = p.grad.clone()
+        oa.step()
+        ob.step()
+        torch.cuda.synchronize()
+        for p, q in zip(a, b):
+            assert max_ulp(p, q) == 0, (step, chunk)
+            for k in ("exp_avg", "exp_avg_sq"):
+                assert max_ulp(oa.state[p][k], ob.state[q][k]) == 0, (step, k)
+
+
 def test_clip_step_is_deterministic(dev):
     """Two runs on the same inputs give the same bits, norm included (fixed reduction order)."""
     import mi_adamw
