@@ -339,3 +339,95 @@ def test_fused_true_refuses_complex_params_as_torch_does(dev):
             opt.step()
         msgs.append(str(e.value))
     assert msgs[0] == msgs[1] and "`fused=True` requires" in msgs[0]
+
+
+SPECIALS = [0.0, -0.0, 1e-45, -1e-45, 1e-40, -3e-39, 1.17e-38, 1e-30, -1e-20, 1e-8, 1.0, -1.0,
+            3e4, -1e15, 1e30, 3.4e38, float("inf"), float("-inf"), float("nan")]
+
+
+def _grid(specials):
+    """Every combination of a special p, g, m and |v| (v >= 0 as in real state)."""
+    s = torch.tensor(specials, dtype=torch.float32)
+    idx = torch.cartesian_prod(*(torch.arange(s.numel()) for _ in range(4)))
+    pv, gv, mv, vv = (s[idx[:, j]] for j in range(4))
+    return pv, gv, mv, vv.abs()
+
+
+def _same_bits(a: np.ndarray, b: np.ndarray) -> bool:
+    """Equal NaN positions and identical bits elsewhere (signed zeros told apart)."""
+    a, b = a.reshape(-1), b.reshape(-1)
+    na, nb = np.isnan(a), np.isnan(b)
+    return bool(np.array_equal(na, nb) and np.array_equal(a[~na].view(np.uint32),
+                                                          b[~nb].view(np.uint32)))
+
+
+@pytest.mark.parametrize("case", [
+    dict(betas=(0.9, 0.95), step=1.0, maximize=False, weight_decay=0.1),
+    dict(betas=(0.3, 0.999), step=7.0, maximize=True, weight_decay=0.1),
+    dict(betas=(0.9, 0.95), step=1000.0, maximize=False, weight_decay=0.0),
+    dict(betas=(0.9, 0.999), step=20.0, maximize=False, weight_decay=0.1, amsgrad=True),
+])
+def test_fused_true_special_values_match_torch_fused(dev, case):
+    """Denormals, signed zeros, tiny and huge magnitudes, inf and NaN in p, g, m, v (and the
+    amsgrad maximum): FusedAdamW(fused=True) equals torch.optim.AdamW(fused=True) bit for
+    bit, and the oracle's fused chain equals both (which pins it on these values)."""
+    import mi_adamw
+    pv, gv, mv, vv = _grid(SPECIALS)
+    ams = case.get("amsgrad", False)
+    xv = vv.roll(1) if ams else None          # a maximum unrelated to v, specials included
+    hp = dict(lr=1e-3, betas=case["betas"], eps=1e-8, weight_decay=case["weight_decay"],
+              maximize=case["maximize"], amsgrad=ams)
+    st = {"step": torch.tensor(case["step"] - 1), "exp_avg": mv.clone(), "exp_avg_sq": vv.clone()}
+    if ams:
+        st["max_exp_avg_sq"] = xv.clone()
+    out = []
+    for cls in (torch.optim.AdamW, mi_adamw.FusedAdamW):
+        p = torch.nn.Parameter(pv.clone().to(dev))
+        p.grad = gv.clone().to(dev)
+        opt = cls([p], fused=True, **hp)
+        load_states(opt, [p], [st])
+        opt.step()
+        torch.cuda.synchronize()
+        s = opt.state[p]
+        out.append([to_np(t) for t in (p, s["exp_avg"], s["exp_avg_sq"])]
+                   + ([to_np(s["max_exp_avg_sq"])] if ams else []))
+    pn, mn, vn = pv.numpy().copy(), mv.numpy().copy(), vv.numpy().copy()
+    xn = xv.numpy().copy() if ams else None
+    O.adamw_step_fused(pn, gv.numpy().copy(), mn, vn, lr=hp["lr"], betas=hp["betas"],
+                       eps=hp["eps"], weight_decay=hp["weight_decay"], step=case["step"],
+                       maximize=hp["maximize"], vmax=xn)
+    oracle = [pn, mn, vn] + ([xn] if ams else [])
+    for what, t, o, orc in zip("pmvx", out[0], out[1], oracle):
+        assert _same_bits(t, o), (what, case)
+        assert _same_bits(t, orc), (what, case, "oracle")
+    print(f"{pv.numel()} special combinations, {case}: identical", flush=True)
+
+
+def test_fused_true_special_values_bf16_state_match_oracle(dev):
+    """The special-value grid with bf16 moments and the bf16 copy in the fused=True chain,
+    against the oracle's fused chain on bf16-stored moments: bf16 rounding of inf, NaN,
+    denormals and overflow to inf."""
+    import mi_adamw
+    pv, gv, mv, vv = _grid([0.0, -0.0, 1e-45, -1e-40, 9.2e-41, 1.17e-38, 1e-30, -1e-20, 1e-8,
+                            1.0, -1.0, 3e4, 3.3961e38, 3.4e38, float("inf"), float("-inf"),
+                            float("nan")])
+    p = torch.nn.Parameter(pv.clone().to(dev))
+    p.grad = gv.clone().to(dev)
+    hp = dict(lr=1e-3, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.1)
+    opt = mi_adamw.FusedAdamW([p], fused=True, state_dtype=torch.bfloat16, bf16_copy=True, **hp)
+    load_states(opt, [p], [{"step": torch.tensor(4.0), "exp_avg": mv.clone(),
+                            "exp_avg_sq": vv.clone()}])
+    opt.step()
+    torch.cuda.synchronize()
+    pn = pv.numpy().copy()
+    mb = O.to_bf16_bits(mv.numpy())
+    vb = O.to_bf16_bits(vv.numpy())
+    O.adamw_step_fused_bf16state(pn, gv.numpy().copy(), mb, vb, step=5.0, **hp)
+    assert _same_bits(pn, to_np(p))
+    got_m = to_np(opt.state[p]["exp_avg"].view(torch.int16)).view(np.uint16)
+    got_v = to_np(opt.state[p]["exp_avg_sq"].view(torch.int16)).view(np.uint16)
+    assert np.array_equal(got_m, mb) and np.array_equal(got_v, vb)
+    copy = to_np(opt.bf16_param(p).view(torch.int16)).view(np.uint16)
+    assert np.array_equal(copy, O.to_bf16_bits(pn))
+    print(f"{pv.numel()} special combinations with bf16 state: identical to the oracle",
+          flush=True)
