@@ -47,6 +47,7 @@
 #include <vector>
 
 #include "mi_adamw.h"
+#include "fp32_math.h"   // bf16x2_bits, bf16_bits, div_by_recip
 
 namespace {
 
@@ -86,14 +87,6 @@ static_assert(sizeof(mi_adamw_fused_hyper) == 56 && offsetof(mi_adamw_fused_hype
 // ---------------------------------------------------------------------------
 // Element math
 
-// fp32 -> bf16, round to nearest even; every NaN becomes 0x7FC0 (the value
-// torch's Tensor.to(torch.bfloat16) produces).
-__device__ __forceinline__ uint32_t bf16_bits(float x) {
-    uint32_t u = __float_as_uint(x);
-    if ((u & 0x7f800000u) == 0x7f800000u && (u & 0x007fffffu)) return 0x7fc0u;
-    u += 0x7fffu + ((u >> 16) & 1u);
-    return u >> 16;
-}
 __device__ __forceinline__ float bf16_to_f32(uint32_t h16) { return __uint_as_float(h16 << 16); }
 
 // Lerp.h:21-35, fp32 opmath, fused the way torch-ROCm compiles it.
@@ -160,6 +153,7 @@ struct FusedScalars {
     double eps;
     float step_size;       // f32(lr / (double)f32(1 - beta1^step))
     float bc2_sqrt;        // f32(sqrt(1 - beta2^step))
+    float inv_bc2_sqrt;    // 1.0f / bc2_sqrt, correctly rounded (for div_by_recip)
     float grad_sign;
     bool decay;            // weight_decay != 0
 };
@@ -181,7 +175,9 @@ __device__ __forceinline__ void adamw_elem(float& p, float g, float& m, float& v
         x = __builtin_fmaxf(x, v);
         dv = x;
     }
-    const float q = __builtin_sqrtf(dv) / h.bc2_sqrt;     // fp32 sqrt and division
+    // fp32 sqrt, then the fp32 quotient by bc2_sqrt: equal to the correctly rounded
+    // division for every value sqrtf can give here (fp32_math.h)
+    const float q = div_by_recip(__builtin_sqrtf(dv), h.bc2_sqrt, h.inv_bc2_sqrt);
     const float d = static_cast<float>(double(q) + h.eps); // + eps in float64
     p = p - (h.step_size * m) / d;                         // fp32
 }
@@ -230,8 +226,8 @@ __device__ __forceinline__ f32x4 ld4_bf16(const uint16_t* p) {
 }
 __device__ __forceinline__ void st4_bf16(uint16_t* p, f32x4 v) {
     u32x2 w;
-    w.x = bf16_bits(v.x) | (bf16_bits(v.y) << 16);
-    w.y = bf16_bits(v.z) | (bf16_bits(v.w) << 16);
+    w.x = bf16x2_bits(v.x, v.y);
+    w.y = bf16x2_bits(v.z, v.w);
     __builtin_nontemporal_store(w, (GLOBAL u32x2*)(p));
 }
 
@@ -450,6 +446,7 @@ struct FusedHyper {
         s.eps = c.eps;
         s.step_size = static_cast<float>(lr / double(bc1));
         s.bc2_sqrt = bc2_sqrt;
+        s.inv_bc2_sqrt = 1.0f / bc2_sqrt;
         s.grad_sign = c.grad_sign;
         s.decay = c.decay != 0;
         return s;

@@ -598,6 +598,47 @@ def test_special_values_match_torch(dev):
         print(f"{n} special combinations, betas {betas}: identical", flush=True)
 
 
+def _rne_bf16_bits(bits: torch.Tensor) -> torch.Tensor:
+    """Round-to-nearest-even fp32 -> bf16 on int32 bit patterns, in int64 arithmetic
+    (u + 0x7fff + ((u >> 16) & 1)) >> 16, every NaN -> 0x7FC0: the conversion torch's
+    c10::BFloat16 performs, restated on the integers."""
+    u = bits.to(torch.int64) & 0xFFFFFFFF
+    r = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16) & 0xFFFF
+    nan = ((u & 0x7F800000) == 0x7F800000) & ((u & 0x007FFFFF) != 0)
+    return torch.where(nan, torch.full_like(r, 0x7FC0), r)
+
+
+@pytest.mark.parametrize("offset", [0, 1])
+def test_bf16_copy_of_every_fp32_pattern(dev, offset):
+    """The bf16 copy the update stores, for all 2^32 fp32 bit patterns as parameters, in
+    16 slices of 2^28: lr 0, no weight decay and g = m = v = 0 leave p as it is, so the
+    copy is the conversion of the input.  It must equal round-to-nearest-even with every
+    NaN stored as 0x7FC0 (restated on the integers) and, for every non-NaN input, torch's
+    own Tensor.to(torch.bfloat16) on the GPU.  offset 0: 16-byte aligned parameters, the
+    four-lane stores; offset 1: a parameter one element into its buffer, the scalar path."""
+    import mi_adamw
+    n = 1 << 28
+    store = torch.zeros(n + 8, device=dev)
+    p = torch.nn.Parameter(store[offset:offset + n])
+    p.grad = torch.zeros(n, device=dev)
+    opt = mi_adamw.FusedAdamW([p], lr=0.0, weight_decay=0.0, bf16_copy=True)
+    base = torch.arange(n, dtype=torch.int64, device=dev)
+    for k in range(16):
+        bits = (base + (k * n - (1 << 31))).to(torch.int32)
+        with torch.no_grad():
+            p.view(torch.int32).copy_(bits)
+        opt.step()
+        torch.cuda.synchronize()
+        got = opt.bf16_param(p).view(torch.int16).to(torch.int64) & 0xFFFF
+        assert torch.equal(got, _rne_bf16_bits(bits)), (k, offset)
+        ok = ~torch.isnan(p.detach())
+        assert torch.equal(p.detach().view(torch.int32)[ok], bits[ok]), (k, offset)
+        ref = p.detach()[ok].to(torch.bfloat16).view(torch.int16).to(torch.int64) & 0xFFFF
+        assert torch.equal(got[ok], ref), (k, offset)
+        del got, ok, ref
+    print(f"2^32 patterns, offset {offset}: the copy is RNE with NaN -> 0x7FC0", flush=True)
+
+
 def test_special_values_bf16_state_match_oracle(dev):
     """The special-value grid with bf16 moments (and a bf16 copy), against the oracle's
     bf16-state model: bf16 rounding of inf, NaN (0x7FC0), denormals and overflow to inf."""
