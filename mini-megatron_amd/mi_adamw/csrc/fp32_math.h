@@ -24,7 +24,7 @@ __device__ __forceinline__ uint32_t bf16x2_bits(float a, float b) {
 __device__ __forceinline__ uint32_t bf16_bits(float x) { return bf16x2_bits(x, 0.0f) & 0xffffu; }
 
 // s / b, correctly rounded, given r = 1.0f / b (correctly rounded), for the quotients of
-// the fused=True chain: s = sqrtf(v) (+-0, inf, NaN, or in [2^-74.5, 2^64]) and b = bc2_sqrt
+// the fused=True chain with host step counts: s = sqrtf(v) (+-0, inf, NaN, or in [2^-74.5, 2^64]) and b = bc2_sqrt
 // (in [2^-26.5, 1]).  q0 = s * r is within one ulp of s / b, so e = s - q0 * b is exactly
 // representable (a multiple of 2^(i-47) below 2^(i-23), i the exponent of s, normal or
 // subnormal alike at these ranges) and one fma gives it; q0 + e * r, rounded once, is the

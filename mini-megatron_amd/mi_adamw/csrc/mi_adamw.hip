@@ -146,14 +146,20 @@ __device__ __forceinline__ void adamw_elem(float& p, float g, float& m, float& v
 
 // The scalars of torch's fused=True chain for one workgroup (FusedHyper): the float64
 // hyperparameters as _fused_adamw_ receives them, and the per-step values it forms.
-struct FusedScalars {
+// kRecip: the quotient by bc2_sqrt is formed from its reciprocal (div_by_recip), which
+// gives the division's bits; without it, by the division itself.  The host-step chain
+// takes kRecip (its per-step values are kernel arguments, so the reciprocal costs no
+// vector register); the device-step chain forms them after two out-of-line pow calls
+// with the first tile's loads in flight, where one more value spills, so it divides.
+template <bool kRecip>
+struct FusedScalarsT {
     double beta1, one_minus_beta1;
     double beta2, one_minus_beta2;
     double lr_wd;          // lr * weight_decay
     double eps;
     float step_size;       // f32(lr / (double)f32(1 - beta1^step))
     float bc2_sqrt;        // f32(sqrt(1 - beta2^step))
-    float inv_bc2_sqrt;    // 1.0f / bc2_sqrt, correctly rounded (for div_by_recip)
+    float inv_bc2_sqrt;    // kRecip: 1.0f / bc2_sqrt, correctly rounded
     float grad_sign;
     bool decay;            // weight_decay != 0
 };
@@ -162,9 +168,9 @@ struct FusedScalars {
 // p are float64 expressions of fp32 values, each rounded once to fp32; the contractions
 // are those of torch-ROCm's build of that kernel (the left product of each sum fused).
 // ::max there is fmaxf.  g already carries the clip scale and sign.
-template <bool kAms, bool kCapt>
+template <bool kAms, bool kCapt, bool kRecip>
 __device__ __forceinline__ void adamw_elem(float& p, float g, float& m, float& v, float& x,
-                                           const FusedScalars& h) {
+                                           const FusedScalarsT<kRecip>& h) {
     if (h.decay)                                           // param -= lr * wd * param
         p = static_cast<float>(__builtin_fma(-h.lr_wd, double(p), double(p)));
     const double dg = g;
@@ -175,9 +181,12 @@ __device__ __forceinline__ void adamw_elem(float& p, float g, float& m, float& v
         x = __builtin_fmaxf(x, v);
         dv = x;
     }
-    // fp32 sqrt, then the fp32 quotient by bc2_sqrt: equal to the correctly rounded
-    // division for every value sqrtf can give here (fp32_math.h)
-    const float q = div_by_recip(__builtin_sqrtf(dv), h.bc2_sqrt, h.inv_bc2_sqrt);
+    // fp32 sqrt, then the correctly rounded fp32 quotient by bc2_sqrt (div_by_recip gives
+    // the division's bits for every value sqrtf can give here, fp32_math.h)
+    const float s = __builtin_sqrtf(dv);
+    float q;
+    if constexpr (kRecip) q = div_by_recip(s, h.bc2_sqrt, h.inv_bc2_sqrt);
+    else q = s / h.bc2_sqrt;
     const float d = static_cast<float>(double(q) + h.eps); // + eps in float64
     p = p - (h.step_size * m) / d;                         // fp32
 }
@@ -231,7 +240,7 @@ __device__ __forceinline__ void st4_bf16(uint16_t* p, f32x4 v) {
     __builtin_nontemporal_store(w, (GLOBAL u32x2*)(p));
 }
 
-// adamw_elem on the four lanes of a dwordx4 group (H: ElemScalars or FusedScalars).
+// adamw_elem on the four lanes of a dwordx4 group (H: ElemScalars or FusedScalarsT).
 template <bool kAms, bool kCapt, class H>
 __device__ __forceinline__ void adamw_vec(f32x4& p, f32x4 g, f32x4& m, f32x4& v, f32x4& x,
                                           const H& h) {
@@ -420,14 +429,14 @@ __device__ __attribute__((noinline)) double pow_f64(double x, double y) { return
 // they are read through the constant address space.
 template <bool kDevSteps>
 struct FusedHyper {
-    using Scalars = FusedScalars;
+    using Scalars = FusedScalarsT<!kDevSteps>;
     static constexpr bool kCapt = false;
     static constexpr bool kLate = true;
     static constexpr bool kProbe = false;
     FusedPack fp;
     const float* steps;
     const int32_t* step_index;
-    __device__ __forceinline__ FusedScalars get(const mi_adamw_tensor& t, int32_t row) const {
+    __device__ __forceinline__ Scalars get(const mi_adamw_tensor& t, int32_t row) const {
         const FusedSet& c = fp.h[t.hyper];
         float bc1 = c.bc1, bc2_sqrt = c.bc2_sqrt;
         if (kDevSteps) {
@@ -437,7 +446,7 @@ struct FusedHyper {
             bc2_sqrt = static_cast<float>(sqrt(1.0 - pow_f64(c.beta2, step)));
         }
         const double lr = c.lr_ptr ? double(*(const CONSTANT float*)(c.lr_ptr)) : c.lr;
-        FusedScalars s;
+        Scalars s;
         s.beta1 = c.beta1;
         s.one_minus_beta1 = c.one_minus_beta1;
         s.beta2 = c.beta2;
@@ -446,7 +455,7 @@ struct FusedHyper {
         s.eps = c.eps;
         s.step_size = static_cast<float>(lr / double(bc1));
         s.bc2_sqrt = bc2_sqrt;
-        s.inv_bc2_sqrt = 1.0f / bc2_sqrt;
+        if (!kDevSteps) s.inv_bc2_sqrt = 1.0f / bc2_sqrt;
         s.grad_sign = c.grad_sign;
         s.decay = c.decay != 0;
         return s;
