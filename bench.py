@@ -134,26 +134,34 @@ def build_set(name: str, device, capturable: bool = False, write_grads: bool = F
 
 
 def time_fused(opt, steps: int, warmup: int):
-    """Warm up, then time exactly `steps` steps; per-kernel HIP events inside."""
+    """Warm up, then time exactly `steps` steps, with per-kernel HIP events inside the timed
+    region on the launch stream.  Each event record is a marker packet that costs the GPU
+    4-5 us, so the events are shared between steps: one step's last event is the next
+    step's first.  A clipped step adds two (after the norm pass and finalize, after the
+    update), a step without the clip one (its update time is then its step time)."""
     for _ in range(warmup):
         opt.step()
     torch.cuda.synchronize()
-    evs = [tuple(torch.cuda.Event(enable_timing=True) for _ in range(3)) for _ in range(steps)]
-    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    clip = opt.max_grad_norm is not None
+    ends = [torch.cuda.Event(enable_timing=True) for _ in range(steps + 1)]
+    mids = [torch.cuda.Event(enable_timing=True) for _ in range(steps)] if clip else None
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    start.record()
+    ends[0].record()
     for k in range(steps):
-        opt.timing_events = evs[k]
+        opt.timing_events = (None, mids[k] if clip else None, ends[k + 1])
         opt.step()
-    end.record()
     torch.cuda.synchronize()
     wall = (time.perf_counter() - t0) * 1e3 / steps
     opt.timing_events = None
-    gpu = start.elapsed_time(end) / steps
-    norm_ms = [e[0].elapsed_time(e[1]) for e in evs]
-    upd_ms = [e[1].elapsed_time(e[2]) for e in evs]
-    step_ms = [e[0].elapsed_time(e[2]) for e in evs]
+    gpu = ends[0].elapsed_time(ends[steps]) / steps
+    step_ms = [ends[k].elapsed_time(ends[k + 1]) for k in range(steps)]
+    if clip:
+        norm_ms = [ends[k].elapsed_time(mids[k]) for k in range(steps)]
+        upd_ms = [mids[k].elapsed_time(ends[k + 1]) for k in range(steps)]
+    else:
+        norm_ms = [0.0] * steps
+        upd_ms = list(step_ms)
     return gpu, wall, norm_ms, upd_ms, step_ms
 
 

@@ -165,6 +165,12 @@ def _ptr(t: torch.Tensor | None) -> int:
     return 0 if t is None else t.data_ptr()
 
 
+def _record(ev, i: int) -> None:
+    """Record event i of a timing_events tuple, unless the tuple or that entry is None."""
+    if ev is not None and ev[i] is not None:
+        ev[i].record()
+
+
 def _layout(t: torch.Tensor | None) -> tuple:
     """What a table row takes from a state tensor: its address, and that it is dense with
     this many elements."""
@@ -446,6 +452,10 @@ class FusedAdamW(Optimizer):
         self._step_idx: tuple[tuple, torch.Tensor] | None = None
         self._fast: _Fast | None = None
         self.native_steps = 0          # steps taken by the native host path
+        # measurement hook: None, or three torch.cuda.Event recorded on the launch stream
+        # before the norm pass, before the update and after it; an entry that is None is
+        # not recorded (a caller timing back-to-back steps may reuse one step's last event
+        # as the next step's first: each record is a marker packet that costs GPU time)
         self.timing_events = None
         # place_trials: place_buffers' report once it has run (None until then)
         self.placement: dict | None = None
@@ -1063,17 +1073,14 @@ class FusedAdamW(Optimizer):
             for h, gi in enumerate(fast.hyper_group):
                 harr[h] = _hyper(groups[gi], float(fast.hyper_steps[h]))
         ev = self.timing_events
-        if ev is not None:
-            ev[0].record()
+        _record(ev, 0)
         if fast.clip:
             norm = torch.empty((), dtype=torch.float32, device=fast.device)
             _lib.check(host.norm(fast.plan, stream, norm.data_ptr()), "mi_adamw_grad_norm")
             self.last_grad_norm = norm
-        if ev is not None:
-            ev[1].record()
+        _record(ev, 1)
         _lib.check(host.update(fast.plan, stream, fast.harr_addr, len(harr)), "mi_adamw_step")
-        if ev is not None:
-            ev[2].record()
+        _record(ev, 2)
         if self._copy_sync is not None:
             host.sync_versions(fast.plan, self._copy_sync)
         return True
@@ -1276,8 +1283,7 @@ class FusedAdamW(Optimizer):
             self._launch_cache = _LaunchCache(sig, device, launches, norm_launch, grads)
 
         ev = self.timing_events
-        if ev is not None:
-            ev[0].record()
+        _record(ev, 0)
         if self.max_grad_norm is not None:
             norm = torch.empty((), dtype=torch.float32, device=device)
             if norm_launch.n_chunks == 0:
@@ -1316,8 +1322,7 @@ class FusedAdamW(Optimizer):
             flags |= _lib.F_CLIP
             if self.clip_write_grads:
                 flags |= _lib.F_WRITE_GRAD
-        if ev is not None:
-            ev[1].record()
+        _record(ev, 1)
         for launch, (_, _, hs, (ams, fused), _) in zip(launches, parts):
             if launch.n_chunks == 0:
                 continue
@@ -1358,8 +1363,7 @@ class FusedAdamW(Optimizer):
                 launch.rows.data_ptr(), launch.chunks.data_ptr(), launch.n_chunks,
                 self.chunk_elems, harr, len(hs), coef.data_ptr(), state_code, lflags,
                 self.max_blocks, stream), "mi_adamw_step")
-        if ev is not None:
-            ev[2].record()
+        _record(ev, 2)
         if len(parts) == 1 and hyper_group is not None:
             self._fast = self._make_fast(entries, hyper_idx, hyper_group, hyper_ams[0],
                                          hyper_fused[0], launches[0], device, stream, partials,
