@@ -170,6 +170,42 @@ def test_fused_true_with_clip(dev):
 
 
 @pytest.mark.filterwarnings("ignore:This instance was constructed with capturable=True")
+@pytest.mark.parametrize("capturable", [False, True])
+@pytest.mark.parametrize("flat", [False, True])
+def test_fused_true_clip_write_grads_matches_torch(dev, flat, capturable):
+    """fused=True with the clip storing the clipped gradients (clip_write_grads) and the
+    bf16 copy: the stored gradients equal torch's clip_grads_with_norm_ at the kernel's own
+    norm, and p, m, v equal torch's fused AdamW after it, over three chained steps; the
+    copy is the bf16 of p.  capturable=True runs the chain's device-step kernel."""
+    import mi_adamw
+    ref = make_params(SHAPES, dev)
+    ours = clone_params(ref)
+    topt = torch.optim.AdamW(ref, fused=True, capturable=capturable, **HP)
+    opt = mi_adamw.FusedAdamW(ours, fused=True, capturable=capturable, max_grad_norm=1.0,
+                              clip_write_grads=True, bf16_copy=True, flat_buffer=flat, **HP)
+    states = midtrain_state(ref, 1000.0)
+    load_states(topt, ref, states)
+    load_states(opt, ours, states)
+    for step in range(3):
+        set_grads(ref, step, 1e-1)
+        for p, q in zip(ref, ours):
+            if flat and q.grad is not None:
+                q.grad.copy_(p.grad)
+            else:
+                q.grad = p.grad.clone()
+        opt.step()
+        norm = opt.last_grad_norm
+        assert norm.item() > 1.0
+        torch.nn.utils.clip_grads_with_norm_(ref, 1.0, norm.clone())
+        topt.step()
+        _compare(ours, ref, opt, topt)
+        for p, q in zip(ref, ours):
+            assert max_ulp(q.grad, p.grad) == 0
+            assert torch.equal(opt.bf16_param(q).view(torch.int16),
+                               q.detach().to(torch.bfloat16).view(torch.int16))
+
+
+@pytest.mark.filterwarnings("ignore:This instance was constructed with capturable=True")
 def test_fused_true_capturable_replayed_from_a_graph(dev):
     """capturable=True with fused=True: torch runs the fused kernel on device step counts;
     here the fused chain forms the per-step values from the device counts.  Two eager
