@@ -21,7 +21,7 @@ Three kinds of case:
   stepped on eight elements from p = 0 with no gradient and no weight decay, so that
   p is the update itself and shows both values.
 
-Run from the repository root on a GPU box:
+Run from the repository root on a machine with a ROCm GPU:
     python tests/golden/make_fused_golden.py [OUT]       (default: beside this file)
 """
 from __future__ import annotations

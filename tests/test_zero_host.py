@@ -31,7 +31,7 @@ def test_shard_bounds_partition(total, world):
 
 
 def test_shard_bounds_of_the_6p7b_flat_buffer():
-    # 6.7B at 8 ranks: 857,884,672 elements each (SURVEY's 858M per rank)
+    # 6.7B at 8 ranks: 857,884,672 elements each (858M per rank)
     b = shard_bounds(6_863_077_376, 8)
     assert [hi - lo for lo, hi in b] == [857_884_672] * 8
 
