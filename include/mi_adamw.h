@@ -42,7 +42,7 @@
 extern "C" {
 #endif
 
-#define MI_ADAMW_ABI_VERSION 8
+#define MI_ADAMW_ABI_VERSION 9
 #define MI_ADAMW_MAX_HYPER 16      /* hyperparameter sets per launch */
 #define MI_ADAMW_MAX_NORM_BLOCKS 4096 /* partial sums per grad-norm launch */
 
@@ -324,6 +324,26 @@ int mi_adamw_step_capturable(const mi_adamw_tensor *d_tensors, const mi_adamw_ch
                              const float *d_steps, const int32_t *d_step_index,
                              const float *d_grad_scale, int32_t state_dtype, int32_t flags,
                              int32_t max_blocks, void *stream);
+
+/* The same step as mi_adamw_step_capturable (torch's capturable chain, adam.py:480-527,
+ * for a step recorded into a HIP graph), with the per-step values formed once per table
+ * row instead of in every workgroup: a first launch forms each row's values (two powf,
+ * three divisions, from the row's device step count, by the code the update would run)
+ * into d_row_scalars, and the update reads them there.  Both launches go on `stream`, so
+ * a graph that records the call records both.  Same results bit for bit; the update no
+ * longer waits on that prologue, which bounds mi_adamw_step_capturable's update when the
+ * moments are bf16.  d_row_scalars: device memory of n_rows * MI_ADAMW_ROW_SCALAR_BYTES
+ * bytes, 16-byte aligned, provided by the caller and overwritten by every call (calls
+ * that overlap on one buffer race); n_rows: the rows of d_tensors.  The other arguments
+ * are those of mi_adamw_step_capturable. */
+#define MI_ADAMW_ROW_SCALAR_BYTES 64
+int mi_adamw_step_capturable_rows(const mi_adamw_tensor *d_tensors, int32_t n_rows,
+                                  const mi_adamw_chunk *d_chunks, int64_t n_chunks,
+                                  int64_t chunk_elems, const mi_adamw_capt_hyper *hypers,
+                                  int32_t n_hyper, const float *d_steps,
+                                  const int32_t *d_step_index, void *d_row_scalars,
+                                  const float *d_grad_scale, int32_t state_dtype, int32_t flags,
+                                  int32_t max_blocks, void *stream);
 
 /* The fused AdamW update in torch's fused=True chain (mi_adamw_fused_hyper) over
  * every chunk of the tables, or over one contiguous range (_flat).  Replaces

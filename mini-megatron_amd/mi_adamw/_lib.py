@@ -25,11 +25,12 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_DIR = os.environ.get("MI_ADAMW_LIB_DIR") or HERE
 LIB_PATH = os.path.join(LIB_DIR, "libmi_adamw.so")
 
-ABI_VERSION = 8
+ABI_VERSION = 9
 MAX_HYPER = 16
 MAX_NORM_BLOCKS = 4096
 NOALLOC_SCRATCH_BYTES = 4096
 CHUNK_QUANTUM = 4096
+ROW_SCALAR_BYTES = 64   # per table row, mi_adamw_step_capturable_rows
 
 OK = 0
 E_INVALID = -1
@@ -68,6 +69,7 @@ EXPORTS = (
     "mi_adamw_step_prescaled",
     "mi_adamw_step_flat_prescaled",
     "mi_adamw_step_capturable",
+    "mi_adamw_step_capturable_rows",
     "mi_adamw_step_fused_chain",
     "mi_adamw_step_flat_fused_chain",
     "mi_adamw_widen_bf16",
@@ -177,6 +179,8 @@ _SIGNATURES = {
                                      ctypes.c_int),
     "mi_adamw_step_capturable": ([_vp, _vp, _i64, _i64, _vp, _i32, _vp, _vp, _vp, _i32, _i32,
                                   _i32, _vp], ctypes.c_int),
+    "mi_adamw_step_capturable_rows": ([_vp, _i32, _vp, _i64, _i64, _vp, _i32, _vp, _vp, _vp, _vp,
+                                       _i32, _i32, _i32, _vp], ctypes.c_int),
     "mi_adamw_step_fused_chain": ([_vp, _vp, _i64, _i64, _vp, _i32, _vp, _vp, _vp, _f32, _i32,
                                    _i32, _i32, _vp], ctypes.c_int),
     "mi_adamw_step_flat_fused_chain": ([_vp, _vp, _vp, _f32, _i64, _i32, _i32, _i32, _vp],

@@ -1,6 +1,7 @@
-// Two fp32 helpers of the update kernels whose results must equal another, slower form
-// bit for bit: the bf16 conversion of the stored moments and copies, and the division by
-// a per-step constant in the fused=True chain.  Kept in a header so that the check
+// fp32 helpers of the update kernels whose results must equal another, slower form bit
+// for bit: the bf16 conversion of the stored moments and copies, and the quotient by a
+// per-step constant in the fused=True chain (positive divisor) and in the capturable chain
+// (negative divisor).  Kept in a header so that the check
 // program tests/c/div_check.hip runs this very code against the reference forms.
 #pragma once
 
@@ -39,4 +40,24 @@ __device__ __forceinline__ float div_by_recip(float s, float b, float r) {
     const float q0 = s * r;
     const float e = -__builtin_fmaf(q0, b, -s);
     return __builtin_fmaf(__builtin_fmaxf(e, -3.40282347e38f), r, q0);
+}
+
+// s / b, correctly rounded, for a negative b given r = 1.0f / b (correctly rounded): the
+// capturable chain's sqrtf(v) / (sqrt(bc2) * -step_size), with s as above (+-0, inf, NaN,
+// or in [2^-74.5, 2^64]) and |b| in [2^-62, 2^50], where q0, e and the quotient stay
+// normal (the caller divides outside that range).  Every nonzero result is the exact
+// negation of div_by_recip's for |b| (round-to-nearest-even is symmetric), which the
+// significand check covers; e is formed as s - q0 * b here, the form that gives a zero
+// quotient the sign of s / b when b < 0 (the other form does when b > 0).  e is NaN only
+// when q0 is +-inf or NaN, and fmaxf then leaves q0 as it is, as above.
+__device__ __forceinline__ float div_by_neg_recip(float s, float b, float r) {
+    const float q0 = s * r;
+    const float e = __builtin_fmaf(-q0, b, s);
+    return __builtin_fmaf(__builtin_fmaxf(e, -3.40282347e38f), r, q0);
+}
+
+// The range of |b| in which div_by_neg_recip gives the division's bits.
+__device__ __forceinline__ bool neg_recip_in_range(float b) {
+    const float a = __builtin_fabsf(b);
+    return a >= 0x1p-62f && a <= 0x1p50f;
 }

@@ -116,6 +116,8 @@ struct ElemScalars {
     float den_add;         // eps, or eps / -step_size
     float neg_step_size;   // default chain only
     float grad_sign;
+    float inv_den_scale;   // capturable chain: 1.0f / den_scale, when den_recip
+    int32_t den_recip;     // capturable chain: den_scale in div_by_neg_recip's range
 };
 
 // One element of adam.py:419-547.  g already carries the clip scale and sign.
@@ -134,7 +136,9 @@ __device__ __forceinline__ void adamw_elem(float& p, float g, float& m, float& v
     }
     float d = __builtin_sqrtf(dv);                         // adam.py:520/545 sqrt
     if (kCapt) {
-        d = d / h.den_scale;                               // adam.py:520-521 / (bc2_sqrt * -step_size)
+        // adam.py:520-521 / (bc2_sqrt * -step_size): the correctly rounded quotient, from the
+        // workgroup's reciprocal when den_scale is in range (fp32_math.h), else divided
+        d = h.den_recip ? div_by_neg_recip(d, h.den_scale, h.inv_den_scale) : d / h.den_scale;
         d = d + h.den_add;                                 // adam.py:522 add_(eps / -step_size)
         p = p + m / d;                                     // adam.py:527 addcdiv_, value 1
     } else {
@@ -341,6 +345,7 @@ struct StaticHyper {
     static constexpr bool kCapt = false;
     static constexpr bool kLate = false;
     static constexpr bool kProbe = false;
+    static constexpr bool kShare = false;
     HyperPack hp;
     __device__ __forceinline__ ElemScalars get(const mi_adamw_tensor& t, int32_t) const {
         const mi_adamw_hyper& x = hp.h[t.hyper];
@@ -364,6 +369,7 @@ struct CaptHyper {
     static constexpr bool kCapt = true;
     static constexpr bool kLate = true;
     static constexpr bool kProbe = false;
+    static constexpr bool kShare = true;
     CaptPack cp;
     const float* steps;
     const int32_t* step_index;
@@ -393,7 +399,48 @@ struct CaptHyper {
         h.den_add = (1.0f / neg) * c.eps;                             // adam.py:522 eps / neg
         h.neg_step_size = 0.0f;
         h.grad_sign = c.grad_sign;
+        h.den_recip = neg_recip_in_range(h.den_scale);
+        h.inv_den_scale = h.den_recip ? 1.0f / h.den_scale : 0.0f;
         return h;
+    }
+};
+
+// The capturable chain's per-step values formed once per table row
+// (mi_adamw_step_capturable_rows): a first launch runs CaptHyper::get for every row, one
+// thread per row, and the update reads its row's values with scalar loads, as the default
+// chain reads its kernel arguments, instead of forming them in every workgroup.
+struct alignas(16) RowScalars {
+    ElemScalars s;
+    uint8_t pad[MI_ADAMW_ROW_SCALAR_BYTES - sizeof(ElemScalars)];
+};
+static_assert(sizeof(RowScalars) == MI_ADAMW_ROW_SCALAR_BYTES, "one row's values per slot");
+
+__global__ __launch_bounds__(256) void mi_adamw_capt_rows_kernel(
+    const mi_adamw_tensor* __restrict__ rows, int32_t n_rows, CaptHyper hs,
+    RowScalars* __restrict__ out) {
+    const int32_t r = blockIdx.x * 256 + threadIdx.x;
+    if (r >= n_rows) return;
+    out[r].s = hs.get(rows[r], r);
+}
+
+struct CaptRowsHyper {
+    using Scalars = ElemScalars;
+    static constexpr bool kCapt = true;
+    static constexpr bool kLate = true;
+    static constexpr bool kProbe = false;
+    static constexpr bool kShare = false;
+    const RowScalars* rows;
+    __device__ __forceinline__ ElemScalars get(const mi_adamw_tensor&, int32_t row) const {
+        // written by the launch before this one on the stream: read word by word through
+        // the constant address space, so the loads are scalar
+        static_assert(sizeof(ElemScalars) % 4 == 0, "read as 32-bit words");
+        const CONSTANT uint32_t* w = (const CONSTANT uint32_t*)(rows + row);
+        uint32_t v[sizeof(ElemScalars) / 4];
+#pragma unroll
+        for (unsigned k = 0; k < sizeof(ElemScalars) / 4; ++k) v[k] = w[k];
+        ElemScalars s;
+        memcpy(&s, v, sizeof(s));
+        return s;
     }
 };
 
@@ -409,6 +456,11 @@ struct FusedSet {
     float grad_sign;
     int32_t decay;               // weight_decay != 0
     const float* lr_ptr;         // device fp32 lr, or NULL
+    // host step counts and a host lr: the per-step values of the workgroup prologue,
+    // formed once on the host with the same correctly rounded IEEE operations
+    double lr_wd;                // lr * weight_decay
+    float step_size;             // f32(lr / (double)bc1)
+    float inv_bc2_sqrt;          // 1.0f / bc2_sqrt
 };
 
 struct FusedPack {
@@ -433,6 +485,10 @@ struct FusedHyper {
     static constexpr bool kCapt = false;
     static constexpr bool kLate = true;
     static constexpr bool kProbe = false;
+    // every wave forms its own: with device step counts the two out-of-line float64 pow
+    // calls in one wave's branch spill under this chain's 64-VGPR cap, and with host step
+    // counts the prologue is a few loads
+    static constexpr bool kShare = false;
     FusedPack fp;
     const float* steps;
     const int32_t* step_index;
@@ -445,19 +501,26 @@ struct FusedHyper {
             bc1 = static_cast<float>(1.0 - pow_f64(c.beta1, step));
             bc2_sqrt = static_cast<float>(sqrt(1.0 - pow_f64(c.beta2, step)));
         }
-        const double lr = c.lr_ptr ? double(*(const CONSTANT float*)(c.lr_ptr)) : c.lr;
         Scalars s;
         s.beta1 = c.beta1;
         s.one_minus_beta1 = c.one_minus_beta1;
         s.beta2 = c.beta2;
         s.one_minus_beta2 = c.one_minus_beta2;
-        s.lr_wd = lr * c.weight_decay;
         s.eps = c.eps;
-        s.step_size = static_cast<float>(lr / double(bc1));
         s.bc2_sqrt = bc2_sqrt;
-        if (!kDevSteps) s.inv_bc2_sqrt = 1.0f / bc2_sqrt;
         s.grad_sign = c.grad_sign;
         s.decay = c.decay != 0;
+        if (!kDevSteps && !c.lr_ptr) {
+            // formed on the host (fused_set_from)
+            s.lr_wd = c.lr_wd;
+            s.step_size = c.step_size;
+            s.inv_bc2_sqrt = c.inv_bc2_sqrt;
+        } else {
+            const double lr = c.lr_ptr ? double(*(const CONSTANT float*)(c.lr_ptr)) : c.lr;
+            s.lr_wd = lr * c.weight_decay;
+            s.step_size = static_cast<float>(lr / double(bc1));
+            if (!kDevSteps) s.inv_bc2_sqrt = 1.0f / bc2_sqrt;
+        }
         return s;
     }
 };
@@ -472,6 +535,7 @@ struct ProbeHyper {
     static constexpr bool kCapt = false;
     static constexpr bool kLate = false;
     static constexpr bool kProbe = true;
+    static constexpr bool kShare = false;
     __device__ __forceinline__ ElemScalars get(const mi_adamw_tensor&, int32_t) const {
         return ElemScalars{};
     }
@@ -690,6 +754,36 @@ constexpr int update_waves_per_eu() {
     return (HS::kLate && !HS::kCapt && !kAms) ? 8 : 4;
 }
 
+// The scalars of a chunk formed by the workgroup's first wave and read by every wave
+// from LDS: they are the same in every lane, and forming them takes a few hundred
+// instructions (two pow, divisions), which every wave would otherwise issue.  Called
+// by every thread of the workgroup, once per chunk, with parity alternating: wave 0
+// writes buffer `parity` only after all threads have passed the previous chunk's
+// barrier, so no thread still reads the buffer it overwrites (that buffer was last
+// read two chunks back, before that barrier).
+template <class HS>
+__device__ __forceinline__ typename HS::Scalars shared_scalars(const HS& hs,
+                                                               const mi_adamw_tensor& t,
+                                                               int32_t row, int parity) {
+    using S = typename HS::Scalars;
+    __shared__ S buf[2];
+    if (threadIdx.x < 64) {
+        const S h = hs.get(t, row);
+        if (threadIdx.x == 0) buf[parity] = h;
+    }
+    __syncthreads();
+    // the same words in every lane: into scalar registers, so that branches on them are
+    // scalar and the element loop keeps its vector registers
+    static_assert(sizeof(S) % 4 == 0, "shared scalars are read as 32-bit words");
+    uint32_t w[sizeof(S) / 4];
+    memcpy(w, &buf[parity], sizeof(S));
+#pragma unroll
+    for (unsigned k = 0; k < sizeof(S) / 4; ++k) w[k] = __builtin_amdgcn_readfirstlane(w[k]);
+    S r;
+    memcpy(&r, w, sizeof(S));
+    return r;
+}
+
 template <class Src, class HS, typename StateT, bool kClip, bool kCopy, bool kWriteGrad, bool kAms>
 __global__ __launch_bounds__(kUpdThreads)
 __attribute__((amdgpu_waves_per_eu(update_waves_per_eu<HS, kAms>())))
@@ -702,14 +796,16 @@ void mi_adamw_update_kernel(
     constexpr bool kLate = HS::kLate;
     constexpr bool kProbe = HS::kProbe;
     const float scale = kClip ? *grad_scale : 1.0f;
+    int parity = 0;   // shared_scalars' buffer of this chunk
     for (int64_t c = blockIdx.x; c < n_chunks; c += gridDim.x) {
         mi_adamw_tensor t;
         int64_t begin, end;
         int32_t row;
         src.get(c, chunk_elems, t, begin, end, row);
         // Default chain: the scalars are kernel arguments.  Capturable and fused
-        // chains: they take a few hundred instructions (two pow, divisions), formed
-        // once the first tile's loads are in flight.
+        // chains: they are formed once the first tile's loads are in flight; in the
+        // capturable chain (two powf, three divisions: a few hundred instructions) by
+        // the first wave alone and shared through LDS (kShare).
         typename HS::Scalars h;
         if (!kLate) h = hs.get(t, row);
         float* __restrict__ P = t.param;
@@ -720,46 +816,52 @@ void mi_adamw_update_kernel(
         void* __restrict__ X = t.max_exp_avg_sq;
 
         int64_t vend = begin;
+        int64_t i = begin + threadIdx.x * kVec;
+        T cur;
+        bool have = false;
         if (t.flags & MI_ADAMW_T_VEC) {
             vend = begin + ((end - begin) & ~static_cast<int64_t>(kVec - 1));
-            int64_t i = begin + threadIdx.x * kVec;
-            if (i < vend) {
-                T cur;
-                cur.load(P, G, M, V, X, i);
-                if (kLate) {
-                    __builtin_amdgcn_sched_barrier(0);
-                    h = hs.get(t, row);
+            have = i < vend;
+            if (have) cur.load(P, G, M, V, X, i);
+        }
+        if (kLate) {
+            __builtin_amdgcn_sched_barrier(0);
+            if constexpr (HS::kShare) {
+                h = shared_scalars(hs, t, row, parity);
+                parity ^= 1;
+            } else {
+                h = hs.get(t, row);
+            }
+        }
+        if (have) {
+            const float gmul = h.grad_sign;
+            while (true) {
+                const int64_t j = i + kUpdTile;
+                const bool more = j < vend;
+                T nxt = cur;
+                if (more) nxt.load(P, G, M, V, X, j);
+                // the stored value of div_(world), then of the clip, then -g with maximize
+                f32x4 gs = f32x4{cur.g.x * pre, cur.g.y * pre, cur.g.z * pre, cur.g.w * pre};
+                if (kClip) gs = f32x4{gs.x * scale, gs.y * scale, gs.z * scale, gs.w * scale};
+                if (kWriteGrad) st4(G + i, gs);
+                if (kProbe) {
+                    keep(gs);
+                } else {
+                    gs = f32x4{gs.x * gmul, gs.y * gmul, gs.z * gmul, gs.w * gmul};
+                    adamw_vec<kAms, kCapt>(cur.p, gs, cur.m, cur.v, cur.x, h);
                 }
-                const float gmul = h.grad_sign;
-                while (true) {
-                    const int64_t j = i + kUpdTile;
-                    const bool more = j < vend;
-                    T nxt = cur;
-                    if (more) nxt.load(P, G, M, V, X, j);
-                    // the stored value of div_(world), then of the clip, then -g with maximize
-                    f32x4 gs = f32x4{cur.g.x * pre, cur.g.y * pre, cur.g.z * pre, cur.g.w * pre};
-                    if (kClip) gs = f32x4{gs.x * scale, gs.y * scale, gs.z * scale, gs.w * scale};
-                    if (kWriteGrad) st4(G + i, gs);
-                    if (kProbe) {
-                        keep(gs);
-                    } else {
-                        gs = f32x4{gs.x * gmul, gs.y * gmul, gs.z * gmul, gs.w * gmul};
-                        adamw_vec<kAms, kCapt>(cur.p, gs, cur.m, cur.v, cur.x, h);
-                    }
-                    st4(P + i, cur.p);
-                    IO::st(M, i, cur.m);
-                    IO::st(V, i, cur.v);
-                    if (kAms) IO::st(X, i, cur.x);
-                    if (kCopy) st4_bf16(C + i, cur.p);
-                    if (!more) break;
-                    cur = nxt;
-                    i = j;
-                }
+                st4(P + i, cur.p);
+                IO::st(M, i, cur.m);
+                IO::st(V, i, cur.v);
+                if (kAms) IO::st(X, i, cur.x);
+                if (kCopy) st4_bf16(C + i, cur.p);
+                if (!more) break;
+                cur = nxt;
+                i = j;
             }
         }
         // Scalar path: the ragged tail of a vector tensor, or a whole tensor
         // whose pointers are not aligned for dwordx4.
-        if (kLate && vend < end) h = hs.get(t, row);
         const float gmul = h.grad_sign;
         for (int64_t j = vend + threadIdx.x; j < end; j += kUpdThreads) {
             float g1 = ld1(G + j) * pre;
@@ -1030,6 +1132,11 @@ FusedSet fused_set_from(const mi_adamw_fused_hyper& h, bool host_steps) {
     if (host_steps) {
         f.bc1 = static_cast<float>(1.0 - std::pow(h.beta1, double(h.step)));
         f.bc2_sqrt = static_cast<float>(std::sqrt(1.0 - std::pow(h.beta2, double(h.step))));
+        if (!h.lr_ptr) {
+            f.lr_wd = h.lr * h.weight_decay;
+            f.step_size = static_cast<float>(h.lr / double(f.bc1));
+            f.inv_bc2_sqrt = 1.0f / f.bc2_sqrt;
+        }
     }
     f.grad_sign = h.grad_sign;
     f.decay = h.weight_decay != 0.0;
@@ -1052,6 +1159,24 @@ int check_flat(const mi_adamw_tensor* t, int32_t state_dtype, int32_t flags) {
             return MI_ADAMW_E_ALIGN;
     }
     return MI_ADAMW_OK;
+}
+
+// The capturable entry points' host checks and kernel argument: MI_ADAMW_E_INVALID or 0.
+int capt_hyper_from(const mi_adamw_capt_hyper* hypers, int32_t n_hyper, const float* d_steps,
+                    const int32_t* d_step_index, CaptHyper& hs) {
+    if (!hypers || n_hyper <= 0 || n_hyper > MI_ADAMW_MAX_HYPER || !d_steps || !d_step_index)
+        return MI_ADAMW_E_INVALID;
+    for (int32_t i = 0; i < n_hyper; ++i) {
+        const int32_t mode = hypers[i].lr_mode;
+        if (mode != MI_ADAMW_LR_FLOAT && mode != MI_ADAMW_LR_VALUE && mode != MI_ADAMW_LR_DEVICE)
+            return MI_ADAMW_E_INVALID;
+        if (mode == MI_ADAMW_LR_DEVICE && !hypers[i].lr_ptr) return MI_ADAMW_E_INVALID;
+    }
+    memset(&hs, 0, sizeof(hs));
+    memcpy(hs.cp.h, hypers, sizeof(mi_adamw_capt_hyper) * n_hyper);
+    hs.steps = d_steps;
+    hs.step_index = d_step_index;
+    return 0;
 }
 
 }  // namespace
@@ -1112,7 +1237,7 @@ int scratch_on(hipStream_t s, double** out) {
 extern "C" {
 
 const char* mi_adamw_version(void) {
-    return "mi_adamw 8 gfx950 fused clip+adamw (fp32/bf16 state, bf16 copy, amsgrad, flat, "
+    return "mi_adamw 9 gfx950 fused clip+adamw (fp32/bf16 state, bf16 copy, amsgrad, flat, "
            "capturable, fused=True chain, bf16 widen, memory probe, no-alloc norm, range norm, "
            "grad prescale, grad patch)";
 }
@@ -1329,23 +1454,34 @@ int mi_adamw_step_capturable(const mi_adamw_tensor* d_tensors, const mi_adamw_ch
                              const float* d_steps, const int32_t* d_step_index,
                              const float* d_grad_scale, int32_t state_dtype, int32_t flags,
                              int32_t max_blocks, void* stream) {
-    if (!d_tensors || !d_chunks || !hypers || n_hyper <= 0 || n_hyper > MI_ADAMW_MAX_HYPER ||
-        !d_steps || !d_step_index)
-        return MI_ADAMW_E_INVALID;
-    for (int32_t i = 0; i < n_hyper; ++i) {
-        const int32_t mode = hypers[i].lr_mode;
-        if (mode != MI_ADAMW_LR_FLOAT && mode != MI_ADAMW_LR_VALUE && mode != MI_ADAMW_LR_DEVICE)
-            return MI_ADAMW_E_INVALID;
-        if (mode == MI_ADAMW_LR_DEVICE && !hypers[i].lr_ptr) return MI_ADAMW_E_INVALID;
-    }
     CaptHyper hs;
-    memset(&hs, 0, sizeof(hs));
-    memcpy(hs.cp.h, hypers, sizeof(mi_adamw_capt_hyper) * n_hyper);
-    hs.steps = d_steps;
-    hs.step_index = d_step_index;
+    if (!d_tensors || !d_chunks || capt_hyper_from(hypers, n_hyper, d_steps, d_step_index, hs))
+        return MI_ADAMW_E_INVALID;
     TableSource src{d_tensors, d_chunks};
     return launch_update(src, n_chunks, chunk_elems, hs, d_grad_scale, state_dtype, flags,
                          max_blocks, static_cast<hipStream_t>(stream));
+}
+
+int mi_adamw_step_capturable_rows(const mi_adamw_tensor* d_tensors, int32_t n_rows,
+                                  const mi_adamw_chunk* d_chunks, int64_t n_chunks,
+                                  int64_t chunk_elems, const mi_adamw_capt_hyper* hypers,
+                                  int32_t n_hyper, const float* d_steps,
+                                  const int32_t* d_step_index, void* d_row_scalars,
+                                  const float* d_grad_scale, int32_t state_dtype, int32_t flags,
+                                  int32_t max_blocks, void* stream) {
+    CaptHyper hs;
+    if (!d_tensors || n_rows <= 0 || !d_chunks || !d_row_scalars || !aligned(d_row_scalars, 16) ||
+        capt_hyper_from(hypers, n_hyper, d_steps, d_step_index, hs))
+        return MI_ADAMW_E_INVALID;
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    RowScalars* rows = static_cast<RowScalars*>(d_row_scalars);
+    hipLaunchKernelGGL(mi_adamw_capt_rows_kernel, dim3((n_rows + 255) / 256), dim3(256), 0, s,
+                       d_tensors, n_rows, hs, rows);
+    const int rc = launch_status();
+    if (rc) return rc;
+    TableSource src{d_tensors, d_chunks};
+    return launch_update(src, n_chunks, chunk_elems, CaptRowsHyper{rows}, d_grad_scale,
+                         state_dtype, flags, max_blocks, s);
 }
 
 int mi_adamw_step_fused_chain(const mi_adamw_tensor* d_tensors, const mi_adamw_chunk* d_chunks,

@@ -19,9 +19,10 @@ replaces the per-tensor loop with the kernels of libmi_adamw:
 * ``mi_adamw_step`` / ``mi_adamw_step_flat`` -- the AdamW update of every
   tensor, with fp32 or bf16 moments, an optional bf16 model copy and amsgrad's
   running maximum (adam.py:538-543) for the groups that set it;
-* ``mi_adamw_step_capturable`` -- the same update in torch's capturable chain
-  (capturable=True): step counts on the device, the per-step scalars formed
-  in the kernel, so that step() can be recorded into a HIP graph.
+* ``mi_adamw_step_capturable_rows`` -- the same update in torch's capturable
+  chain (capturable=True): step counts on the device, the per-step scalars
+  formed on the device (once per tensor, by a launch before the update), so
+  that step() can be recorded into a HIP graph.
 
 Per-element results match ``torch.optim.AdamW(foreach=False)`` on the same GPU
 tensors: the kernels follow the fp32 op chain and the fused multiply-adds of
@@ -204,16 +205,21 @@ class _Launch:
     """Device-resident tensor and chunk tables for one kernel launch."""
 
     __slots__ = ("rows", "chunks", "n_chunks", "n_rows", "host_rows", "tables", "src", "rest",
-                 "step_index")
+                 "step_index", "row_scalars")
 
     def __init__(self, rows: np.ndarray, chunk_elems: int, device: torch.device,
                  tables: bool = False, src: np.ndarray | None = None,
                  rest: np.ndarray | None = None, step_slots: np.ndarray | None = None):
         lib = _lib.load()
         self.n_rows = len(rows)
-        # capturable launches: row i's index into the device step buffer
+        # capturable launches: row i's index into the device step buffer, and the device
+        # memory in which a step forms each row's per-step values before the update
+        # (mi_adamw_step_capturable_rows), allocated here, never under graph capture
         self.step_index = (None if step_slots is None else
                            _upload(np.ascontiguousarray(step_slots, dtype=np.int32), device))
+        self.row_scalars = (None if step_slots is None else
+                            torch.empty(self.n_rows * _lib.ROW_SCALAR_BYTES, dtype=torch.uint8,
+                                        device=device))
         self.host_rows = rows.copy()
         self.tables = tables or len(rows) != 1
         # src[i]: the entry whose gradient row i points at (-1: a flat group row, whose
@@ -1332,11 +1338,12 @@ class FusedAdamW(Optimizer):
                 continue
             if self.capturable:
                 carr = (_lib.CaptHyper * len(hs))(*hs)
-                _lib.check(lib.mi_adamw_step_capturable(
-                    launch.rows.data_ptr(), launch.chunks.data_ptr(), launch.n_chunks,
-                    self.chunk_elems, carr, len(hs), self._steps.data_ptr(),
-                    launch.step_index.data_ptr(), coef.data_ptr(), state_code, lflags,
-                    self.max_blocks, stream), "mi_adamw_step_capturable")
+                _lib.check(lib.mi_adamw_step_capturable_rows(
+                    launch.rows.data_ptr(), launch.n_rows, launch.chunks.data_ptr(),
+                    launch.n_chunks, self.chunk_elems, carr, len(hs), self._steps.data_ptr(),
+                    launch.step_index.data_ptr(), launch.row_scalars.data_ptr(),
+                    coef.data_ptr(), state_code, lflags, self.max_blocks, stream),
+                    "mi_adamw_step_capturable_rows")
                 continue
             harr = (_lib.Hyper * len(hs))(*hs)
             pre = self.grad_prescale

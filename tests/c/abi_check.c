@@ -177,6 +177,16 @@ static int cpu_checks(void)
     ch.lr_mode = MI_ADAMW_LR_DEVICE;
     CHECK(mi_adamw_step_capturable(fake, fake, 1, 4096, &ch, 1, fake, fake, NULL, 0, 0, 0,
                                    NULL) == MI_ADAMW_E_INVALID, "device lr without a pointer");
+    ch.lr_mode = MI_ADAMW_LR_FLOAT;
+    CHECK(mi_adamw_step_capturable_rows(fake, 1, fake, 1, 4096, &ch, 1, fake, fake, NULL, NULL,
+                                        0, 0, 0, NULL) == MI_ADAMW_E_INVALID,
+          "capturable rows without row scalars");
+    CHECK(mi_adamw_step_capturable_rows(fake, 1, fake, 1, 4096, &ch, 1, fake, fake,
+                                        (void *)(uintptr_t)8, NULL, 0, 0, 0, NULL) ==
+              MI_ADAMW_E_INVALID, "misaligned row scalars");
+    CHECK(mi_adamw_step_capturable_rows(fake, 0, fake, 1, 4096, &ch, 1, fake, fake,
+                                        (void *)(uintptr_t)4096, NULL, 0, 0, 0, NULL) ==
+              MI_ADAMW_E_INVALID, "capturable rows with no rows");
     CHECK(mi_adamw_widen_bf16(NULL, fake, 1, 4096, NULL) == MI_ADAMW_E_INVALID,
           "widen without tensors");
     CHECK(mi_adamw_widen_bf16(fake, fake, 0, 4096, NULL) == MI_ADAMW_E_INVALID,
@@ -455,7 +465,12 @@ static void capt_case(void)
     int32_t *d_index = dev_copy(step_index, sizeof step_index);
     const float lr_dev = 2e-3f;
     float *d_lr = dev_copy(&lr_dev, sizeof lr_dev);
-    for (int pass = 0; pass < 2; ++pass) {
+    void *d_row_scalars = NULL;
+    HIP(hipMalloc(&d_row_scalars, NT * MI_ADAMW_ROW_SCALAR_BYTES));
+    /* passes 0, 1: mi_adamw_step_capturable; 2, 3: mi_adamw_step_capturable_rows; even
+     * passes a float lr, odd ones a device lr; the state carries over from pass to pass */
+    for (int pass = 0; pass < 4; ++pass) {
+        const int dev_lr = pass & 1, rows_entry = pass >= 2;
         mi_adamw_capt_hyper ch;
         memset(&ch, 0, sizeof ch);
         ch.beta1 = 0.5f;
@@ -465,7 +480,7 @@ static void capt_case(void)
         ch.eps = 1e-8f;
         ch.grad_sign = 1.0f;
         float lr, wd_factor;
-        if (pass == 0) {
+        if (!dev_lr) {
             ch.lr_mode = MI_ADAMW_LR_FLOAT;
             ch.lr = lr = (float)1e-3;
             ch.wd_factor = wd_factor = (float)(1.0 - 1e-3 * 0.1);
@@ -476,10 +491,15 @@ static void capt_case(void)
             lr = lr_dev;
             wd_factor = 1.0f - lr_dev * 0.1f;   /* two fp32 ops, as on the device */
         }
-        const int rc = mi_adamw_step_capturable(d_rows, d_chunks, n_chunks, 4096, &ch, 1,
-                                                d_steps, d_index, NULL, MI_ADAMW_STATE_F32, 0,
-                                                0, NULL);
-        CHECK(rc == 0, "mi_adamw_step_capturable: %s", mi_adamw_strerror(rc));
+        const int rc =
+            rows_entry
+                ? mi_adamw_step_capturable_rows(d_rows, NT, d_chunks, n_chunks, 4096, &ch, 1,
+                                                d_steps, d_index, d_row_scalars, NULL,
+                                                MI_ADAMW_STATE_F32, 0, 0, NULL)
+                : mi_adamw_step_capturable(d_rows, d_chunks, n_chunks, 4096, &ch, 1, d_steps,
+                                           d_index, NULL, MI_ADAMW_STATE_F32, 0, 0, NULL);
+        CHECK(rc == 0, "mi_adamw_step_capturable%s: %s", rows_entry ? "_rows" : "",
+              mi_adamw_strerror(rc));
         HIP(hipDeviceSynchronize());
         for (int k = 0; k < NT; ++k) {
             const int64_t n = numel[k];
@@ -489,7 +509,7 @@ static void capt_case(void)
             oc.beta2 = ch.beta2;
             oc.one_minus_beta2 = ch.one_minus_beta2;
             oc.grad_sign = 1.0f;
-            oracle_capt_scalars(ch.beta1, ch.beta2, lr, ch.eps, steps[step_index[k]], pass,
+            oracle_capt_scalars(ch.beta1, ch.beta2, lr, ch.eps, steps[step_index[k]], dev_lr,
                                 &oc.den_scale, &oc.den_add);
             oracle_adamw_capt_f32(pr[k], g[k], mr[k], vr[k], NULL, n, &oc, &ROCM_OPS, 1.0f, 0);
             back(p[k], dp[k], n * 4);
@@ -506,8 +526,10 @@ static void capt_case(void)
     }
     HIP(hipFree(d_rows)); HIP(hipFree(d_chunks)); HIP(hipFree(d_steps)); HIP(hipFree(d_index));
     HIP(hipFree(d_lr));
+    HIP(hipFree(d_row_scalars));
     free(chunks);
-    printf("abi_check gpu: capturable tables, steps 3 and 1, float then device lr: bit-exact\n");
+    printf("abi_check gpu: capturable tables, steps 3 and 1, float then device lr, both entry "
+           "points: bit-exact\n");
 }
 
 /* The clip split at the all-reduce over `world` slices of one flat range, with the

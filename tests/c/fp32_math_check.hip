@@ -1,4 +1,4 @@
-// Checks the two fp32 helpers of the update kernels (mini-megatron_amd/mi_adamw/csrc/
+// Checks the fp32 helpers of the update kernels (mini-megatron_amd/mi_adamw/csrc/
 // fp32_math.h), compiled from that header, against the forms they replace, on the GPU:
 //
 // 1. bf16x2_bits against round-to-nearest-even on the integers, (u + 0x7fff +
@@ -10,9 +10,13 @@
 //    - s and b at every exponent pairing the fused=True chain can give (s = sqrtf(v) in
 //      [2^-75, 2^64] and +-0, inf, NaN; b = bc2_sqrt in [2^-27, 1]), sampled;
 //    - every pair of significands (s, b in [1, 2), 2^46 pairs), unless a smaller number of
-//      the 128 launches of 2^39 pairs is asked for.
+//      the 128 launches of 2^39 pairs is asked for;
+// 4. div_by_neg_recip(s, b, 1.0f / b), the capturable chain's quotient by a negative b,
+//    against s / b: s as in 3, b in -[2^-62, 2^50] at every exponent (sampled), and the
+//    significand pairs of 16 of the 128 launches with b negated (its nonzero results are
+//    the exact negations of div_by_recip's, which 3 covers in full).
 //
-// Usage: fp32_math_check [launches]   (default 128: all pairs; about 31 s on an MI355X)
+// Usage: fp32_math_check [launches]   (default 128: all pairs; about 35 s on an MI355X)
 // Prints one line per step and "fp32_math_check: ok" when nothing differs.
 #include <hip/hip_runtime.h>
 
@@ -71,27 +75,31 @@ __device__ __forceinline__ bool same(float x, float y) {
     return (x != x && y != y) || __float_as_uint(x) == __float_as_uint(y);
 }
 
+template <bool kNeg>
 __global__ void check_div_sampled(const float* s, const float* b, int ns, int nb,
                                   unsigned long long* bad, uint32_t* first) {
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= ns * nb) return;
-    const float sv = s[i / nb], bv = b[i % nb];
-    const float want = sv / bv, got = div_by_recip(sv, bv, 1.0f / bv);
+    const float sv = s[i / nb], bv = kNeg ? -b[i % nb] : b[i % nb];
+    const float want = sv / bv;
+    const float got = kNeg ? div_by_neg_recip(sv, bv, 1.0f / bv) : div_by_recip(sv, bv, 1.0f / bv);
     if (!same(want, got))
         record(bad, first, __float_as_uint(sv), __float_as_uint(bv), __float_as_uint(want),
                __float_as_uint(got));
 }
 
 // thread t: b significand b_base + (t >> 6); s significands [(t & 63) << 17, + 2^17)
+template <bool kNeg>
 __global__ __launch_bounds__(256) void check_div_all(uint32_t b_base, unsigned long long* bad,
                                                      uint32_t* first) {
     const uint32_t t = blockIdx.x * 256u + threadIdx.x;
-    const float b = __uint_as_float(0x3f800000u | (b_base + (t >> 6)));
+    const float b = __uint_as_float((kNeg ? 0xbf800000u : 0x3f800000u) | (b_base + (t >> 6)));
     const float r = 1.0f / b;
     const uint32_t s0 = (t & 63u) << 17;
     for (uint32_t k = 0; k < (1u << 17); ++k) {
         const float s = __uint_as_float(0x3f800000u | (s0 + k));
-        const float want = s / b, got = div_by_recip(s, b, r);
+        const float want = s / b;
+        const float got = kNeg ? div_by_neg_recip(s, b, r) : div_by_recip(s, b, r);
         if (__float_as_uint(want) != __float_as_uint(got))
             record(bad, first, __float_as_uint(s), __float_as_uint(b), __float_as_uint(want),
                    __float_as_uint(got));
@@ -175,15 +183,28 @@ int main(int argc, char** argv) {
     CK(hipMalloc(&dbb, nb * sizeof(float)));
     CK(hipMemcpy(dss, ss.data(), ns * sizeof(float), hipMemcpyHostToDevice));
     CK(hipMemcpy(dbb, bb.data(), nb * sizeof(float), hipMemcpyHostToDevice));
-    check_div_sampled<<<(ns * nb + 255) / 256, 256>>>(dss, dbb, ns, nb, bad, first);
+    check_div_sampled<false><<<(ns * nb + 255) / 256, 256>>>(dss, dbb, ns, nb, bad, first);
     CK(hipDeviceSynchronize());
     char what[128];
     snprintf(what, sizeof what, "div_by_recip, %d sampled and special pairs", ns * nb);
     if (report(what, bad, first, &total)) return 2;
 
+    // 4a. the negative divisor over its whole range, sampled (b negated in the kernel)
+    const int nbn = 113 * 64;
+    std::vector<float> bneg(nbn);
+    for (int e = 0; e < 113; ++e)
+        for (int j = 0; j < 64; ++j) bneg[e * 64 + j] = ldexpf(j ? rand_sig() : 1.0f, e - 62);
+    float* dbn;
+    CK(hipMalloc(&dbn, nbn * sizeof(float)));
+    CK(hipMemcpy(dbn, bneg.data(), nbn * sizeof(float), hipMemcpyHostToDevice));
+    check_div_sampled<true><<<(ns * nbn + 255) / 256, 256>>>(dss, dbn, ns, nbn, bad, first);
+    CK(hipDeviceSynchronize());
+    snprintf(what, sizeof what, "div_by_neg_recip, %d sampled and special pairs", ns * nbn);
+    if (report(what, bad, first, &total)) return 2;
+
     // 3b. every pair of significands
     for (int L = 0; L < launches; ++L) {
-        check_div_all<<<(1u << 22) / 256, 256>>>((uint32_t)L << 16, bad, first);
+        check_div_all<false><<<(1u << 22) / 256, 256>>>((uint32_t)L << 16, bad, first);
         CK(hipDeviceSynchronize());
         unsigned long long sofar;
         CK(hipMemcpy(&sofar, bad, sizeof sofar, hipMemcpyDeviceToHost));
@@ -196,6 +217,14 @@ int main(int argc, char** argv) {
     snprintf(what, sizeof what, "div_by_recip, significand pairs (%d of 128 launches)", launches);
     if (report(what, bad, first, &total)) return 2;
 
+    // 4b. b negated: 16 launches spread over the significands of b
+    const int neg_launches = launches < 16 ? launches : 16;
+    for (int L = 0; L < neg_launches; ++L)
+        check_div_all<true><<<(1u << 22) / 256, 256>>>((uint32_t)(L * 8) << 16, bad, first);
+    CK(hipDeviceSynchronize());
+    snprintf(what, sizeof what, "div_by_neg_recip, significand pairs (%d launches)", neg_launches);
+    if (report(what, bad, first, &total)) return 2;
+
     CK(hipFree(bad));
     CK(hipFree(first));
     CK(hipFree(ds));
@@ -203,6 +232,7 @@ int main(int argc, char** argv) {
     CK(hipFree(dq));
     CK(hipFree(dss));
     CK(hipFree(dbb));
+    CK(hipFree(dbn));
     if (total) {
         printf("fp32_math_check: FAILED (%llu differ)\n", total);
         return 1;
