@@ -370,6 +370,23 @@ int mi_adamw_step_flat_fused_chain(const mi_adamw_tensor *t, const mi_adamw_fuse
                                    int64_t chunk_elems, int32_t state_dtype, int32_t flags,
                                    int32_t max_blocks, void *stream);
 
+/* mi_adamw_step_fused_chain with device step counts (d_steps, d_step_index required),
+ * the per-step values formed once per table row instead of in every workgroup, as
+ * mi_adamw_step_capturable_rows does for the capturable chain: a first launch forms each
+ * row's values (two float64 pow and the divisions, by the code the update would run) into
+ * d_row_scalars (n_rows * MI_ADAMW_ROW_SCALAR_BYTES bytes, 16-byte aligned, overwritten by
+ * every call), and the update reads them there.  Same results bit for bit.  Replaces, as
+ * mi_adamw_step_fused_chain does, torch._fused_adamw_ (adam.py:878-895) for
+ * torch.optim.AdamW(fused=True, capturable=True). */
+int mi_adamw_step_fused_chain_rows(const mi_adamw_tensor *d_tensors, int32_t n_rows,
+                                   const mi_adamw_chunk *d_chunks, int64_t n_chunks,
+                                   int64_t chunk_elems, const mi_adamw_fused_hyper *hypers,
+                                   int32_t n_hyper, const float *d_steps,
+                                   const int32_t *d_step_index, void *d_row_scalars,
+                                   const float *d_grad_scale, float grad_prescale,
+                                   int32_t state_dtype, int32_t flags, int32_t max_blocks,
+                                   void *stream);
+
 /* Measurement helper with no counterpart in the reference, for benchmarks that want
  * the memory ceiling of the update on the tensors it actually runs on: the same
  * launch as mi_adamw_step / mi_adamw_step_flat (tables or one flat range, launch

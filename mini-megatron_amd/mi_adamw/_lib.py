@@ -71,6 +71,7 @@ EXPORTS = (
     "mi_adamw_step_capturable",
     "mi_adamw_step_capturable_rows",
     "mi_adamw_step_fused_chain",
+    "mi_adamw_step_fused_chain_rows",
     "mi_adamw_step_flat_fused_chain",
     "mi_adamw_widen_bf16",
     "mi_adamw_probe",
@@ -185,6 +186,8 @@ _SIGNATURES = {
                                    _i32, _i32, _vp], ctypes.c_int),
     "mi_adamw_step_flat_fused_chain": ([_vp, _vp, _vp, _f32, _i64, _i32, _i32, _i32, _vp],
                                        ctypes.c_int),
+    "mi_adamw_step_fused_chain_rows": ([_vp, _i32, _vp, _i64, _i64, _vp, _i32, _vp, _vp, _vp,
+                                        _vp, _f32, _i32, _i32, _i32, _vp], ctypes.c_int),
     "mi_adamw_widen_bf16": ([_vp, _vp, _i64, _i64, _vp], ctypes.c_int),
     "mi_adamw_probe": ([_vp, _vp, _i64, _i64, _i32, _i32, _i32, _vp], ctypes.c_int),
     "mi_adamw_probe_flat": ([_vp, _i64, _i32, _i32, _i32, _vp], ctypes.c_int),

@@ -525,6 +525,71 @@ struct FusedHyper {
     }
 };
 
+// The fused=True chain's per-step values with device step counts formed once per table
+// row (mi_adamw_step_fused_chain_rows): a first launch runs FusedHyper<true>::get for
+// every row, one thread per row (two float64 pow, divisions), and keeps what depends on
+// the step in the row's slot; the update reads it with scalar loads and takes the rest
+// from the group's set, as with host step counts, and forms the quotient by bc2_sqrt from
+// the reciprocal formed here (div_by_recip).
+struct FusedRow {
+    double lr_wd;              // lr * weight_decay
+    float step_size;           // f32(lr / (double)bc1)
+    float bc2_sqrt;            // f32(sqrt(1 - pow(beta2, step)))
+    float inv_bc2_sqrt;        // 1.0f / bc2_sqrt
+    float unused;
+};
+static_assert(sizeof(FusedRow) <= MI_ADAMW_ROW_SCALAR_BYTES, "one row's values per slot");
+
+__global__ __launch_bounds__(256) void mi_adamw_fused_rows_kernel(
+    const mi_adamw_tensor* __restrict__ rows, int32_t n_rows, FusedHyper<true> hs,
+    RowScalars* __restrict__ out) {
+    const int32_t r = blockIdx.x * 256 + threadIdx.x;
+    if (r >= n_rows) return;
+    const FusedScalarsT<false> s = hs.get(rows[r], r);
+    FusedRow f;
+    f.lr_wd = s.lr_wd;
+    f.step_size = s.step_size;
+    f.bc2_sqrt = s.bc2_sqrt;
+    f.inv_bc2_sqrt = 1.0f / s.bc2_sqrt;
+    f.unused = 0.0f;
+    memcpy(&out[r], &f, sizeof(f));
+}
+
+struct FusedRowsHyper {
+    using Scalars = FusedScalarsT<true>;
+    static constexpr bool kCapt = false;
+    static constexpr bool kLate = true;
+    static constexpr bool kProbe = false;
+    static constexpr bool kShare = false;
+    FusedPack fp;
+    const RowScalars* rows;
+    __device__ __forceinline__ Scalars get(const mi_adamw_tensor& t, int32_t row) const {
+        const FusedSet& c = fp.h[t.hyper];
+        // written by the launch before this one on the stream: read word by word through
+        // the constant address space, so the loads are scalar
+        static_assert(sizeof(FusedRow) % 4 == 0, "read as 32-bit words");
+        const CONSTANT uint32_t* w = (const CONSTANT uint32_t*)(rows + row);
+        uint32_t v[sizeof(FusedRow) / 4];
+#pragma unroll
+        for (unsigned k = 0; k < sizeof(FusedRow) / 4; ++k) v[k] = w[k];
+        FusedRow f;
+        memcpy(&f, v, sizeof(f));
+        Scalars s;
+        s.beta1 = c.beta1;
+        s.one_minus_beta1 = c.one_minus_beta1;
+        s.beta2 = c.beta2;
+        s.one_minus_beta2 = c.one_minus_beta2;
+        s.eps = c.eps;
+        s.grad_sign = c.grad_sign;
+        s.decay = c.decay != 0;
+        s.lr_wd = f.lr_wd;
+        s.step_size = f.step_size;
+        s.bc2_sqrt = f.bc2_sqrt;
+        s.inv_bc2_sqrt = f.inv_bc2_sqrt;
+        return s;
+    }
+};
+
 // Memory-only twin of the update, for measurement (mi_adamw_probe): the same
 // loads and stores, launch shape and cache hints, with the arithmetic left out.
 // Every value is stored back as it was read (the bf16 copy as the bf16 of the
@@ -1509,6 +1574,38 @@ int mi_adamw_step_fused_chain(const mi_adamw_tensor* d_tensors, const mi_adamw_c
     memset(&hs, 0, sizeof(hs));
     for (int32_t i = 0; i < n_hyper; ++i) hs.fp.h[i] = fused_set_from(hypers[i], true);
     return launch_update(src, n_chunks, chunk_elems, hs, d_grad_scale, state_dtype, flags,
+                         max_blocks, s, grad_prescale);
+}
+
+int mi_adamw_step_fused_chain_rows(const mi_adamw_tensor* d_tensors, int32_t n_rows,
+                                   const mi_adamw_chunk* d_chunks, int64_t n_chunks,
+                                   int64_t chunk_elems, const mi_adamw_fused_hyper* hypers,
+                                   int32_t n_hyper, const float* d_steps,
+                                   const int32_t* d_step_index, void* d_row_scalars,
+                                   const float* d_grad_scale, float grad_prescale,
+                                   int32_t state_dtype, int32_t flags, int32_t max_blocks,
+                                   void* stream) {
+    if (!d_tensors || n_rows <= 0 || !d_chunks || !hypers || n_hyper <= 0 ||
+        n_hyper > MI_ADAMW_MAX_HYPER || !finite(grad_prescale) || !d_steps || !d_step_index ||
+        !d_row_scalars || !aligned(d_row_scalars, 16))
+        return MI_ADAMW_E_INVALID;
+    FusedHyper<true> hs;
+    memset(&hs, 0, sizeof(hs));
+    for (int32_t i = 0; i < n_hyper; ++i) hs.fp.h[i] = fused_set_from(hypers[i], false);
+    hs.steps = d_steps;
+    hs.step_index = d_step_index;
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    RowScalars* rows = static_cast<RowScalars*>(d_row_scalars);
+    hipLaunchKernelGGL(mi_adamw_fused_rows_kernel, dim3((n_rows + 255) / 256), dim3(256), 0, s,
+                       d_tensors, n_rows, hs, rows);
+    const int rc = launch_status();
+    if (rc) return rc;
+    FusedRowsHyper rh;
+    memset(&rh, 0, sizeof(rh));
+    rh.fp = hs.fp;
+    rh.rows = rows;
+    TableSource src{d_tensors, d_chunks};
+    return launch_update(src, n_chunks, chunk_elems, rh, d_grad_scale, state_dtype, flags,
                          max_blocks, s, grad_prescale);
 }
 

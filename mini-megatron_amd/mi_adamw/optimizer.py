@@ -1390,9 +1390,16 @@ class FusedAdamW(Optimizer):
                 state_code, flags, self.max_blocks, stream), "mi_adamw_step_flat_fused_chain")
             return
         farr = (_lib.FusedHyper * len(hs))(*hs)
-        steps = idx = None
         if self.capturable:
-            steps, idx = self._steps.data_ptr(), launch.step_index.data_ptr()
+            # device step counts: the per-step values formed once per row before the update
+            _lib.check(lib.mi_adamw_step_fused_chain_rows(
+                launch.rows.data_ptr(), launch.n_rows, launch.chunks.data_ptr(), launch.n_chunks,
+                self.chunk_elems, farr, len(hs), self._steps.data_ptr(),
+                launch.step_index.data_ptr(), launch.row_scalars.data_ptr(), coef.data_ptr(),
+                pre, state_code, flags, self.max_blocks, stream),
+                "mi_adamw_step_fused_chain_rows")
+            return
+        steps = idx = None
         _lib.check(lib.mi_adamw_step_fused_chain(
             launch.rows.data_ptr(), launch.chunks.data_ptr(), launch.n_chunks, self.chunk_elems,
             farr, len(hs), steps, idx, coef.data_ptr(), pre, state_code, flags, self.max_blocks,

@@ -255,6 +255,12 @@ static int cpu_checks(void)
     CHECK(mi_adamw_step_fused_chain(fake, fake, 1, 4096, fh, 1, NULL, NULL, NULL, 1.0f, 0,
                                     MI_ADAMW_F_CLIP, 0, NULL) == MI_ADAMW_E_INVALID,
           "fused chain clip without a scale");
+    CHECK(mi_adamw_step_fused_chain_rows(fake, 1, fake, 1, 4096, fh, 1, NULL, NULL,
+                                         (void *)(uintptr_t)4096, NULL, 1.0f, 0, 0, 0, NULL) ==
+              MI_ADAMW_E_INVALID, "fused chain rows without device steps");
+    CHECK(mi_adamw_step_fused_chain_rows(fake, 1, fake, 1, 4096, fh, 1, fake_f, fake, NULL, NULL,
+                                         1.0f, 0, 0, 0, NULL) == MI_ADAMW_E_INVALID,
+          "fused chain rows without row scalars");
     t.grad = (float *)(uintptr_t)(8192 + 4);
     CHECK(mi_adamw_step_flat_fused_chain(&t, fh, NULL, 1.0f, 4096, MI_ADAMW_STATE_F32, 0, 0,
                                          NULL) == MI_ADAMW_E_ALIGN, "misaligned fused flat range");
@@ -806,7 +812,11 @@ static void fused_case(void)
     int32_t *d_index = dev_copy(step_index, sizeof step_index);
     const float lr_dev = 2e-3f;
     float *d_lr = dev_copy(&lr_dev, sizeof lr_dev);
-    for (int pass = 0; pass < 2; ++pass) {
+    void *d_row_scalars = NULL;
+    HIP(hipMalloc(&d_row_scalars, NT * MI_ADAMW_ROW_SCALAR_BYTES));
+    /* pass 0: host steps; 1: device steps and lr, mi_adamw_step_fused_chain; 2: the same
+     * through mi_adamw_step_fused_chain_rows; the state carries over */
+    for (int pass = 0; pass < 3; ++pass) {
         mi_adamw_fused_hyper h[NT];
         oracle_fused o[NT];
         int rc;
@@ -823,8 +833,13 @@ static void fused_case(void)
                 h[k].lr_ptr = d_lr;
                 h[k].step = 0.0f;        /* and the device step counts */
             }
-            rc = mi_adamw_step_fused_chain(d_rows, d_chunks, n_chunks, 4096, h, NT, d_steps,
-                                           d_index, NULL, 1.0f, MI_ADAMW_STATE_F32, 0, 0, NULL);
+            rc = pass == 1
+                     ? mi_adamw_step_fused_chain(d_rows, d_chunks, n_chunks, 4096, h, NT,
+                                                 d_steps, d_index, NULL, 1.0f,
+                                                 MI_ADAMW_STATE_F32, 0, 0, NULL)
+                     : mi_adamw_step_fused_chain_rows(d_rows, NT, d_chunks, n_chunks, 4096, h,
+                                                      NT, d_steps, d_index, d_row_scalars, NULL,
+                                                      1.0f, MI_ADAMW_STATE_F32, 0, 0, NULL);
         }
         CHECK(rc == 0, "mi_adamw_step_fused_chain (pass %d): %s", pass, mi_adamw_strerror(rc));
         HIP(hipDeviceSynchronize());
@@ -847,9 +862,10 @@ static void fused_case(void)
     }
     HIP(hipFree(d_rows)); HIP(hipFree(d_chunks)); HIP(hipFree(d_steps)); HIP(hipFree(d_index));
     HIP(hipFree(d_lr));
+    HIP(hipFree(d_row_scalars));
     free(chunks);
     printf("abi_check gpu: fused=True chain, flat with clip, tables with two sets, device steps "
-           "and lr: bit-exact\n");
+           "and lr (both entry points): bit-exact\n");
 }
 
 static int gpu_checks(void)
