@@ -334,8 +334,9 @@ int mi_adamw_step_capturable(const mi_adamw_tensor *d_tensors, const mi_adamw_ch
  * longer waits on that prologue, which bounds mi_adamw_step_capturable's update when the
  * moments are bf16.  d_row_scalars: device memory of n_rows * MI_ADAMW_ROW_SCALAR_BYTES
  * bytes, 16-byte aligned, provided by the caller and overwritten by every call (calls
- * that overlap on one buffer race); n_rows: the rows of d_tensors.  The other arguments
- * are those of mi_adamw_step_capturable. */
+ * that overlap on one buffer race); n_rows: the rows of d_tensors, above every chunk's
+ * `tensor` (the update reads the slot of that row).  The other arguments are those of
+ * mi_adamw_step_capturable. */
 #define MI_ADAMW_ROW_SCALAR_BYTES 64
 int mi_adamw_step_capturable_rows(const mi_adamw_tensor *d_tensors, int32_t n_rows,
                                   const mi_adamw_chunk *d_chunks, int64_t n_chunks,

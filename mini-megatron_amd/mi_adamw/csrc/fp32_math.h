@@ -1,8 +1,8 @@
 // fp32 helpers of the update kernels whose results must equal another, slower form bit
 // for bit: the bf16 conversion of the stored moments and copies, and the quotient by a
 // per-step constant in the fused=True chain (positive divisor) and in the capturable chain
-// (negative divisor).  Kept in a header so that the check
-// program tests/c/div_check.hip runs this very code against the reference forms.
+// (negative divisor).  Kept in a header so that the check program
+// tests/c/fp32_math_check.hip runs this very code against the forms it replaces.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -25,13 +25,14 @@ __device__ __forceinline__ uint32_t bf16x2_bits(float a, float b) {
 __device__ __forceinline__ uint32_t bf16_bits(float x) { return bf16x2_bits(x, 0.0f) & 0xffffu; }
 
 // s / b, correctly rounded, given r = 1.0f / b (correctly rounded), for the quotients of
-// the fused=True chain with host step counts: s = sqrtf(v) (+-0, inf, NaN, or in [2^-74.5, 2^64]) and b = bc2_sqrt
-// (in [2^-26.5, 1]).  q0 = s * r is within one ulp of s / b, so e = s - q0 * b is exactly
+// the fused=True chain when bc2_sqrt comes from the host or from the per-row launch:
+// s = sqrtf(v) (+-0, inf, NaN, or in [2^-74.5, 2^64]) and b = bc2_sqrt (in [2^-26.5, 1]
+// for every step count >= 1 and float64 beta2 in [0, 1)).  q0 = s * r is within one ulp of s / b, so e = s - q0 * b is exactly
 // representable (a multiple of 2^(i-47) below 2^(i-23), i the exponent of s, normal or
 // subnormal alike at these ranges) and one fma gives it; q0 + e * r, rounded once, is the
 // correctly rounded quotient (Markstein's correction).  The rounding of that last fma is
 // scale-invariant at these ranges, so the check of every pair of significands in [1, 2)
-// (tests/c/div_check.hip) covers every s and b above.
+// (tests/c/fp32_math_check.hip) covers every s and b above.
 // e is formed as -(q0 * b - s) so that s = -0 gives e = -0 and the quotient -0.  e is NaN
 // only when q0 is +-inf or NaN; fmaxf then gives -FLT_MAX, a finite correction that the
 // exact fma adds to an infinite or NaN q0 without changing it.  Four instructions (the

@@ -152,9 +152,10 @@ __device__ __forceinline__ void adamw_elem(float& p, float g, float& m, float& v
 // hyperparameters as _fused_adamw_ receives them, and the per-step values it forms.
 // kRecip: the quotient by bc2_sqrt is formed from its reciprocal (div_by_recip), which
 // gives the division's bits; without it, by the division itself.  The host-step chain
-// takes kRecip (its per-step values are kernel arguments, so the reciprocal costs no
-// vector register); the device-step chain forms them after two out-of-line pow calls
-// with the first tile's loads in flight, where one more value spills, so it divides.
+// and the per-row chain (FusedRowsHyper) take kRecip: their per-step values are kernel
+// arguments or scalar loads, so the reciprocal costs no vector register.  The device-step
+// chain that forms them in every workgroup does so after two out-of-line pow calls with
+// the first tile's loads in flight, where one more value spills, so it divides.
 template <bool kRecip>
 struct FusedScalarsT {
     double beta1, one_minus_beta1;
@@ -445,8 +446,9 @@ struct CaptRowsHyper {
 };
 
 // One set of the fused=True chain as the kernel takes it: the float64 hyperparameters
-// and, with host step counts, the two per-step values the library formed on the host
-// from them (fused_set_from).
+// and, with host step counts, the per-step values the library formed on the host from
+// them (fused_set_from): both bias corrections, and with a host lr also lr_wd,
+// step_size and inv_bc2_sqrt.
 struct FusedSet {
     double beta1, one_minus_beta1;
     double beta2, one_minus_beta2;

@@ -1399,8 +1399,8 @@ class FusedAdamW(Optimizer):
                 pre, state_code, flags, self.max_blocks, stream),
                 "mi_adamw_step_fused_chain_rows")
             return
-        steps = idx = None
+        # host step counts (hs[i].step): no step buffer
         _lib.check(lib.mi_adamw_step_fused_chain(
             launch.rows.data_ptr(), launch.chunks.data_ptr(), launch.n_chunks, self.chunk_elems,
-            farr, len(hs), steps, idx, coef.data_ptr(), pre, state_code, flags, self.max_blocks,
+            farr, len(hs), None, None, coef.data_ptr(), pre, state_code, flags, self.max_blocks,
             stream), "mi_adamw_step_fused_chain")
