@@ -5,9 +5,9 @@ torch's capturable chain keeps the step counts on the device and forms the
 per-step values there in fp32 (adam.py:480-527): ``beta ** step`` by the device
 pow, ``lr / bc1`` (a float lr as ``bc1.reciprocal() * lr``), ``sqrt(bc2) *
 -step_size`` and ``eps / -step_size``, then ``p += m / (sqrt(v) / (sqrt(bc2) *
--step_size) + eps / -step_size)``.  The kernel forms the same values in every
-workgroup from the tensor's device step count, so parameters, moments and step
-counts must be bit-identical step after step, eager or replayed from a graph.
+-step_size) + eps / -step_size)``.  A launch before the update forms the same values
+once per tensor from its device step count, so parameters, moments and step counts
+must be bit-identical step after step, eager or replayed from a graph.
 """
 from __future__ import annotations
 
@@ -350,6 +350,48 @@ def test_capturable_params_without_grads_and_many_groups(dev):
                 assert max_ulp(topt.state[p]["exp_avg_sq"], oopt.state[q]["exp_avg_sq"]) == 0
     steps = {float(oopt.state[q]["step"]) for q in ours}
     assert len(steps) > 1
+
+
+@pytest.mark.parametrize("fused", [False, True])
+def test_capturable_more_rows_than_one_prep_workgroup(dev, fused):
+    """300 tensors in one launch: the launch that forms each table row's per-step values
+    runs 256 rows per workgroup, so rows 256-299 come from its second workgroup.  Row i
+    and row i - 256 differ in shape, group (lr) and device step count (steps 2-7 each skip
+    the tensors with i mod 7 == step - 1), so a row reading another row's slot changes
+    bits; the last step skips none, so its launch has all 300 rows.
+    Both capturable chains: torch's capturable AdamW (foreach=False) and fused=True."""
+    import mi_adamw
+    cycle = [(37,), (4099,), (64, 48), (5,), (129,)]
+    shapes = [cycle[i % len(cycle)] for i in range(300)]
+    ref = make_params(shapes, dev)
+    ours = clone_params(ref)
+
+    def groups(ps):
+        return [dict(params=ps[75 * k:75 * (k + 1)], lr=1e-4 * (k + 1),
+                     weight_decay=0.05 * k) for k in range(4)]
+
+    kw = dict(fused=True) if fused else dict(foreach=False)
+    topt = torch.optim.AdamW(groups(ref), capturable=True, **kw)
+    oopt = mi_adamw.FusedAdamW(groups(ours), capturable=True, **kw)
+    for step in range(1, 9):
+        set_grads(ref, step, 1e-3)
+        for i, (p, q) in enumerate(zip(ref, ours)):
+            if 1 < step < 8 and i % 7 == step - 1:
+                p.grad = None
+                q.grad = None
+            else:
+                q.grad = p.grad.clone()
+        topt.step()
+        oopt.step()
+        torch.cuda.synchronize()
+        assert max_ulp_all(ref, ours) == 0
+        for p, q in zip(ref, ours):
+            ts, os_ = topt.state[p], oopt.state[q]
+            assert torch.equal(ts["step"], os_["step"])
+            assert max_ulp(ts["exp_avg"], os_["exp_avg"]) == 0
+            assert max_ulp(ts["exp_avg_sq"], os_["exp_avg_sq"]) == 0
+    assert max(l.n_rows for l in oopt._launch_cache.launches) > 256
+    assert float(oopt.state[ours[0]]["step"]) != float(oopt.state[ours[256]]["step"])
 
 
 def test_capturable_deepcopy_mid_training(dev):
