@@ -6,10 +6,33 @@ seeded with base + i (params 1000, exp_avg 2000, exp_avg_sq 3000, grads
 """
 from __future__ import annotations
 
+import os
+
 import numpy as np
 import torch
 
 from mi_adamw.workloads import GPTShape, init_kind
+
+
+def seeds(default: int) -> range:
+    """The seeds of a seeded random test: range(default), or, for a wider sweep, the range
+    that the environment variable MI_ADAMW_SEEDS names as "lo:hi" (hi excluded)."""
+    spec = os.environ.get("MI_ADAMW_SEEDS")
+    if not spec:
+        return range(default)
+    lo, hi = (int(x) for x in spec.split(":"))
+    if not 0 <= lo < hi:
+        raise ValueError(f"MI_ADAMW_SEEDS={spec!r}: expected lo:hi with 0 <= lo < hi")
+    return range(lo, hi)
+
+
+def same_bits(a: torch.Tensor, b: torch.Tensor) -> bool:
+    """Whether two tensors of one 16-bit dtype (a bf16 copy and the bf16 of its master)
+    hold the same bits.  Unlike torch.equal, a NaN equals a NaN of the same bits: torch's
+    capturable chain with lr = 0 forms NaN where a second moment is 0, and so do the
+    kernels, so the copy holds the bf16 NaN of that master."""
+    return a.shape == b.shape and torch.equal(a.contiguous().view(torch.int16),
+                                              b.contiguous().view(torch.int16))
 
 
 def gen(device, seed: int) -> torch.Generator:

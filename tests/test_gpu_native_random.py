@@ -18,7 +18,7 @@ import random
 import pytest
 import torch
 
-from _helpers import clone_params, gen, make_params, max_ulp_all
+from _helpers import clone_params, gen, make_params, max_ulp_all, seeds
 
 pytestmark = pytest.mark.gpu
 
@@ -51,7 +51,7 @@ def _state_diff(ref, ours, topt, oopt):
 
 @pytest.mark.parametrize("chain", ["default", "fused"])
 @pytest.mark.parametrize("layout", ["tables", "flat"])
-@pytest.mark.parametrize("seed", range(6))
+@pytest.mark.parametrize("seed", seeds(6))
 def test_random_step_sequences(dev, seed, layout, chain):
     """In the flat layout the parameters, gradients and moments are views of its buffers:
     a replaced p.data, gradient or state tensor is copied into its slice at the next step,
